@@ -1,0 +1,139 @@
+/*
+ * sk_attn.h -- C ABI of libsk_attn.so, the gfx950 (MI355X) attention kernels.
+ *
+ * Plain C: pointers, sizes and ints only.  No allocation happens inside the
+ * library: every output, the backward scratch and the decode split buffer
+ * are device memory that the caller owns and passes in.  All launches go on
+ * the HIP stream the caller passes (NULL = the null stream); no call
+ * synchronises the host.  Calls are re-entrant and thread-safe.
+ *
+ * Tensor layout is (B, H, S, D) with D contiguous ("BHSD").  Where a call
+ * takes strides they are ELEMENT strides, given as int64_t[3] = {b, h, s};
+ * the D stride is always 1.  Device pointers to bf16/fp16/fp32 data must be
+ * 16-byte aligned and every stride a multiple of 8 elements (16 bytes) for
+ * bf16/fp16, 4 elements for fp32.
+ *
+ * Return value: SK_OK (0) on success; a negative SK_E* code for a rejected
+ * argument (nothing launched); a positive hipError_t for a HIP launch
+ * failure.  sk_last_error() gives the message of the last failure on the
+ * calling thread.
+ */
+#ifndef SK_ATTN_H_
+#define SK_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define SK_API __attribute__((visibility("default")))
+#else
+#define SK_API
+#endif
+
+#define SK_ABI_VERSION 1
+
+/* Element type codes. */
+#define SK_F32 0
+#define SK_F16 1
+#define SK_BF16 2
+
+/* Error codes (negative: argument rejected before any launch). */
+#define SK_OK 0
+#define SK_EINVAL (-1)      /* bad shape, stride, alignment or pointer   */
+#define SK_EUNSUPPORTED (-2) /* dtype / head dim this library has no kernel for */
+#define SK_EWORKSPACE (-3)  /* workspace pointer NULL or smaller than required */
+
+/* Version of this ABI; equals SK_ABI_VERSION of the header it was built with. */
+SK_API int sk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+SK_API const char* sk_last_error(void);
+
+/*
+ * Forward attention.  Replaces the launcher flash_attn_fwd
+ * (reference: src/stackkernels/_core/attention/flash_fwd.py:182-264) and its
+ * kernel _flash_fwd_kernel (:15-179).
+ *
+ *   q (B,Hq,Sq,D)  k, v (B,Hkv,Sk,D)  ->  o (B,Hq,Sq,D) in the input dtype,
+ *   lse (B,Hq,Sq) fp32, contiguous.
+ *
+ * Hq % Hkv == 0; query head h reads KV head h / (Hq/Hkv).  With is_causal the
+ * mask is bottom-right aligned: key j is visible to query i iff
+ * j <= i + (Sk - Sq).  A row with no visible key gets o = 0, lse = -inf.
+ * sm_scale multiplies q.k before the softmax.  D: any multiple of 8 up to 256.
+ */
+SK_API int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                const int64_t* q_strides, const int64_t* k_strides,
+                const int64_t* v_strides, const int64_t* o_strides,
+                int is_causal, float sm_scale, void* stream);
+
+/*
+ * Bytes of scratch sk_attn_bwd needs for these dims (row statistics and the
+ * fp32 dQ accumulator).  Replaces allocate_delta_buffer
+ * (reference: src/stackkernels/_opt/memory/workspace.py:16-23).
+ */
+SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                          int is_causal, size_t* bytes);
+
+/*
+ * Backward attention.  Replaces flash_attn_bwd
+ * (reference: src/stackkernels/_core/attention/flash_bwd.py:362-528) with its
+ * three kernels _bwd_preprocess_kernel (:15-55), _flash_bwd_dq_kernel
+ * (:58-198) and _flash_bwd_dkv_kernel (:201-359).
+ *
+ * All tensors contiguous BHSD: dout, q, o, dq (B,Hq,Sq,D); k, v, dk, dv
+ * (B,Hkv,Sk,D); lse (B,Hq,Sq) fp32 as written by sk_attn_fwd.  dk and dv are
+ * summed over the query heads that share a KV head.  Rows with lse = -inf
+ * contribute nothing.  workspace: >= sk_attn_bwd_workspace() bytes, any
+ * contents (the call initialises what it uses).
+ */
+SK_API int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
+                const void* o, const float* lse, void* dq, void* dk, void* dv,
+                void* workspace, size_t workspace_bytes,
+                int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                int is_causal, float sm_scale, void* stream);
+
+/*
+ * Split-KV plan for single-token decode: the number of key splits the gfx950
+ * table picks and the scratch bytes sk_decode then needs.  Replaces the split
+ * heuristic chain decode_heuristic -> seed_configs
+ * (reference: src/stackkernels/_opt/heuristics/flash_decode.py:9-12,
+ * src/stackkernels/_opt/classes/decode.py:9-63) as used at
+ * src/stackkernels/_core/attention/decode.py:220-226.
+ */
+SK_API int sk_decode_plan(int dtype, int B, int Hq, int Hkv, int Sk, int D,
+                   int* num_splits, size_t* workspace_bytes);
+
+/*
+ * Single-token decode (Sq == 1), non-causal over all Sk keys.  Replaces the
+ * launcher flash_decode (reference: src/stackkernels/_core/attention/decode.py:192-312)
+ * and its kernels _flash_decode_split_kernel (:15-121) and
+ * _flash_decode_reduce_kernel (:124-189).
+ *
+ *   q (B,Hq,1,D), k/v (B,Hkv,Sk,D) with any b/h/s strides  ->  o (B,Hq,1,D).
+ *
+ * num_splits: as returned by sk_decode_plan, or any value in [1, Sk] (0 lets
+ * the library plan).  workspace: >= the plan's bytes for that split count
+ * (sk_decode_workspace), any contents.
+ */
+SK_API int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o,
+              void* workspace, size_t workspace_bytes, int num_splits,
+              int B, int Hq, int Hkv, int Sk, int D,
+              const int64_t* q_strides, const int64_t* k_strides,
+              const int64_t* v_strides, const int64_t* o_strides,
+              float sm_scale, void* stream);
+
+/* Scratch bytes sk_decode needs for an explicit split count. */
+SK_API int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,
+                        size_t* workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SK_ATTN_H_ */

@@ -1,0 +1,256 @@
+"""CPU oracle for the StackKernels attention path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import this module, and only as the checker.  The product path never
+calls it: device tensors run the HIP library, and the library fails loudly
+when it is missing.
+
+What it restates (all arithmetic in float64 unless a caller asks otherwise):
+
+* ``repeat_kv``            -- ``src/stackkernels/_reference/torch/attention.py:10-14``
+* ``allowed_mask``         -- bottom-right causal rule, ``_core/attention/_masks.py:22-35``
+                              and ``_reference/torch/attention.py:63-68``
+* ``attention_forward``    -- ``_reference/torch/attention.py:17-76`` (scores, mask,
+                              logsumexp, softmax, NaN->0 for fully masked rows, P.V)
+* ``attention_backward``   -- the gradient of ``attention_forward``; the reference
+                              obtains it by autograd through the same function
+                              (``src/stackkernels/torch/attention.py:82-102``).  Written
+                              here in closed form: dV = P^T dO, dP = dO V^T,
+                              dS = P * (dP - rowsum(dO * O)), dQ = s dS K, dK = s dS^T Q,
+                              with dK/dV summed over each KV head's query group.
+* ``decode``               -- ``src/stackkernels/torch/attention.py:134-155`` (CPU branch
+                              ``:154`` calls the non-causal reference with S_q = 1).
+* ``split_partials`` / ``combine_partials`` -- the split-KV decomposition and the
+                              LSE-weighted merge of ``_core/attention/decode.py:81-121,166-186``.
+
+How each function is pinned (see ``tests/test_oracle.py``):
+
+* against the committed golden vectors in ``tests/golden/`` (written by
+  ``tests/golden/make_golden.py`` from torch's own
+  ``scaled_dot_product_attention`` in float64 -- an independent library
+  routine, with its autograd for the gradients);
+* against a brute-force per-element loop on tiny shapes;
+* against central finite differences of ``attention_forward`` (backward);
+* through invariants a plausible slip would break: rows of P sum to one,
+  GQA equals MHA on repeated K/V with grads summed per group, a causal row
+  does not depend on keys it may not see, ``S_k = 1`` gives ``O = V`` and
+  ``LSE = score``, ``q = 0`` gives the mean of the visible V rows and
+  ``LSE = log(#visible)``, fully masked rows give ``O = 0`` and
+  ``LSE = -inf`` and zero gradients, and the split-KV merge is invariant to
+  the number of splits.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+NEG_INF = float("-inf")
+
+
+def repeat_kv(x: np.ndarray, n_rep: int) -> np.ndarray:
+    """(B, H_kv, S, D) -> (B, H_kv * n_rep, S, D), each KV head repeated in place.
+
+    Follows ``_reference/torch/attention.py:10-14`` (``repeat_interleave`` on dim 1):
+    query head ``h`` reads KV head ``h // n_rep``.
+    """
+    if n_rep == 1:
+        return x
+    return np.repeat(x, n_rep, axis=1)
+
+
+def allowed_mask(s_q: int, s_k: int) -> np.ndarray:
+    """Boolean (S_q, S_k): True where query i may attend key j, i.e. j <= i + (S_k - S_q).
+
+    Bottom-right alignment, ``_core/attention/_masks.py:22-35``.
+    """
+    i = np.arange(s_q)[:, None]
+    j = np.arange(s_k)[None, :]
+    return j <= i + (s_k - s_q)
+
+
+def _default_scale(d: int, sm_scale: float | None) -> float:
+    # src/stackkernels/torch/attention.py:33-36
+    return 1.0 / math.sqrt(d) if sm_scale is None else float(sm_scale)
+
+
+def attention_forward(q, k, v, is_causal=False, sm_scale=None, dtype=np.float64):
+    """Return (O, LSE) for BHSD inputs, following ``_reference/torch/attention.py:17-76``.
+
+    O has shape (B, H_q, S_q, D), LSE (B, H_q, S_q).  Fully masked rows give
+    O = 0 and LSE = -inf.  Inputs are upcast to ``dtype`` first, as the
+    reference upcasts to float32 (``:56-59``); the default float64 is the
+    checker's precision.
+    """
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    b, hq, sq, d = q.shape
+    hkv, sk = k.shape[1], k.shape[2]
+    assert hq % hkv == 0
+    scale = _default_scale(d, sm_scale)
+    kk = repeat_kv(k, hq // hkv)
+    vv = repeat_kv(v, hq // hkv)
+    scores = np.matmul(q, np.swapaxes(kk, -1, -2)) * scale
+    if is_causal:
+        scores = np.where(allowed_mask(sq, sk)[None, None], scores, NEG_INF)
+    if sk == 0:
+        lse = np.full((b, hq, sq), NEG_INF, dtype=dtype)
+        return np.zeros((b, hq, sq, d), dtype=dtype), lse
+    m = scores.max(axis=-1, keepdims=True)
+    finite = np.isfinite(m)
+    m_safe = np.where(finite, m, 0.0)
+    e = np.exp(scores - m_safe)
+    l = e.sum(axis=-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        lse = np.where(finite, m_safe + np.log(l), NEG_INF)[..., 0]
+        p = np.where(finite, e / l, 0.0)
+    out = np.matmul(p, vv)
+    return out.astype(dtype), lse.astype(dtype)
+
+
+def softmax_probs(q, k, is_causal=False, sm_scale=None):
+    """P = softmax(scale Q K^T + mask) with fully masked rows set to 0, float64."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    hq, hkv = q.shape[1], k.shape[1]
+    sq, sk, d = q.shape[2], k.shape[2], q.shape[3]
+    scale = _default_scale(d, sm_scale)
+    s = np.matmul(q, np.swapaxes(repeat_kv(k, hq // hkv), -1, -2)) * scale
+    if is_causal:
+        s = np.where(allowed_mask(sq, sk)[None, None], s, NEG_INF)
+    m = s.max(axis=-1, keepdims=True) if sk else np.zeros(s.shape[:-1] + (1,))
+    m = np.where(np.isfinite(m), m, 0.0)
+    e = np.exp(s - m)
+    l = e.sum(axis=-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return np.where(l > 0, e / np.where(l > 0, l, 1.0), 0.0)
+
+
+def attention_backward(q, k, v, do, is_causal=False, sm_scale=None):
+    """Return (dQ, dK, dV) of ``sum(O * dO)`` w.r.t. q, k, v, float64.
+
+    This is the gradient the reference computes by autograd through its
+    reference forward (``src/stackkernels/torch/attention.py:82-102``).
+    dK/dV come back in the KV-head shape: the ``repeat_kv`` copies of a head
+    are summed over its query group.  Rows that see no key contribute zero.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    do = np.asarray(do, dtype=np.float64)
+    b, hq, sq, d = q.shape
+    hkv, sk = k.shape[1], k.shape[2]
+    g = hq // hkv
+    scale = _default_scale(d, sm_scale)
+    kk = repeat_kv(k, g)
+    vv = repeat_kv(v, g)
+    p = softmax_probs(q, k, is_causal, sm_scale)  # (B, Hq, Sq, Sk)
+    out = np.matmul(p, vv)
+    dvv = np.matmul(np.swapaxes(p, -1, -2), do)
+    dp = np.matmul(do, np.swapaxes(vv, -1, -2))
+    delta = (do * out).sum(axis=-1, keepdims=True)
+    ds = p * (dp - delta)
+    dq = np.matmul(ds, kk) * scale
+    dkk = np.matmul(np.swapaxes(ds, -1, -2), q) * scale
+    dk = dkk.reshape(b, hkv, g, sk, d).sum(axis=2)
+    dv = dvv.reshape(b, hkv, g, sk, d).sum(axis=2)
+    return dq, dk, dv
+
+
+def decode(q, k, v, sm_scale=None, dtype=np.float64):
+    """Single-token decode: O of ``attention_forward(q, k, v, is_causal=False)``.
+
+    ``src/stackkernels/torch/attention.py:134-155``; the reference asserts
+    ``S_q == 1`` (``_core/attention/decode.py:212``).
+    """
+    assert np.asarray(q).shape[2] == 1, "flash_decode requires q_len == 1"
+    out, _ = attention_forward(q, k, v, is_causal=False, sm_scale=sm_scale, dtype=dtype)
+    return out
+
+
+def split_partials(q, k, v, num_splits, sm_scale=None):
+    """Per-split normalised partial outputs and LSEs for S_q = 1 decode.
+
+    Split ``s`` covers keys ``[s*c, min((s+1)*c, S_k))`` with ``c = ceil(S_k / num_splits)``,
+    the chunking of ``_core/attention/decode.py:228-230``.  Returns
+    (O_s of shape (B, H_q, splits, D), LSE_s of shape (B, H_q, splits)); an
+    empty split has O_s = 0 and LSE_s = -inf.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    b, hq, _, d = q.shape
+    sk = k.shape[2]
+    chunk = -(-sk // num_splits) if sk else 0
+    outs = np.zeros((b, hq, num_splits, d))
+    lses = np.full((b, hq, num_splits), NEG_INF)
+    for s in range(num_splits):
+        lo, hi = s * chunk, min((s + 1) * chunk, sk)
+        if hi <= lo:
+            continue
+        o, l = attention_forward(q, k[:, :, lo:hi], v[:, :, lo:hi], False, sm_scale)
+        outs[:, :, s] = o[:, :, 0]
+        lses[:, :, s] = l[:, :, 0]
+    return outs, lses
+
+
+def combine_partials(outs, lses):
+    """LSE-weighted merge of split partials, ``_core/attention/decode.py:166-186``.
+
+    O = sum_s exp(LSE_s - M) O_s / sum_s exp(LSE_s - M), M = max_s LSE_s;
+    all splits empty gives O = 0.  Returns (O of shape (B, H_q, 1, D), LSE).
+    """
+    outs = np.asarray(outs, dtype=np.float64)
+    lses = np.asarray(lses, dtype=np.float64)
+    m = lses.max(axis=-1, keepdims=True)
+    finite = np.isfinite(m)
+    w = np.where(finite, np.exp(lses - np.where(finite, m, 0.0)), 0.0)
+    den = w.sum(axis=-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        o = np.where(den[..., None] > 0, (w[..., None] * outs).sum(axis=-2, keepdims=True)
+                     / np.where(den > 0, den, 1.0)[..., None], 0.0)
+        lse = np.where(finite, m + np.log(np.where(den > 0, den, 1.0)), NEG_INF)[..., 0]
+    return o, lse
+
+
+def attention_forward_loops(q, k, v, is_causal=False, sm_scale=None):
+    """Brute-force per-element restatement for tiny shapes (pins ``attention_forward``)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    b, hq, sq, d = q.shape
+    hkv, sk = k.shape[1], k.shape[2]
+    g = hq // hkv
+    scale = _default_scale(d, sm_scale)
+    out = np.zeros((b, hq, sq, d))
+    lse = np.full((b, hq, sq), NEG_INF)
+    for bi in range(b):
+        for h in range(hq):
+            kh = h // g
+            for i in range(sq):
+                keys = [j for j in range(sk) if not is_causal or j <= i + sk - sq]
+                if not keys:
+                    continue
+                s = [scale * sum(q[bi, h, i, t] * k[bi, kh, j, t] for t in range(d)) for j in keys]
+                mx = max(s)
+                w = [math.exp(x - mx) for x in s]
+                tot = sum(w)
+                lse[bi, h, i] = mx + math.log(tot)
+                for wj, j in zip(w, keys):
+                    out[bi, h, i] += (wj / tot) * v[bi, kh, j]
+    return out, lse
+
+
+__all__ = [
+    "repeat_kv",
+    "allowed_mask",
+    "attention_forward",
+    "attention_backward",
+    "softmax_probs",
+    "decode",
+    "split_partials",
+    "combine_partials",
+    "attention_forward_loops",
+]

@@ -1,0 +1,72 @@
+"""Split-KV single-token decode launcher over the gfx950 HIP kernels.
+
+Same contract as the reference's ``flash_decode``
+(``src/stackkernels/_core/attention/decode.py:192-312``): q (B, H_q, 1, D),
+k/v (B, H_kv, S_k, D) with any b/h/s strides (no copy when rows are
+16-byte aligned), returns (B, H_q, 1, D) in q's dtype.  ``S_q != 1`` raises
+``AssertionError`` as the reference does (``:212``).  The split count comes
+from the library's gfx950 table (``plan``) unless ``num_splits`` is given.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from stackkernels_amd._core.attention import _lib
+from stackkernels_amd._core.attention._common import (
+    check_device,
+    default_scale,
+    kernel_head_dim,
+    kernel_operand,
+    pad_head,
+    stream_of,
+)
+from stackkernels_amd._core.attention.layout import validate_attention_layout
+
+
+def plan(dtype: torch.dtype, b: int, hq: int, hkv: int, sk: int, d: int) -> tuple[int, int]:
+    """(num_splits, workspace bytes) the library picks for this decode shape."""
+    lib = _lib.load()
+    ns = ctypes.c_int(0)
+    nb = ctypes.c_size_t(0)
+    _lib.check(lib.sk_decode_plan(_lib.dtype_code(dtype), b, hq, hkv, sk, kernel_head_dim(d),
+                                  ctypes.byref(ns), ctypes.byref(nb)), "flash_decode plan")
+    return ns.value, nb.value
+
+
+def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None = None):
+    """Launch split + combine; see module docstring."""
+    b, hq, hkv, sq, sk, d = validate_attention_layout(q, k, v)
+    assert sq == 1, f"flash_decode requires q_len == 1, got {sq}"
+    dev = check_device(q, k, v)
+    scale = default_scale(d, sm_scale)
+    dk = kernel_head_dim(d)
+    qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k, v))
+    lib = _lib.load()
+    code = _lib.dtype_code(q.dtype)
+    if num_splits is None:
+        ns, nbytes = plan(q.dtype, b, hq, hkv, sk, d)
+    else:
+        ns = int(num_splits)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_workspace(code, b, hq, hkv, sk, dk, ns, ctypes.byref(nb)),
+                   "flash_decode")
+        nbytes = nb.value
+    out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.sk_decode(
+            code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
+            ws.numel(), ns, b, hq, hkv, sk, dk,
+            _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+            scale, stream_of(dev),
+        )
+    _lib.check(rc, "flash_decode")
+    if dk != d:
+        out = out[..., :d].contiguous()
+    return out
+
+
+__all__ = ["flash_decode", "plan"]

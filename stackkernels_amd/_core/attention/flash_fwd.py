@@ -1,0 +1,48 @@
+"""Forward attention launcher over the gfx950 HIP kernel.
+
+Same contract as the reference's ``flash_attn_fwd``
+(``src/stackkernels/_core/attention/flash_fwd.py:182-264``): returns
+``(out, lse)`` with ``out`` (B, H_q, S_q, D) in the input dtype and ``lse``
+(B, H_q, S_q) fp32; GQA/MQA by ``H_q % H_kv == 0``; bottom-right causal mask.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from stackkernels_amd._core.attention import _lib
+from stackkernels_amd._core.attention._common import (
+    check_device,
+    default_scale,
+    kernel_head_dim,
+    kernel_operand,
+    pad_head,
+    stream_of,
+)
+from stackkernels_amd._core.attention.layout import validate_attention_layout
+
+
+def flash_attn_fwd(q, k, v, is_causal: bool = False, sm_scale: float | None = None):
+    """Launch the HIP forward kernel; see module docstring."""
+    b, hq, hkv, sq, sk, d = validate_attention_layout(q, k, v)
+    dev = check_device(q, k, v)
+    scale = default_scale(d, sm_scale)
+    dk = kernel_head_dim(d)
+    qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k, v))
+    out = torch.empty((b, hq, sq, dk), dtype=q.dtype, device=dev)
+    lse = torch.empty((b, hq, sq), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.sk_attn_fwd(
+            _lib.dtype_code(q.dtype), qk.data_ptr(), kk.data_ptr(), vk.data_ptr(),
+            out.data_ptr(), lse.data_ptr(), b, hq, hkv, sq, sk, dk,
+            _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+            int(bool(is_causal)), scale, stream_of(dev),
+        )
+    _lib.check(rc, "flash_attn_fwd")
+    if dk != d:
+        out = out[..., :d].contiguous()
+    return out, lse
+
+
+__all__ = ["flash_attn_fwd"]

@@ -1,0 +1,61 @@
+"""PyTorch reference attention: the path CPU tensors and ``backend='reference'`` take.
+
+Same function, arguments and results as the reference's
+``attention_reference`` / ``repeat_kv``
+(``src/stackkernels/_reference/torch/attention.py:10-76``), which this
+build must keep so existing callers and tests behave identically:
+
+* inputs upcast to float32; KV heads repeated in place for GQA/MQA;
+* scores = q k^T * sm_scale (default 1/sqrt(D));
+* bottom-right causal mask: key j visible to query i iff j <= i + (S_k - S_q);
+* LSE = logsumexp over keys (``-inf`` on a row with no visible key);
+* P = softmax with NaN (fully masked rows) replaced by 0;
+* out = (P v) cast back to q's dtype.
+
+The backward of this path is autograd through this function, as the
+reference's ``FlashAttentionFunction.backward`` does.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+
+def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """(B, H_kv, S, D) -> (B, H_kv * n_rep, S, D); query head h reads KV head h // n_rep."""
+    return x if n_rep == 1 else x.repeat_interleave(n_rep, dim=1)
+
+
+def attention_reference(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    is_causal: bool = False,
+    sm_scale: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Scaled dot-product attention with MHA/GQA/MQA; returns (out, lse)."""
+    _, h_q, s_q, d = q.shape
+    _, h_kv, s_k, d_k = k.shape
+    assert d == d_k, f"Head dimensions must match: {d} != {d_k}"
+    assert h_q % h_kv == 0, f"Query heads {h_q} must be divisible by KV heads {h_kv}"
+    scale = 1.0 / math.sqrt(d) if sm_scale is None else sm_scale
+
+    group = h_q // h_kv
+    qf = q.float()
+    kf = repeat_kv(k, group).float()
+    vf = repeat_kv(v, group).float()
+    scores = (qf @ kf.transpose(-2, -1).contiguous()) * scale
+    if is_causal:
+        rows = torch.arange(s_q, device=q.device)[:, None]
+        cols = torch.arange(s_k, device=q.device)[None, :]
+        hidden = cols > rows + (s_k - s_q)
+        scores = scores.masked_fill(hidden, float("-inf"))
+    lse = torch.logsumexp(scores, dim=-1)
+    probs = torch.nan_to_num(torch.softmax(scores, dim=-1), nan=0.0)
+    out = (probs @ vf).to(q.dtype)
+    return out, lse
+
+
+__all__ = ["attention_reference", "repeat_kv"]

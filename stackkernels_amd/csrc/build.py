@@ -1,0 +1,90 @@
+"""Build libsk_attn.so for gfx950 with hipcc, in place.
+
+Links against torch's own HIP runtime (``torch/lib/libamdhip64.so``, same
+SONAME as ROCm's) with an rpath to it, so a process that has imported torch
+maps exactly one HIP runtime and the library's launches run on torch's
+streams.  Usage: ``python -m stackkernels_amd.csrc.build`` or ``build()``.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+INCLUDE = os.path.join(REPO, "include")
+SOURCES = ["sk_abi.hip", "sk_fwd.hip", "sk_decode.hip", "sk_fp32.hip", "sk_bwd.hip"]
+LIB_NAME = "libsk_attn.so"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=fast",
+    "-fvisibility=hidden",
+    # packed fp32 arithmetic stays off: only scalar fp32 VALU ops are emitted.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def _torch_lib_dir() -> str:
+    import importlib.util
+
+    spec = importlib.util.find_spec("torch")
+    if spec is None or spec.origin is None:
+        raise RuntimeError("torch is not importable; it provides the HIP runtime to link against")
+    return os.path.join(os.path.dirname(spec.origin), "lib")
+
+
+def _hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def lib_path() -> str:
+    return os.path.join(HERE, LIB_NAME)
+
+
+def build(verbose: bool = False, jobs: int = 5) -> str:
+    """Compile every HIP source for gfx950 and link ``libsk_attn.so`` next to them."""
+    hipcc = _hipcc()
+    out_dir = os.path.join(HERE, "_build")
+    os.makedirs(out_dir, exist_ok=True)
+    objs = []
+
+    def compile_one(src: str) -> str:
+        obj = os.path.join(out_dir, src.replace(".hip", ".o"))
+        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{HERE}", "-c", os.path.join(HERE, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tlib = _torch_lib_dir()
+    tmp = lib_path() + ".tmp"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+           f"-L{tlib}", "-lamdhip64", f"-Wl,-rpath,{tlib}", "-Wl,--no-undefined"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, lib_path())
+    return lib_path()
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

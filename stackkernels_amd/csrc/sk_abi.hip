@@ -1,0 +1,308 @@
+// extern "C" entry points of libsk_attn.so (declared in include/sk_attn.h).
+//
+// This layer validates arguments, fills the kernel parameter blocks, applies
+// the gfx950 split table for decode, and launches on the caller's stream.  It
+// never allocates device memory and never synchronises the host.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "sk_attn.h"
+#include "sk_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return (int)e;
+}
+
+int elem_bytes(int dtype) { return dtype == SK_F32 ? 4 : 2; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Common shape checks; messages follow the reference's
+// validate_attention_layout (src/stackkernels/_opt/memory/layout.py:19-39).
+int check_dims(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D) {
+  if (dtype != SK_F32 && dtype != SK_F16 && dtype != SK_BF16)
+    return fail(SK_EUNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (B < 0 || Hq < 0 || Hkv <= 0 || Sq < 0 || Sk < 0 || D <= 0)
+    return fail(SK_EINVAL, "invalid sizes B=%d Hq=%d Hkv=%d Sq=%d Sk=%d D=%d", B, Hq, Hkv, Sq, Sk, D);
+  if (Hq % Hkv != 0)
+    return fail(SK_EINVAL, "Query heads (%d) must be divisible by KV heads (%d) for GQA/MQA", Hq, Hkv);
+  if (sk::padded_head_dim(D) == 0)
+    return fail(SK_EUNSUPPORTED, "head dim %d unsupported: need a multiple of 8 in [8, 256]", D);
+  return SK_OK;
+}
+
+int check_strides(int dtype, const char* name, const int64_t* st) {
+  if (!st) return fail(SK_EINVAL, "%s strides pointer is NULL", name);
+  const int64_t unit = dtype == SK_F32 ? 4 : 8;  // 16 bytes in elements
+  for (int i = 0; i < 3; ++i)
+    if (st[i] < 0 || st[i] % unit != 0)
+      return fail(SK_EINVAL, "%s stride[%d]=%lld must be a non-negative multiple of %lld elements",
+                  name, i, (long long)st[i], (long long)unit);
+  return SK_OK;
+}
+
+int check_ptr(const char* name, const void* p) {
+  if (!p) return fail(SK_EINVAL, "%s pointer is NULL", name);
+  if (!aligned16(p)) return fail(SK_EINVAL, "%s pointer is not 16-byte aligned", name);
+  return SK_OK;
+}
+
+// gfx950 decode split table.  A split is one workgroup per (batch, KV head).
+// One-wave workgroups (groups up to 16 heads) take 18 KB of LDS each, so a CU
+// holds 8 of them; 32- and 64-head groups use 2 and 4 waves.  The table aims
+// for about two full waves of workgroups over the 256 CUs, keeps every split
+// at least 256 keys (8 tiles) so the fixed cost per workgroup stays small,
+// and caps the split count at 1024 (the combine kernel's LDS weight array).
+int plan_splits(int B, int Hq, int Hkv, int Sk) {
+  if (Sk <= 0 || B <= 0 || Hkv <= 0) return 1;
+  const int group = Hq / Hkv;
+  const int waves = group <= 16 ? 1 : group <= 32 ? 2 : 4;
+  const int64_t slots = 256LL * 8 / waves;  // resident workgroups on the chip
+  const int64_t units = (int64_t)B * Hkv;
+  int64_t splits = (2 * slots + units - 1) / units;
+  splits = std::min<int64_t>(splits, std::max(1, Sk / 256));
+  splits = std::max<int64_t>(1, std::min<int64_t>(splits, 1024));
+  return (int)splits;
+}
+
+int keys_per_split_for(int Sk, int splits) {
+  int kps = (Sk + splits - 1) / splits;
+  kps = (kps + 31) / 32 * 32;
+  return std::max(kps, 32);
+}
+
+size_t decode_ws_bytes(int dtype, int B, int Hq, int D, int splits) {
+  if (dtype == SK_F32) return (size_t)B * Hq * sizeof(float);  // LSE of the fp32 forward
+  if (splits <= 1) return 0;
+  const size_t dpad = (size_t)sk::padded_head_dim(D);
+  return (size_t)B * Hq * splits * (dpad + 1) * sizeof(float);
+}
+
+size_t bwd_ws_bytes(int B, int Hq, int Sq) {
+  const size_t rows = (size_t)B * Hq * Sq;
+  return 2 * ((rows * sizeof(float) + 255) / 256 * 256);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sk_abi_version(void) { return SK_ABI_VERSION; }
+
+const char* sk_last_error(void) { return g_err; }
+
+int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                int B, int Hq, int Hkv, int Sq, int Sk, int D, const int64_t* q_strides,
+                const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                int is_causal, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
+  if (rc) return rc;
+  if ((rc = check_strides(dtype, "q", q_strides)) || (rc = check_strides(dtype, "k", k_strides)) ||
+      (rc = check_strides(dtype, "v", v_strides)) || (rc = check_strides(dtype, "o", o_strides)))
+    return rc;
+  if ((int64_t)B * Hq * Sq == 0) return SK_OK;
+  if ((rc = check_ptr("q", q)) || (rc = check_ptr("o", o)) || (rc = check_ptr("lse", lse)))
+    return rc;
+  if (Sk > 0 && ((rc = check_ptr("k", k)) || (rc = check_ptr("v", v)))) return rc;
+
+  sk::FwdParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.lse = lse;
+  p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_ss = o_strides[2];
+  p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+  p.scale = std::fabs(sm_scale);
+  p.scale_log2 = p.scale * 1.4426950408889634f;
+  const bool neg = sm_scale < 0.f;
+  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, sk::padded_head_dim(D));
+  p.n_mblocks = (Sq + rows - 1) / rows;
+  if ((int64_t)p.n_mblocks * B * Hq > 0x7fffffffLL)
+    return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p.n_mblocks * B * Hq);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == SK_F32) {
+    p.q_sign = neg ? 1u : 0u;
+    e = sk::launch_fwd_f32(p, is_causal != 0, s);
+  } else {
+    p.q_sign = neg ? 0x80008000u : 0u;
+    e = sk::launch_fwd_mfma(dtype, p, is_causal != 0, s);
+  }
+  if (e != hipSuccess) return hip_fail(e, "sk_attn_fwd launch");
+  return SK_OK;
+}
+
+int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
+                          size_t* bytes) {
+  g_err[0] = 0;
+  (void)is_causal;
+  int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
+  if (rc) return rc;
+  if (!bytes) return fail(SK_EINVAL, "bytes pointer is NULL");
+  *bytes = bwd_ws_bytes(B, Hq, Sq);
+  return SK_OK;
+}
+
+int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
+                const void* o, const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                int is_causal, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
+  if (rc) return rc;
+  if ((int64_t)B * Hq * Sq == 0 && (int64_t)B * Hkv * Sk == 0) return SK_OK;
+  const size_t need = bwd_ws_bytes(B, Hq, Sq);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(SK_EWORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+  if ((int64_t)B * Hq * Sq > 0 &&
+      ((rc = check_ptr("dout", dout)) || (rc = check_ptr("q", q)) || (rc = check_ptr("o", o)) ||
+       (rc = check_ptr("lse", lse)) || (rc = check_ptr("dq", dq))))
+    return rc;
+  if ((int64_t)B * Hkv * Sk > 0 && ((rc = check_ptr("k", k)) || (rc = check_ptr("v", v)) ||
+                                    (rc = check_ptr("dk", dk)) || (rc = check_ptr("dv", dv))))
+    return rc;
+  if (need > 0 && (rc = check_ptr("workspace", workspace))) return rc;
+
+  sk::BwdParams p{};
+  p.dout = dout, p.q = q, p.k = k, p.v = v, p.o = o, p.lse = lse;
+  p.dq = dq, p.dk = dk, p.dv = dv;
+  const size_t rows = (size_t)B * Hq * Sq;
+  const size_t rows_bytes = (rows * sizeof(float) + 255) / 256 * 256;
+  p.delta = (float*)workspace;
+  p.lse_log2 = (float*)((char*)workspace + rows_bytes);
+  p.dq_acc = nullptr;
+  p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+  p.scale = sm_scale;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (rows > 0) e = sk::launch_bwd_prep(dtype, p, s);
+  if (e != hipSuccess) return hip_fail(e, "sk_attn_bwd preprocess launch");
+  if (dtype == SK_F32)
+    e = sk::launch_bwd_f32(p, is_causal != 0, s);
+  else
+    e = sk::launch_bwd_mfma(dtype, p, is_causal != 0, s);
+  if (e != hipSuccess) return hip_fail(e, "sk_attn_bwd launch");
+  return SK_OK;
+}
+
+int sk_decode_plan(int dtype, int B, int Hq, int Hkv, int Sk, int D, int* num_splits,
+                   size_t* workspace_bytes) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
+  if (rc) return rc;
+  if (!num_splits || !workspace_bytes) return fail(SK_EINVAL, "output pointer is NULL");
+  int splits = dtype == SK_F32 ? 1 : plan_splits(B, Hq, Hkv, Sk);
+  if (splits > 1) splits = (Sk + keys_per_split_for(Sk, splits) - 1) / keys_per_split_for(Sk, splits);
+  *num_splits = splits;
+  *workspace_bytes = decode_ws_bytes(dtype, B, Hq, D, splits);
+  return SK_OK;
+}
+
+int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,
+                        size_t* workspace_bytes) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
+  if (rc) return rc;
+  if (!workspace_bytes) return fail(SK_EINVAL, "output pointer is NULL");
+  if (num_splits < 1 || num_splits > 1024)
+    return fail(SK_EINVAL, "num_splits=%d outside [1, 1024]", num_splits);
+  *workspace_bytes = decode_ws_bytes(dtype, B, Hq, D, num_splits);
+  return SK_OK;
+}
+
+int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, void* workspace,
+              size_t workspace_bytes, int num_splits, int B, int Hq, int Hkv, int Sk, int D,
+              const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+              const int64_t* o_strides, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
+  if (rc) return rc;
+  if ((rc = check_strides(dtype, "q", q_strides)) || (rc = check_strides(dtype, "k", k_strides)) ||
+      (rc = check_strides(dtype, "v", v_strides)) || (rc = check_strides(dtype, "o", o_strides)))
+    return rc;
+  if ((int64_t)B * Hq == 0) return SK_OK;
+  if ((rc = check_ptr("q", q)) || (rc = check_ptr("o", o))) return rc;
+  if (Sk > 0 && ((rc = check_ptr("k", k)) || (rc = check_ptr("v", v)))) return rc;
+  if (Hq / Hkv > 64 && dtype != SK_F32)
+    return fail(SK_EUNSUPPORTED, "decode supports up to 64 query heads per KV head, got %d", Hq / Hkv);
+
+  if (dtype == SK_F32) num_splits = 1;
+  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk);
+  if (num_splits < 1 || num_splits > 1024)
+    return fail(SK_EINVAL, "num_splits=%d outside [1, 1024]", num_splits);
+  const int kps = keys_per_split_for(Sk, num_splits);
+  if (Sk > 0) num_splits = std::min(num_splits, (Sk + kps - 1) / kps);
+  const size_t need = decode_ws_bytes(dtype, B, Hq, D, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(SK_EWORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+  if (need > 0 && (rc = check_ptr("workspace", workspace))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+
+  if (dtype == SK_F32) {
+    // fp32 decode is the fp32 forward with one query row (reference:
+    // src/stackkernels/torch/attention.py:154 computes it the same way).
+    sk::FwdParams p{};
+    p.q = q, p.k = k, p.v = v, p.o = o, p.lse = (float*)workspace;
+    p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_ss = q_strides[2];
+    p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_ss = k_strides[2];
+    p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_ss = v_strides[2];
+    p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_ss = o_strides[2];
+    p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = 1, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+    p.scale = std::fabs(sm_scale);
+    p.scale_log2 = p.scale * 1.4426950408889634f;
+    p.q_sign = sm_scale < 0.f ? 1u : 0u;
+    p.n_mblocks = 1;
+    hipError_t e = sk::launch_fwd_f32(p, false, s);
+    if (e != hipSuccess) return hip_fail(e, "sk_decode launch");
+    return SK_OK;
+  }
+
+  sk::DecParams p{};
+  p.q = q, p.k = k, p.v = v, p.o = o;
+  p.q_sb = q_strides[0], p.q_sh = q_strides[1];
+  p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0], p.o_sh = o_strides[1];
+  p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+  p.num_splits = num_splits;
+  p.keys_per_split = kps;
+  p.dpad = sk::padded_head_dim(D);
+  p.scale = std::fabs(sm_scale);
+  p.scale_log2 = p.scale * 1.4426950408889634f;
+  p.q_sign = sm_scale < 0.f ? 0x80008000u : 0u;
+  if (num_splits > 1) {
+    p.part_o = (float*)workspace;
+    p.part_lse = p.part_o + (size_t)B * Hq * num_splits * p.dpad;
+  }
+  hipError_t e = sk::launch_decode_mfma(dtype, p, s);
+  if (e != hipSuccess) return hip_fail(e, "sk_decode split launch");
+  if (num_splits > 1) {
+    e = sk::launch_decode_combine(dtype, p, s);
+    if (e != hipSuccess) return hip_fail(e, "sk_decode combine launch");
+  }
+  return SK_OK;
+}
+
+}  // extern "C"

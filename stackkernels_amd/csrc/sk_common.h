@@ -1,0 +1,124 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Element storage is raw 16-bit words (bf16 or fp16) or fp32.  MFMA operands
+// are 8 x 16-bit values per lane (one 128-bit register quad).  Layouts used by
+// the kernels (checked on gfx950 hardware):
+//
+//   v_mfma_f32_32x32x16_{bf16,f16}: lane l supplies A[row l%32][k 8*(l/32)+e],
+//     B[k 8*(l/32)+e][col l%32], e = 0..7; result register r of lane l is
+//     C[row 8*(r/4) + 4*(l/32) + r%4][col l%32].
+//   v_mfma_f32_16x16x32_{bf16,f16}: A[row l%16][k 8*(l/16)+e], B[k 8*(l/16)+e]
+//     [col l%16]; result r is C[row 4*(l/16) + r][col l%16].
+//   ds_read_b64_tr_b16: within each group of 16 lanes, lane j addresses 4
+//     consecutive 16-bit words; lane i receives word (i%4) of lanes
+//     4e + i/4 for e = 0..3.  If lane j points at row r0 + j/4, column
+//     c0 + 4*(j%4) of a row-major tile, lane i receives column c0 + i of
+//     rows r0..r0+3: a transposed 4 x 16 read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sk {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Type tags for the two 16-bit element types.
+struct BF16 {
+  static constexpr int code = 2;
+};
+struct F16 {
+  static constexpr int code = 1;
+};
+
+template <class T>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<BF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<F16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <class T>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Two fp32 values -> one dword of two 16-bit values (round to nearest even).
+template <class T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
+  f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
+  f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+}
+
+// 16-bit word -> fp32.
+template <class T>
+__device__ __forceinline__ float to_f32(uint16_t x);
+template <>
+__device__ __forceinline__ float to_f32<BF16>(uint16_t x) {
+  return __builtin_bit_cast(float, (uint32_t)x << 16);
+}
+template <>
+__device__ __forceinline__ float to_f32<F16>(uint16_t x) {
+  return (float)__builtin_bit_cast(_Float16, x);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max / sum of a value across lanes l and l^32 of a wave64.
+__device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32); }
+
+// Transposed 4 x 16 read from a row-major LDS tile (see header comment).
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__device__ __forceinline__ u32x4 lds_read_b128(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ u32x4 ldg_b128(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 ldg_b128_cached(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+}  // namespace sk

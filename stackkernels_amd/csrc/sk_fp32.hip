@@ -1,0 +1,351 @@
+// fp32 attention kernels (forward, backward) on the gfx950 vector ALUs, and
+// the backward row-statistics pass shared by every dtype.
+//
+// fp32 inputs are computed in true fp32 (no reduced-precision MFMA inputs),
+// which is what the reference path does (_reference/torch/attention.py:56-61).
+// Four lanes share one row: each holds a quarter of the head dimension, and
+// q.k partial sums are combined with two cross-lane adds.  K/V (or Q/dO)
+// tiles of 16 rows are staged in LDS; the online softmax is updated once per
+// tile.
+#include "sk_common.h"
+#include "sk_kernels.h"
+
+namespace sk {
+
+constexpr int kF32Rows = 64;  // rows per workgroup (4 lanes per row)
+constexpr int kF32Tile = 16;  // keys (or queries) per LDS tile
+
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  return x;
+}
+
+// Forward: O = softmax(scale q k^T + mask) v, LSE in natural log.
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
+  constexpr int DC = DP / 4;  // head-dim slice per lane
+  __shared__ float ks[kF32Tile][DP];
+  __shared__ float vs[kF32Tile][DP];
+
+  const int tid = threadIdx.x;
+  const int part = tid & 3;
+  const int rloc = tid >> 2;
+  const int bh_count = p.B * p.Hq;
+  const int mblk = p.n_mblocks - 1 - blockIdx.x / bh_count;
+  const int bh = blockIdx.x % bh_count;
+  const int b = bh / p.Hq, hq = bh % p.Hq, hkv = hq / p.group;
+  const int m0 = mblk * kF32Rows;
+  const int row = m0 + rloc;
+  const int diag = p.Sk - p.Sq;
+  const bool row_ok = row < p.Sq;
+
+  const float* qp = (const float*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)row * p.q_ss;
+  const float* kbase = (const float*)p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = (const float*)p.v + b * p.v_sb + hkv * p.v_sh;
+  const float sgn = p.q_sign ? -1.f : 1.f;
+
+  float q[DC], acc[DC];
+#pragma unroll
+  for (int i = 0; i < DC; ++i) {
+    const int d = part * DC + i;
+    q[i] = (row_ok && d < p.D) ? qp[d] * sgn : 0.f;
+    acc[i] = 0.f;
+  }
+  float m_run = kNegInf, l_run = 0.f;
+  int n_end = p.Sk;
+  if (CAUSAL) n_end = min(p.Sk, m0 + kF32Rows + diag);
+  const int lim = CAUSAL ? min(p.Sk - 1, row + diag) : p.Sk - 1;
+
+  for (int n0 = 0; n0 < n_end; n0 += kF32Tile) {
+    __syncthreads();
+    for (int e = tid; e < kF32Tile * DP; e += 256) {
+      const int r = e / DP, d = e % DP, n = n0 + r;
+      const bool ok = n < p.Sk && d < p.D;
+      ks[r][d] = ok ? kbase[(int64_t)n * p.k_ss + d] : 0.f;
+      vs[r][d] = ok ? vbase[(int64_t)n * p.v_ss + d] : 0.f;
+    }
+    __syncthreads();
+    float s[kF32Tile];
+    float mt = kNegInf;
+#pragma unroll
+    for (int j = 0; j < kF32Tile; ++j) {
+      float x = 0.f;
+#pragma unroll
+      for (int i = 0; i < DC; ++i) x = fmaf(q[i], ks[j][part * DC + i], x);
+      x = quad_sum(x) * p.scale;
+      if (n0 + j > lim) x = kNegInf;
+      s[j] = x;
+      mt = fmaxf(mt, x);
+    }
+    const float m_new = fmaxf(m_run, mt);
+    const float m_sub = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = __expf(m_run - m_sub);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int i = 0; i < DC; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int j = 0; j < kF32Tile; ++j) {
+      const float pj = expf(s[j] - m_sub);
+      l_run += pj;
+#pragma unroll
+      for (int i = 0; i < DC; ++i) acc[i] = fmaf(pj, vs[j][part * DC + i], acc[i]);
+    }
+  }
+  if (!row_ok) return;
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  float* op = (float*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)row * p.o_ss;
+#pragma unroll
+  for (int i = 0; i < DC; ++i) {
+    const int d = part * DC + i;
+    if (d < p.D) op[d] = acc[i] * inv;
+  }
+  if (part == 0) p.lse[(int64_t)bh * p.Sq + row] = l_run > 0.f ? m_run + logf(l_run) : kNegInf;
+}
+
+// Row statistics for the backward, any dtype:
+//   delta[r]    = sum_d dO[r,d] * O[r,d]          (reference flash_bwd.py:15-55)
+//   lse_log2[r] = lse[r] * log2(e), or +inf where lse = -inf so that
+//                 exp2(s - lse_log2) is exactly 0 on rows that see no key.
+template <class T>
+__device__ __forceinline__ float ld_elem(const void* p, int64_t i);
+template <>
+__device__ __forceinline__ float ld_elem<float>(const void* p, int64_t i) {
+  return ((const float*)p)[i];
+}
+template <>
+__device__ __forceinline__ float ld_elem<BF16>(const void* p, int64_t i) {
+  return to_f32<BF16>(((const uint16_t*)p)[i]);
+}
+template <>
+__device__ __forceinline__ float ld_elem<F16>(const void* p, int64_t i) {
+  return to_f32<F16>(((const uint16_t*)p)[i]);
+}
+
+template <class T>
+__global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
+  const int64_t r = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int part = threadIdx.x & 3;
+  float x = 0.f;
+  if (r < rows) {
+    const int64_t base = r * p.D;
+    for (int d = part; d < p.D; d += 4) x = fmaf(ld_elem<T>(p.dout, base + d), ld_elem<T>(p.o, base + d), x);
+  }
+  x = quad_sum(x);
+  if (r < rows && part == 0) {
+    p.delta[r] = x;
+    const float l = p.lse[r];
+    p.lse_log2[r] = l == kNegInf ? __builtin_inff() : l * kLog2e;
+  }
+}
+
+// dQ for fp32: rows of queries, loop over keys.
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(256) bwd_dq_f32_kernel(BwdParams p) {
+  constexpr int DC = DP / 4;
+  __shared__ float ks[kF32Tile][DP];
+  __shared__ float vs[kF32Tile][DP];
+  const int tid = threadIdx.x, part = tid & 3, rloc = tid >> 2;
+  const int bh_count = p.B * p.Hq;
+  const int mblk = p.n_mblocks - 1 - blockIdx.x / bh_count;
+  const int bh = blockIdx.x % bh_count;
+  const int b = bh / p.Hq, hq = bh % p.Hq, hkv = hq / p.group;
+  const int row = mblk * kF32Rows + rloc;
+  const bool row_ok = row < p.Sq;
+  const int diag = p.Sk - p.Sq;
+  const int64_t qrow = ((int64_t)bh * p.Sq + row) * p.D;
+  const float* kbase = (const float*)p.k + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+  const float* vbase = (const float*)p.v + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+
+  float q[DC], g[DC], acc[DC];
+#pragma unroll
+  for (int i = 0; i < DC; ++i) {
+    const int d = part * DC + i;
+    const bool ok = row_ok && d < p.D;
+    q[i] = ok ? ((const float*)p.q)[qrow + d] : 0.f;
+    g[i] = ok ? ((const float*)p.dout)[qrow + d] : 0.f;
+    acc[i] = 0.f;
+  }
+  const float lse2 = row_ok ? p.lse_log2[(int64_t)bh * p.Sq + row] : __builtin_inff();
+  const float dl = row_ok ? p.delta[(int64_t)bh * p.Sq + row] : 0.f;
+  int n_end = p.Sk;
+  if (CAUSAL) n_end = min(p.Sk, mblk * kF32Rows + kF32Rows + diag);
+  const int lim = CAUSAL ? min(p.Sk - 1, row + diag) : p.Sk - 1;
+  for (int n0 = 0; n0 < n_end; n0 += kF32Tile) {
+    __syncthreads();
+    for (int e = tid; e < kF32Tile * DP; e += 256) {
+      const int r = e / DP, d = e % DP, n = n0 + r;
+      const bool ok = n < p.Sk && d < p.D;
+      ks[r][d] = ok ? kbase[(int64_t)n * p.D + d] : 0.f;
+      vs[r][d] = ok ? vbase[(int64_t)n * p.D + d] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int j = 0; j < kF32Tile; ++j) {
+      float s = 0.f, dp = 0.f;
+#pragma unroll
+      for (int i = 0; i < DC; ++i) {
+        s = fmaf(q[i], ks[j][part * DC + i], s);
+        dp = fmaf(g[i], vs[j][part * DC + i], dp);
+      }
+      s = quad_sum(s);
+      dp = quad_sum(dp);
+      const float pj = (n0 + j > lim) ? 0.f : exp2f(s * p.scale_log2 - lse2);
+      const float ds = pj * (dp - dl);
+#pragma unroll
+      for (int i = 0; i < DC; ++i) acc[i] = fmaf(ds, ks[j][part * DC + i], acc[i]);
+    }
+  }
+  if (!row_ok) return;
+#pragma unroll
+  for (int i = 0; i < DC; ++i) {
+    const int d = part * DC + i;
+    if (d < p.D) ((float*)p.dq)[qrow + d] = acc[i] * p.scale;
+  }
+}
+
+// dK, dV for fp32: rows of keys of one KV head; loop over the group's query
+// heads and their queries (the GQA sum happens in registers, no atomics).
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(256) bwd_dkv_f32_kernel(BwdParams p) {
+  constexpr int DC = DP / 4;
+  __shared__ float qs[kF32Tile][DP];
+  __shared__ float gs[kF32Tile][DP];
+  __shared__ float ls[kF32Tile], dls[kF32Tile];
+  const int tid = threadIdx.x, part = tid & 3, rloc = tid >> 2;
+  const int bk_count = p.B * p.Hkv;
+  const int nblk = blockIdx.x / bk_count;
+  const int bk = blockIdx.x % bk_count;
+  const int b = bk / p.Hkv, hkv = bk % p.Hkv;
+  const int n = nblk * kF32Rows + rloc;
+  const bool key_ok = n < p.Sk;
+  const int diag = p.Sk - p.Sq;
+  const int64_t krow = ((int64_t)bk * p.Sk + n) * p.D;
+
+  float k[DC], v[DC], dk[DC], dv[DC];
+#pragma unroll
+  for (int i = 0; i < DC; ++i) {
+    const int d = part * DC + i;
+    const bool ok = key_ok && d < p.D;
+    k[i] = ok ? ((const float*)p.k)[krow + d] : 0.f;
+    v[i] = ok ? ((const float*)p.v)[krow + d] : 0.f;
+    dk[i] = dv[i] = 0.f;
+  }
+  // Query rows that can see some key of this block: i >= n0 - diag.
+  int m_begin = 0;
+  if (CAUSAL) m_begin = max(0, nblk * kF32Rows - diag);
+  for (int gi = 0; gi < p.group; ++gi) {
+    const int hq = hkv * p.group + gi;
+    const int64_t bh = (int64_t)b * p.Hq + hq;
+    for (int m0 = m_begin; m0 < p.Sq; m0 += kF32Tile) {
+      __syncthreads();
+      for (int e = tid; e < kF32Tile * DP; e += 256) {
+        const int r = e / DP, d = e % DP, m = m0 + r;
+        const bool ok = m < p.Sq && d < p.D;
+        const int64_t idx = (bh * p.Sq + m) * p.D + d;
+        qs[r][d] = ok ? ((const float*)p.q)[idx] : 0.f;
+        gs[r][d] = ok ? ((const float*)p.dout)[idx] : 0.f;
+      }
+      if (tid < kF32Tile) {
+        const int m = m0 + tid;
+        ls[tid] = m < p.Sq ? p.lse_log2[bh * p.Sq + m] : __builtin_inff();
+        dls[tid] = m < p.Sq ? p.delta[bh * p.Sq + m] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int j = 0; j < kF32Tile; ++j) {
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int i = 0; i < DC; ++i) {
+          s = fmaf(k[i], qs[j][part * DC + i], s);
+          dp = fmaf(v[i], gs[j][part * DC + i], dp);
+        }
+        s = quad_sum(s);
+        dp = quad_sum(dp);
+        const int m = m0 + j;
+        const bool vis = m < p.Sq && (!CAUSAL || n <= m + diag);
+        const float pj = vis ? exp2f(s * p.scale_log2 - ls[j]) : 0.f;
+        const float ds = pj * (dp - dls[j]);
+#pragma unroll
+        for (int i = 0; i < DC; ++i) {
+          dv[i] = fmaf(pj, gs[j][part * DC + i], dv[i]);
+          dk[i] = fmaf(ds, qs[j][part * DC + i], dk[i]);
+        }
+      }
+    }
+  }
+  if (!key_ok) return;
+#pragma unroll
+  for (int i = 0; i < DC; ++i) {
+    const int d = part * DC + i;
+    if (d < p.D) {
+      ((float*)p.dk)[krow + d] = dk[i] * p.scale;
+      ((float*)p.dv)[krow + d] = dv[i];
+    }
+  }
+}
+
+template <int DP>
+static void launch_fwd_f32_dp(const FwdParams& p, bool causal, hipStream_t s) {
+  const dim3 grid((unsigned)(p.n_mblocks * p.B * p.Hq));
+  if (causal)
+    hipLaunchKernelGGL((fwd_f32_kernel<DP, true>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((fwd_f32_kernel<DP, false>), grid, dim3(256), 0, s, p);
+}
+
+hipError_t launch_fwd_f32(const FwdParams& p, bool causal, hipStream_t s) {
+  switch (padded_head_dim(p.D)) {
+    case 64: launch_fwd_f32_dp<64>(p, causal, s); break;
+    case 96: launch_fwd_f32_dp<96>(p, causal, s); break;
+    case 128: launch_fwd_f32_dp<128>(p, causal, s); break;
+    case 256: launch_fwd_f32_dp<256>(p, causal, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s) {
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
+  const dim3 grid((unsigned)((rows + 63) / 64));
+  if (dtype == 0)
+    hipLaunchKernelGGL((bwd_prep_kernel<float>), grid, dim3(256), 0, s, p);
+  else if (dtype == BF16::code)
+    hipLaunchKernelGGL((bwd_prep_kernel<BF16>), grid, dim3(256), 0, s, p);
+  else if (dtype == F16::code)
+    hipLaunchKernelGGL((bwd_prep_kernel<F16>), grid, dim3(256), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <int DP>
+static void launch_bwd_f32_dp(const BwdParams& p, bool causal, hipStream_t s) {
+  const int mb = (p.Sq + kF32Rows - 1) / kF32Rows;
+  const int nb = (p.Sk + kF32Rows - 1) / kF32Rows;
+  BwdParams q = p;
+  q.n_mblocks = mb;
+  const dim3 gq((unsigned)(mb * p.B * p.Hq)), gk((unsigned)(nb * p.B * p.Hkv));
+  if (causal) {
+    hipLaunchKernelGGL((bwd_dq_f32_kernel<DP, true>), gq, dim3(256), 0, s, q);
+    hipLaunchKernelGGL((bwd_dkv_f32_kernel<DP, true>), gk, dim3(256), 0, s, q);
+  } else {
+    hipLaunchKernelGGL((bwd_dq_f32_kernel<DP, false>), gq, dim3(256), 0, s, q);
+    hipLaunchKernelGGL((bwd_dkv_f32_kernel<DP, false>), gk, dim3(256), 0, s, q);
+  }
+}
+
+hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s) {
+  switch (padded_head_dim(p.D)) {
+    case 64: launch_bwd_f32_dp<64>(p, causal, s); break;
+    case 96: launch_bwd_f32_dp<96>(p, causal, s); break;
+    case 128: launch_bwd_f32_dp<128>(p, causal, s); break;
+    case 256: launch_bwd_f32_dp<256>(p, causal, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sk

@@ -1,0 +1,80 @@
+// Kernel parameter blocks and host-side launcher declarations shared by the
+// kernel translation units and the C-ABI layer (sk_abi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sk {
+
+// Forward attention, prefill shape.  Strides are element strides.
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int B, Hq, Hkv, Sq, Sk, D, group;
+  int n_mblocks;     // ceil(Sq / rows per workgroup)
+  float scale;       // |sm_scale|
+  float scale_log2;  // |sm_scale| * log2(e)
+  uint32_t q_sign;   // 0, or the sign-bit mask that negates q when sm_scale < 0
+};
+
+// Split-KV decode (Sq == 1).
+struct DecParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* part_o;    // [B*Hq][num_splits][dpad] fp32, normalised per split
+  float* part_lse;  // [B*Hq][num_splits]
+  int64_t q_sb, q_sh;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh;
+  int B, Hq, Hkv, Sk, D, group;
+  int num_splits, keys_per_split, dpad;
+  float scale, scale_log2;
+  uint32_t q_sign;
+};
+
+// Backward attention; every tensor contiguous BHSD.
+struct BwdParams {
+  const void* dout;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const float* lse;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* delta;     // [B*Hq*Sq] fp32 scratch: rowsum(dO * O)
+  float* lse_log2;  // [B*Hq*Sq] fp32 scratch: lse * log2(e) (+inf for empty rows)
+  float* dq_acc;    // [B*Hq*Sq*D] fp32 scratch (dQ accumulator) or null
+  int B, Hq, Hkv, Sq, Sk, D, group;
+  float scale, scale_log2;
+  int n_mblocks, n_nblocks;
+};
+
+// Launchers: return hipSuccess or the launch error.  dtype is SK_F32/F16/BF16.
+hipError_t launch_fwd_mfma(int dtype, const FwdParams& p, bool causal, hipStream_t s);
+hipError_t launch_fwd_f32(const FwdParams& p, bool causal, hipStream_t s);
+hipError_t launch_decode_mfma(int dtype, const DecParams& p, hipStream_t s);
+hipError_t launch_decode_combine(int dtype, const DecParams& p, hipStream_t s);
+hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s);
+hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s);
+hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s);
+
+// Rows of queries one forward workgroup covers for (dtype, padded head dim).
+int fwd_rows_per_block(int dtype, int dpad);
+// Padded head dim the kernels are compiled for (64, 96, 128 or 256), or 0.
+int padded_head_dim(int d);
+
+}  // namespace sk

@@ -1,0 +1,10 @@
+"""PyTorch frontend: the reference's ``stackkernels.torch`` attention API."""
+
+from stackkernels_amd.torch.attention import (
+    FlashAttention,
+    FlashAttentionFunction,
+    flash_attention,
+    flash_decode,
+)
+
+__all__ = ["flash_attention", "flash_decode", "FlashAttention", "FlashAttentionFunction"]

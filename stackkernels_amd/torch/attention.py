@@ -1,0 +1,180 @@
+"""PyTorch attention API over the gfx950 HIP kernels.
+
+Drop-in for ``stackkernels.torch.attention``
+(``src/stackkernels/torch/attention.py:17-231``): the same functions,
+autograd Function, module, custom op and ``__all__``.  What changes is what
+runs behind them: ROCm device tensors go to ``libsk_attn.so`` (forward,
+backward and split-KV decode kernels written for gfx950); CPU tensors and
+``backend='reference'`` run the PyTorch reference path, exactly where the
+reference did.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+import torch.nn as nn
+
+from stackkernels_amd._core.attention.decode import flash_decode as core_flash_decode
+from stackkernels_amd._core.attention.flash_bwd import flash_attn_bwd
+from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
+from stackkernels_amd._reference.torch.attention import attention_reference
+from stackkernels_amd.torch._dispatch import should_use_hip
+from stackkernels_amd.torch._utils import ensure_contiguous
+
+
+class FlashAttentionFunction(torch.autograd.Function):
+    """FlashAttention-2 forward/backward with MHA, GQA and MQA support.
+
+    ``forward(ctx, q, k, v, is_causal=False, sm_scale=None)`` returns the
+    output; ``backward`` returns ``(dq, dk, dv, None, None)``.  Reference:
+    ``src/stackkernels/torch/attention.py:17-102``.
+    """
+
+    @staticmethod
+    def forward(
+        ctx: Any,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        is_causal: bool = False,
+        sm_scale: float | None = None,
+    ) -> torch.Tensor:
+        use_hip = should_use_hip(q)
+        scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else sm_scale
+        ctx.use_hip = use_hip
+        ctx.is_causal = is_causal
+        ctx.sm_scale = scale
+        qc, kc, vc = ensure_contiguous(q), ensure_contiguous(k), ensure_contiguous(v)
+        if use_hip:
+            out, lse = flash_attn_fwd(qc, kc, vc, is_causal=is_causal, sm_scale=scale)
+        else:
+            out, lse = attention_reference(qc, kc, vc, is_causal=is_causal, sm_scale=scale)
+        ctx.save_for_backward(qc, kc, vc, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, do: torch.Tensor):
+        q, k, v, out, lse = ctx.saved_tensors
+        do = ensure_contiguous(do)
+        if ctx.use_hip:
+            dq, dk, dv = flash_attn_bwd(do, q, k, v, out, lse, is_causal=ctx.is_causal,
+                                        sm_scale=ctx.sm_scale)
+            return dq, dk, dv, None, None
+        # Reference path: autograd through the reference forward
+        # (src/stackkernels/torch/attention.py:82-102).
+        qr, kr, vr = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        with torch.enable_grad():
+            out_ref, _ = attention_reference(qr, kr, vr, is_causal=ctx.is_causal,
+                                             sm_scale=ctx.sm_scale)
+            out_ref.backward(do)
+        return qr.grad, kr.grad, vr.grad, None, None
+
+
+def flash_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    is_causal: bool = False,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """Flash Attention forward (differentiable).
+
+    Supports MHA (H_q == H_kv), GQA (H_q > H_kv > 1), MQA (H_kv == 1), the
+    bottom-right causal mask ``k <= q + (S_k - S_q)`` and head dims up to 256
+    (64, 80, 96, 128, 256 as in the reference, and any other up to 256).
+
+    Args:
+        q: (B, H_q, S_q, D).  k, v: (B, H_kv, S_k, D).
+        is_causal: apply the bottom-right causal mask.
+        sm_scale: score scale, default 1/sqrt(D).
+
+    Returns:
+        (B, H_q, S_q, D) in q's dtype.
+    """
+    return FlashAttentionFunction.apply(q, k, v, is_causal, sm_scale)
+
+
+def flash_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """Split-KV decode for one query token (S_q = 1) over the whole cache.
+
+    Args:
+        q: (B, H_q, 1, D).  k, v: (B, H_kv, S_k, D); any b/h/s strides.
+        sm_scale: score scale, default 1/sqrt(D).
+
+    Returns:
+        (B, H_q, 1, D) in q's dtype.
+    """
+    if should_use_hip(q):
+        return core_flash_decode(q, k, v, sm_scale=sm_scale)
+    out, _ = attention_reference(q, k, v, is_causal=False, sm_scale=sm_scale)
+    return out
+
+
+class FlashAttention(nn.Module):
+    """FlashAttention module with MHA, GQA and MQA support.
+
+    Args:
+        is_causal: apply the bottom-right aligned causal mask. Default: False.
+        sm_scale: softmax scale. Default: 1/sqrt(D).
+
+    Examples:
+        >>> attn = FlashAttention(is_causal=True)
+        >>> q = torch.randn(2, 8, 1024, 64)
+        >>> out = attn(q, q, q)
+    """
+
+    def __init__(self, is_causal: bool = False, sm_scale: float | None = None) -> None:
+        super().__init__()
+        self.is_causal = is_causal
+        self.sm_scale = sm_scale
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        return flash_attention(q, k, v, is_causal=self.is_causal, sm_scale=self.sm_scale)
+
+
+# torch.library custom op under the reference's name
+# (src/stackkernels/torch/attention.py:200-223): ``torch.ops.stackkernels.flash_attn_op``,
+# forward only, fake impl returns empty_like(q).  If that name is already
+# registered in this process (the original package imported alongside), the
+# existing registration is kept.
+def _register_custom_op() -> bool:
+    try:
+        torch.ops.stackkernels.flash_attn_op  # noqa: B018
+        return False
+    except (AttributeError, RuntimeError):
+        pass
+
+    @torch.library.custom_op("stackkernels::flash_attn_op", mutates_args=())
+    def _flash_attn_op(
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        is_causal: bool,
+        sm_scale: float | None,
+    ) -> torch.Tensor:
+        return flash_attention(q, k, v, is_causal=is_causal, sm_scale=sm_scale)
+
+    @_flash_attn_op.register_fake
+    def _flash_attn_op_fake(q, k, v, is_causal, sm_scale):
+        return torch.empty_like(q)
+
+    return True
+
+
+_CUSTOM_OP_REGISTERED = _register_custom_op()
+
+
+__all__ = [
+    "flash_attention",
+    "flash_decode",
+    "FlashAttention",
+    "FlashAttentionFunction",
+]

@@ -1,0 +1,110 @@
+"""The C-ABI library: it loads, exports what include/sk_attn.h declares, binds
+torch's HIP runtime, and rejects bad arguments before launching anything.
+No test here launches a kernel, so all of it runs without a GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sk_attn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from stackkernels_amd._core.attention import _lib
+    from stackkernels_amd.csrc import build
+
+    if not os.path.exists(_lib.LIB_PATH):
+        build.build()
+    return _lib.load()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return re.findall(r"SK_API\s+[\w\s\*]+?\b(sk_\w+)\s*\(", text)
+
+
+def test_header_declares_expected_api():
+    names = set(header_functions())
+    assert {"sk_abi_version", "sk_last_error", "sk_attn_fwd", "sk_attn_bwd",
+            "sk_attn_bwd_workspace", "sk_decode_plan", "sk_decode", "sk_decode_workspace"} <= names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in sk_attn.h but not exported"
+
+
+def test_abi_version(lib):
+    from stackkernels_amd._core.attention import _lib
+
+    assert lib.sk_abi_version() == _lib.ABI_VERSION
+
+
+def test_single_hip_runtime(lib):
+    from stackkernels_amd._core.attention import _lib
+
+    runtimes = _lib.loaded_hip_runtimes()
+    assert len(runtimes) == 1, runtimes
+    assert "torch" in runtimes[0]
+
+
+def _st(*x):
+    return (ctypes.c_int64 * 3)(*x)
+
+
+def _fwd(lib, **kw):
+    a = dict(dtype=2, q=16, k=16, v=16, o=16, lse=16, B=1, Hq=4, Hkv=2, Sq=8, Sk=8, D=64,
+             qs=_st(2048, 512, 64), ks=_st(1024, 512, 64), vs=_st(1024, 512, 64), os_=_st(2048, 512, 64),
+             causal=0, scale=0.125)
+    a.update(kw)
+    return lib.sk_attn_fwd(a["dtype"], a["q"], a["k"], a["v"], a["o"], a["lse"], a["B"], a["Hq"],
+                           a["Hkv"], a["Sq"], a["Sk"], a["D"], a["qs"], a["ks"], a["vs"], a["os_"],
+                           a["causal"], a["scale"], None)
+
+
+def test_fwd_argument_errors(lib):
+    from stackkernels_amd._core.attention import _lib
+
+    assert _fwd(lib, Hq=3) == _lib.SK_EINVAL
+    assert "divisible" in _lib.last_error()
+    assert _fwd(lib, D=12) == _lib.SK_EUNSUPPORTED
+    assert _fwd(lib, D=264) == _lib.SK_EUNSUPPORTED
+    assert _fwd(lib, dtype=7) == _lib.SK_EUNSUPPORTED
+    assert _fwd(lib, q=17) == _lib.SK_EINVAL and "aligned" in _lib.last_error()
+    assert _fwd(lib, q=None) == _lib.SK_EINVAL
+    assert _fwd(lib, qs=_st(2048, 512, 60)) == _lib.SK_EINVAL and "stride" in _lib.last_error()
+    assert _fwd(lib, B=0) == _lib.SK_OK  # empty: nothing to launch
+
+
+def test_decode_plan_table(lib):
+    ns, nb = ctypes.c_int(), ctypes.c_size_t()
+    # C4: bf16 GQA B=64 Hq=32 Hkv=8 Sk=32768 D=128
+    assert lib.sk_decode_plan(2, 64, 32, 8, 32768, 128, ctypes.byref(ns), ctypes.byref(nb)) == 0
+    assert 1 < ns.value <= 1024
+    assert nb.value == 64 * 32 * ns.value * (128 + 1) * 4
+    # small cache: one split, no scratch
+    assert lib.sk_decode_plan(2, 2, 8, 2, 32, 64, ctypes.byref(ns), ctypes.byref(nb)) == 0
+    assert ns.value == 1 and nb.value == 0
+    # C5: fp16 MQA B=8 Hq=64 Hkv=1 Sk=131072
+    assert lib.sk_decode_plan(1, 8, 64, 1, 131072, 128, ctypes.byref(ns), ctypes.byref(nb)) == 0
+    assert ns.value >= 64
+
+
+def test_decode_argument_errors(lib):
+    from stackkernels_amd._core.attention import _lib
+
+    st = _st(1024, 128, 128)
+    rc = lib.sk_decode(2, 16, 16, 16, 16, None, 0, 4, 1, 8, 2, 100, 128, st, st, st, st, 0.1, None)
+    assert rc == _lib.SK_EWORKSPACE
+    rc = lib.sk_decode(2, 16, 16, 16, 16, None, 0, 2000, 1, 8, 2, 100, 128, st, st, st, st, 0.1, None)
+    assert rc == _lib.SK_EINVAL
+
+
+def test_bwd_workspace(lib):
+    nb = ctypes.c_size_t()
+    assert lib.sk_attn_bwd_workspace(2, 2, 32, 8, 2048, 8192, 128, 1, ctypes.byref(nb)) == 0
+    assert nb.value >= 2 * 2 * 32 * 2048 * 4

@@ -1,0 +1,206 @@
+"""Pin the CPU oracle (oracle/attention_oracle.py) before it is used as the checker.
+
+Each function is checked against something other than its own formula:
+torch SDPA golden vectors (tests/golden), a brute-force loop, finite
+differences, and invariants chosen so that a dropped term, wrong sign, wrong
+mask alignment or wrong GQA mapping fails at least one of them.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from oracle import attention_oracle as orc
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden_attention.npz")
+CASES = ["mha_noncausal", "gqa_causal_prefix", "mqa_causal_square", "gqa_causal_chunked",
+         "decode_mqa", "custom_scale"]
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _case(golden, name):
+    g = {k.split("/", 1)[1]: v for k, v in golden.items() if k.startswith(name + "/")}
+    b, hq, hkv, sq, sk, d, causal = (int(x) for x in g["meta"])
+    return g, bool(causal), float(g["scale"])
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_forward_matches_golden(golden, name):
+    g, causal, scale = _case(golden, name)
+    out, lse = orc.attention_forward(g["q"], g["k"], g["v"], causal, scale)
+    np.testing.assert_allclose(out, g["out"], atol=1e-12, rtol=0)
+    assert np.array_equal(np.isneginf(lse), np.isneginf(g["lse"]))
+    fin = np.isfinite(g["lse"])
+    np.testing.assert_allclose(lse[fin], g["lse"][fin], atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_backward_matches_golden(golden, name):
+    g, causal, scale = _case(golden, name)
+    dq, dk, dv = orc.attention_backward(g["q"], g["k"], g["v"], g["do"], causal, scale)
+    np.testing.assert_allclose(dq, g["dq"], atol=1e-11, rtol=0)
+    np.testing.assert_allclose(dk, g["dk"], atol=1e-11, rtol=0)
+    np.testing.assert_allclose(dv, g["dv"], atol=1e-11, rtol=0)
+
+
+def test_golden_decode_case(golden):
+    g, _, scale = _case(golden, "decode_mqa")
+    np.testing.assert_allclose(orc.decode(g["q"], g["k"], g["v"], scale), g["out"], atol=1e-12)
+
+
+def test_planted_top_left_mask_is_caught(golden):
+    """A plausible slip -- top-left instead of bottom-right causal alignment -- fails golden."""
+    g, _, scale = _case(golden, "gqa_causal_prefix")  # S_q=8 < S_k=24: alignments differ
+    q, k, v = g["q"], g["k"], g["v"]
+    sq, sk = q.shape[2], k.shape[2]
+    kk = orc.repeat_kv(k, q.shape[1] // k.shape[1])
+    vv = orc.repeat_kv(v, q.shape[1] // k.shape[1])
+    s = np.einsum("bhid,bhjd->bhij", q, kk) * scale
+    top_left = np.arange(sk)[None, :] <= np.arange(sq)[:, None]
+    s = np.where(top_left, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    wrong = (p / p.sum(-1, keepdims=True)) @ vv
+    assert np.abs(wrong - g["out"]).max() > 1e-2
+
+
+def _rand(rng, *shape):
+    return rng.standard_normal(shape)
+
+
+@pytest.mark.parametrize("hq,hkv,sq,sk,causal", [
+    (2, 2, 3, 3, False), (2, 1, 3, 5, True), (4, 2, 5, 3, True), (2, 2, 1, 4, True), (3, 1, 4, 4, True),
+])
+def test_forward_matches_loops(hq, hkv, sq, sk, causal):
+    rng = np.random.default_rng(1)
+    q, k, v = _rand(rng, 2, hq, sq, 4), _rand(rng, 2, hkv, sk, 4), _rand(rng, 2, hkv, sk, 4)
+    o1, l1 = orc.attention_forward(q, k, v, causal)
+    o2, l2 = orc.attention_forward_loops(q, k, v, causal)
+    np.testing.assert_allclose(o1, o2, atol=1e-12)
+    np.testing.assert_array_equal(np.isneginf(l1), np.isneginf(l2))
+    np.testing.assert_allclose(l1[np.isfinite(l2)], l2[np.isfinite(l2)], atol=1e-12)
+
+
+@pytest.mark.parametrize("hq,hkv,sq,sk,causal", [(2, 1, 3, 4, True), (2, 2, 4, 2, True), (4, 2, 3, 3, False)])
+def test_backward_matches_finite_differences(hq, hkv, sq, sk, causal):
+    rng = np.random.default_rng(2)
+    d = 3
+    q, k, v = _rand(rng, 1, hq, sq, d), _rand(rng, 1, hkv, sk, d), _rand(rng, 1, hkv, sk, d)
+    do = _rand(rng, 1, hq, sq, d)
+    dq, dk, dv = orc.attention_backward(q, k, v, do, causal)
+
+    def loss(q_, k_, v_):
+        return float((orc.attention_forward(q_, k_, v_, causal)[0] * do).sum())
+
+    eps = 1e-6
+    for arr, grad, idx in ((q, dq, 0), (k, dk, 1), (v, dv, 2)):
+        num = np.zeros_like(arr)
+        it = np.nditer(arr, flags=["multi_index"])
+        for _ in it:
+            mi = it.multi_index
+            args = [q.copy(), k.copy(), v.copy()]
+            args[idx][mi] += eps
+            up = loss(*args)
+            args[idx][mi] -= 2 * eps
+            dn = loss(*args)
+            num[mi] = (up - dn) / (2 * eps)
+        np.testing.assert_allclose(grad, num, atol=1e-6)
+
+
+def test_softmax_rows_sum_to_one():
+    rng = np.random.default_rng(3)
+    p = orc.softmax_probs(_rand(rng, 1, 2, 6, 4), _rand(rng, 1, 2, 9, 4), is_causal=True)
+    np.testing.assert_allclose(p.sum(-1), 1.0, atol=1e-12)
+
+
+def test_gqa_equals_mha_on_repeated_kv_and_grads_sum_per_group():
+    rng = np.random.default_rng(4)
+    q, k, v = _rand(rng, 2, 6, 5, 4), _rand(rng, 2, 2, 7, 4), _rand(rng, 2, 2, 7, 4)
+    do = _rand(rng, 2, 6, 5, 4)
+    kr, vr = np.repeat(k, 3, axis=1), np.repeat(v, 3, axis=1)
+    o_gqa, _ = orc.attention_forward(q, k, v, True)
+    o_mha, _ = orc.attention_forward(q, kr, vr, True)
+    np.testing.assert_allclose(o_gqa, o_mha, atol=1e-12)
+    _, dk_g, dv_g = orc.attention_backward(q, k, v, do, True)
+    _, dk_m, dv_m = orc.attention_backward(q, kr, vr, do, True)
+    np.testing.assert_allclose(dk_g, dk_m.reshape(2, 2, 3, 7, 4).sum(2), atol=1e-12)
+    np.testing.assert_allclose(dv_g, dv_m.reshape(2, 2, 3, 7, 4).sum(2), atol=1e-12)
+    # head h reads KV head h // group (repeat_interleave), not h % H_kv
+    alt = np.tile(k, (1, 3, 1, 1))
+    o_alt, _ = orc.attention_forward(q, alt, np.tile(v, (1, 3, 1, 1)), True)
+    assert np.abs(o_alt - o_gqa).max() > 1e-3
+
+
+def test_causal_row_ignores_hidden_keys():
+    rng = np.random.default_rng(5)
+    q, k, v = _rand(rng, 1, 1, 4, 4), _rand(rng, 1, 1, 6, 4), _rand(rng, 1, 1, 6, 4)
+    o1, _ = orc.attention_forward(q, k, v, True)
+    k2, v2 = k.copy(), v.copy()
+    # row 1 sees keys j <= 1 + 2 = 3; perturb keys 4, 5
+    k2[..., 4:, :] += 10.0
+    v2[..., 4:, :] -= 7.0
+    o2, _ = orc.attention_forward(q, k2, v2, True)
+    np.testing.assert_allclose(o1[..., :2, :], o2[..., :2, :], atol=1e-12)
+    assert np.abs(o1[..., 3, :] - o2[..., 3, :]).max() > 1e-3
+
+
+def test_single_key_gives_v_and_score():
+    rng = np.random.default_rng(6)
+    q, k, v = _rand(rng, 1, 2, 3, 4), _rand(rng, 1, 2, 1, 4), _rand(rng, 1, 2, 1, 4)
+    o, lse = orc.attention_forward(q, k, v, False, 0.7)
+    np.testing.assert_allclose(o, np.broadcast_to(v, o.shape), atol=1e-12)
+    np.testing.assert_allclose(lse, 0.7 * (q * k).sum(-1), atol=1e-12)
+
+
+def test_zero_query_gives_mean_of_visible_values():
+    rng = np.random.default_rng(7)
+    q = np.zeros((1, 1, 3, 4))
+    k, v = _rand(rng, 1, 1, 5, 4), _rand(rng, 1, 1, 5, 4)
+    o, lse = orc.attention_forward(q, k, v, True)
+    for i in range(3):
+        vis = i + 2 + 1  # keys 0 .. i + (5 - 3)
+        np.testing.assert_allclose(o[0, 0, i], v[0, 0, :vis].mean(0), atol=1e-12)
+        np.testing.assert_allclose(lse[0, 0, i], np.log(vis), atol=1e-12)
+
+
+def test_fully_masked_rows():
+    rng = np.random.default_rng(8)
+    q, k, v = _rand(rng, 1, 2, 6, 4), _rand(rng, 1, 1, 2, 4), _rand(rng, 1, 1, 2, 4)
+    do = _rand(rng, 1, 2, 6, 4)
+    o, lse = orc.attention_forward(q, k, v, True)
+    assert np.all(o[:, :, :4] == 0) and np.all(np.isneginf(lse[:, :, :4]))
+    dq, dk, dv = orc.attention_backward(q, k, v, do, True)
+    assert np.all(dq[:, :, :4] == 0)
+    do2 = do.copy()
+    do2[:, :, :4] = 123.0  # gradients flowing into dead rows change nothing
+    _, dk2, dv2 = orc.attention_backward(q, k, v, do2, True)
+    np.testing.assert_allclose(dk, dk2, atol=1e-12)
+    np.testing.assert_allclose(dv, dv2, atol=1e-12)
+
+
+def test_empty_keys():
+    o, lse = orc.attention_forward(np.ones((1, 1, 2, 4)), np.ones((1, 1, 0, 4)), np.ones((1, 1, 0, 4)))
+    assert np.all(o == 0) and np.all(np.isneginf(lse))
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16])
+def test_split_combine_invariant(splits):
+    rng = np.random.default_rng(9)
+    q, k, v = _rand(rng, 2, 4, 1, 8), _rand(rng, 2, 2, 37, 8), _rand(rng, 2, 2, 37, 8)
+    ref, ref_lse = orc.attention_forward(q, k, v, False)
+    o, lse = orc.combine_partials(*orc.split_partials(q, k, v, splits))
+    np.testing.assert_allclose(o, ref, atol=1e-12)
+    np.testing.assert_allclose(lse, ref_lse[..., 0], atol=1e-12)
+
+
+def test_decode_is_noncausal_forward_and_causal_with_one_query():
+    rng = np.random.default_rng(10)
+    q, k, v = _rand(rng, 1, 4, 1, 8), _rand(rng, 1, 2, 9, 8), _rand(rng, 1, 2, 9, 8)
+    o = orc.decode(q, k, v)
+    np.testing.assert_allclose(o, orc.attention_forward(q, k, v, False)[0], atol=1e-12)
+    np.testing.assert_allclose(o, orc.attention_forward(q, k, v, True)[0], atol=1e-12)

@@ -1,0 +1,105 @@
+"""The CPU / reference-backend path against the oracle.
+
+Mirrors the reference's own attention tests (tests/ops/test_flash_attn.py,
+tests/ops/test_flash_decode.py): same grids, seed 42, but checked against the
+float64 oracle instead of against the path itself.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_oracle as orc
+from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
+from stackkernels_amd._reference.torch.attention import attention_reference, repeat_kv
+from stackkernels_amd.torch import FlashAttention, flash_attention, flash_decode
+
+
+def _np(t):
+    return t.detach().double().numpy()
+
+
+@pytest.mark.parametrize("heads", [(8, 8), (8, 2), (8, 1)])
+@pytest.mark.parametrize("seq_lens", [(32, 32), (16, 64), (64, 32)])
+@pytest.mark.parametrize("head_dim", [64, 80, 96, 128, 256])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_forward_grid(heads, seq_lens, head_dim, is_causal):
+    torch.manual_seed(42)
+    hq, hkv = heads
+    sq, sk = seq_lens
+    q = torch.randn(2, hq, sq, head_dim)
+    k = torch.randn(2, hkv, sk, head_dim)
+    v = torch.randn(2, hkv, sk, head_dim)
+    out = flash_attention(q, k, v, is_causal=is_causal)
+    ref, ref_lse = orc.attention_forward(_np(q), _np(k), _np(v), is_causal)
+    np.testing.assert_allclose(_np(out), ref, atol=1e-5, rtol=0)
+    _, lse = attention_reference(q, k, v, is_causal=is_causal)
+    fin = np.isfinite(ref_lse)
+    np.testing.assert_array_equal(np.isneginf(_np(lse)), ~fin)
+    np.testing.assert_allclose(_np(lse)[fin], ref_lse[fin], atol=1e-5)
+
+
+@pytest.mark.parametrize("heads", [(4, 4), (4, 2), (4, 1)])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_backward_grid(heads, is_causal):
+    torch.manual_seed(42)
+    hq, hkv = heads
+    q = torch.randn(2, hq, 16, 64, requires_grad=True)
+    k = torch.randn(2, hkv, 16, 64, requires_grad=True)
+    v = torch.randn(2, hkv, 16, 64, requires_grad=True)
+    out = flash_attention(q, k, v, is_causal=is_causal)
+    g = torch.randn_like(out)
+    out.backward(g)
+    dq, dk, dv = orc.attention_backward(_np(q), _np(k), _np(v), _np(g), is_causal)
+    np.testing.assert_allclose(_np(q.grad), dq, atol=1e-5)
+    np.testing.assert_allclose(_np(k.grad), dk, atol=1e-5)
+    np.testing.assert_allclose(_np(v.grad), dv, atol=1e-5)
+
+
+@pytest.mark.parametrize("heads", [(8, 8), (8, 2), (8, 1)])
+@pytest.mark.parametrize("kv_len", [32, 128, 512, 1024])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_decode_grid(heads, kv_len, head_dim):
+    torch.manual_seed(42)
+    hq, hkv = heads
+    q = torch.randn(2, hq, 1, head_dim)
+    k = torch.randn(2, hkv, kv_len, head_dim)
+    v = torch.randn(2, hkv, kv_len, head_dim)
+    out = flash_decode(q, k, v)
+    np.testing.assert_allclose(_np(out), orc.decode(_np(q), _np(k), _np(v)), atol=1e-5)
+
+
+def test_module_and_custom_op():
+    torch.manual_seed(42)
+    q, k, v = torch.randn(1, 4, 16, 64), torch.randn(1, 2, 16, 64), torch.randn(1, 2, 16, 64)
+    out = FlashAttention(is_causal=True)(q, k, v)
+    assert out.shape == q.shape and not torch.isnan(out).any()
+    op = torch.ops.stackkernels.flash_attn_op(q, k, v, True, None)
+    torch.testing.assert_close(op, out)
+
+
+def test_fully_masked_rows_reference_path():
+    q, k, v = torch.randn(1, 2, 6, 8), torch.randn(1, 1, 2, 8), torch.randn(1, 1, 2, 8)
+    out, lse = attention_reference(q, k, v, is_causal=True)
+    assert torch.all(out[:, :, :4] == 0) and torch.all(torch.isneginf(lse[:, :, :4]))
+
+
+def test_repeat_kv():
+    x = torch.arange(6.0).reshape(1, 2, 3, 1)
+    r = repeat_kv(x, 2)
+    assert r.shape == (1, 4, 3, 1)
+    assert torch.equal(r[:, 0], x[:, 0]) and torch.equal(r[:, 1], x[:, 0]) and torch.equal(r[:, 2], x[:, 1])
+
+
+@pytest.mark.parametrize("shapes,msg", [
+    (((2, 4, 8, 64), (2, 3, 8, 64), (2, 3, 8, 64)), "divisible"),
+    (((2, 4, 8, 64), (1, 4, 8, 64), (1, 4, 8, 64)), "Batch mismatch"),
+    (((2, 4, 8, 64), (2, 4, 8, 32), (2, 4, 8, 32)), "Head dimension mismatch"),
+    (((2, 4, 8, 64), (2, 4, 8, 64), (2, 2, 8, 64)), "K and V head count mismatch"),
+    (((2, 4, 8, 64), (2, 4, 8, 64), (2, 4, 9, 64)), "K and V sequence length mismatch"),
+    (((4, 8, 64), (2, 4, 8, 64), (2, 4, 8, 64)), "Expected 4D"),
+])
+def test_launcher_rejects_bad_layouts(shapes, msg):
+    q, k, v = (torch.zeros(s) for s in shapes)
+    with pytest.raises(ValueError, match=msg):
+        flash_attn_fwd(q, k, v)
