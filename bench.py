@@ -1,0 +1,367 @@
+"""Benchmark of the MI355X attention path (one JSON line on stdout).
+
+Workloads (inputs synthetic, seeded, generated on the device):
+
+* ``fwd``        -- C2, the headline line: flash_attention forward, bf16, causal
+                    MHA, B=4, H=32, S=4096, D=128.  A step is one forward call
+                    (``flash_attn_fwd``: the fwd kernel).  Metric TFLOP/s over the
+                    exact unmasked pair count, 4*D*pairs*B*H.
+* ``fwdbwd``     -- C3: forward + backward, bf16, causal GQA (bottom-right),
+                    B=2, Hq=32, Hkv=8, Sq=2048, Sk=8192, D=128.  14*D*pairs*B*Hq.
+* ``decode``     -- C4: flash_decode, bf16 GQA, B=64, Hq=32, Hkv=8, Sk=32768,
+                    D=128.  GB/s over K+V read once + q read + O written.
+* ``decode_mqa`` -- C5: flash_decode, fp16 MQA, B=8, Hq=64, Hkv=1, Sk=131072,
+                    D=128 (two KV buffer sets alternate so the 256 MB
+                    Infinity Cache cannot hold the working set).
+
+``python bench.py`` runs ``fwd`` as the headline (``value``) and, unless
+``--no-extra``, the other three as entries of ``extra``.  Each line carries a
+``roofline`` object for the dominant kernel (algorithmic work per launch over
+the average launch time measured with HIP events on the launch stream) and a
+``cpu_baseline`` measured on this host with the PyTorch reference path
+(fp32, the reference's own CPU algorithm) on a bounded sample.
+
+One GPU only: ``--gpus N`` with N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "attn fwd/bwd TFLOP/s (% bf16 MFMA peak); flash_decode KV GB/s (% HBM peak)"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+
+
+def causal_pairs(sq: int, sk: int, causal: bool) -> int:
+    """Unmasked (i, j) pairs per (batch, head) under the bottom-right mask."""
+    if not causal:
+        return sq * sk
+    off = sk - sq
+    return sum(max(0, min(sk, i + off + 1)) for i in range(sq))
+
+
+WORKLOADS = {
+    "fwd": dict(name="C2 flash_attention fwd bf16 causal MHA", B=4, Hq=32, Hkv=32, Sq=4096,
+                Sk=4096, D=128, causal=True, dtype="bf16", kind="fwd"),
+    "fwdbwd": dict(name="C3 flash_attention fwd+bwd bf16 causal GQA bottom-right", B=2, Hq=32,
+                   Hkv=8, Sq=2048, Sk=8192, D=128, causal=True, dtype="bf16", kind="fwdbwd"),
+    "decode": dict(name="C4 flash_decode bf16 GQA", B=64, Hq=32, Hkv=8, Sq=1, Sk=32768, D=128,
+                   causal=False, dtype="bf16", kind="decode"),
+    "decode_mqa": dict(name="C5 flash_decode fp16 MQA start_pos=Sk-1", B=8, Hq=64, Hkv=1, Sq=1,
+                       Sk=131072, D=128, causal=False, dtype="fp16", kind="decode"),
+}
+
+
+def work_units(w: dict) -> tuple[float, str]:
+    """Algorithmic work of one step: (FLOP or bytes, unit of the rate)."""
+    if w["kind"] == "decode":
+        esz = 2
+        kv = 2 * w["B"] * w["Hkv"] * w["Sk"] * w["D"] * esz
+        qo = 2 * w["B"] * w["Hq"] * w["D"] * esz
+        return float(kv + qo), "GB/s"
+    pairs = causal_pairs(w["Sq"], w["Sk"], w["causal"])
+    per = 4 if w["kind"] == "fwd" else 14
+    return float(per * w["D"] * pairs * w["B"] * w["Hq"]), "TFLOP/s"
+
+
+def _rate(units: float, unit: str, seconds: float) -> float:
+    return units / seconds / (1e12 if unit == "TFLOP/s" else 1e9)
+
+
+def _make_inputs(w: dict, torch, dev, sets: int = 1):
+    dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float16
+    g = torch.Generator(device=dev).manual_seed(0)
+    out = []
+    for _ in range(sets):
+        q = torch.randn(w["B"], w["Hq"], w["Sq"], w["D"], generator=g, device=dev, dtype=dt)
+        k = torch.randn(w["B"], w["Hkv"], w["Sk"], w["D"], generator=g, device=dev, dtype=dt)
+        if w["name"].startswith("C5"):
+            v = torch.rand(w["B"], w["Hkv"], w["Sk"], w["D"], generator=g, device=dev, dtype=dt)
+            v.mul_(2).sub_(1)
+        else:
+            v = torch.randn(w["B"], w["Hkv"], w["Sk"], w["D"], generator=g, device=dev, dtype=dt)
+        out.append((q, k, v))
+    return out
+
+
+def _abi_launcher(w: dict, inputs, do, torch, dev):
+    """A closure that launches the dominant kernel(s) straight through the C ABI on
+    preallocated buffers (no Python allocation), for per-launch timing."""
+    import ctypes
+
+    from stackkernels_amd._core.attention import _lib
+
+    lib = _lib.load()
+    code = _lib.dtype_code(inputs[0][0].dtype)
+    stream = _lib.stream_ptr(dev)
+    B, Hq, Hkv, Sq, Sk, D = (w[k_] for k_ in ("B", "Hq", "Hkv", "Sq", "Sk", "D"))
+    scale = 1.0 / math.sqrt(D)
+    q0 = inputs[0][0]
+    if w["kind"] == "decode":
+        ns = ctypes.c_int(0)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+                   "plan")
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+        o = torch.empty_like(q0)
+        st = [(_lib.strides3(q), _lib.strides3(k), _lib.strides3(v)) for q, k, v in inputs]
+        so = _lib.strides3(o)
+
+        def launch(i):
+            q, k, v = inputs[i % len(inputs)]
+            sq_, sk_, sv_ = st[i % len(inputs)]
+            rc = lib.sk_decode(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                               ws.data_ptr(), ws.numel(), ns.value, B, Hq, Hkv, Sk, D,
+                               sq_, sk_, sv_, so, scale, stream)
+            _lib.check(rc, "sk_decode")
+        return launch
+    q, k, v = inputs[0]
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=dev)
+    sq_, sk_, sv_, so = (_lib.strides3(t) for t in (q, k, v, o))
+
+    def fwd():
+        rc = lib.sk_attn_fwd(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                             lse.data_ptr(), B, Hq, Hkv, Sq, Sk, D, sq_, sk_, sv_, so,
+                             int(w["causal"]), scale, stream)
+        _lib.check(rc, "sk_attn_fwd")
+    if w["kind"] == "fwd":
+        return lambda i: fwd()
+    nb = ctypes.c_size_t(0)
+    _lib.check(lib.sk_attn_bwd_workspace(code, B, Hq, Hkv, Sq, Sk, D, int(w["causal"]),
+                                         ctypes.byref(nb)), "bwd workspace")
+    ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+    def fwdbwd(i):
+        fwd()
+        rc = lib.sk_attn_bwd(code, do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                             o.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                             dv.data_ptr(), ws.data_ptr(), ws.numel(), B, Hq, Hkv, Sq, Sk, D,
+                             int(w["causal"]), scale, stream)
+        _lib.check(rc, "sk_attn_bwd")
+    return fwdbwd
+
+
+def _time_loop(fn, steps: int, warmup: int, torch, stream):
+    """Run ``fn(i)`` warmup + steps times; return (total ms / steps, sorted per-step ms).
+
+    Each step is bracketed by its own event pair on the launch stream; while the
+    host keeps the queue full, the pair measures exactly that step's kernels."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(steps):
+        evs[i][0].record(stream)
+        fn(i)
+        evs[i][1].record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, sorted(a.elapsed_time(b) for a, b in evs)
+
+
+def run_gpu(w: dict, steps: int, warmup: int):
+    """Time ``steps`` steps of the public API and of the bare C-ABI launches;
+    return (ms per API step, mean ms per C-ABI launch, details)."""
+    import torch
+
+    from stackkernels_amd._core.attention import _lib
+    from stackkernels_amd._core.attention.decode import flash_decode, plan
+    from stackkernels_amd._core.attention.flash_bwd import flash_attn_bwd
+    from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
+
+    dev = torch.device("cuda:0")
+    sets = 2 if w["name"].startswith("C5") else 1
+    inputs = _make_inputs(w, torch, dev, sets)
+    details: dict = {}
+    do = None
+    if w["kind"] == "fwdbwd":
+        g = torch.Generator(device=dev).manual_seed(1)
+        do = torch.randn(inputs[0][0].shape, generator=g, device=dev, dtype=inputs[0][0].dtype)
+
+    if w["kind"] == "decode":
+        q0 = inputs[0][0]
+        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+
+        def step(i):
+            q, k, v = inputs[i % sets]
+            flash_decode(q, k, v)
+    elif w["kind"] == "fwd":
+        def step(i):
+            q, k, v = inputs[0]
+            flash_attn_fwd(q, k, v, is_causal=w["causal"])
+    else:
+        def step(i):
+            q, k, v = inputs[0]
+            o, lse = flash_attn_fwd(q, k, v, is_causal=w["causal"])
+            flash_attn_bwd(do, q, k, v, o, lse, is_causal=w["causal"])
+
+    stream = torch.cuda.current_stream(dev)
+    ms_step, _ = _time_loop(step, steps, warmup, torch, stream)
+    launch = _abi_launcher(w, inputs, do, torch, dev)
+    _, per = _time_loop(launch, steps, warmup, torch, stream)
+    details["launch_ms_median"] = round(per[len(per) // 2], 5)
+    details["launch_ms_min"] = round(per[0], 5)
+    mean = sum(per) / len(per)
+    details["launch_ms_mean"] = round(mean, 5)
+    assert _lib._lib is not None, "native library was not loaded"
+    return ms_step, mean, details
+
+
+def run_cpu_baseline(w: dict, budget_s: float):
+    """The reference's CPU algorithm (fp32 torch, ``attention_reference``) on a bounded
+    sample of the workload: one batch row, KV-head groups in turn, repeated until
+    ``budget_s`` of CPU time has passed.  Returns the cpu_baseline object."""
+    import torch
+
+    from stackkernels_amd._reference.torch.attention import attention_reference
+
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(0)
+    grp = w["Hq"] // w["Hkv"]
+    if w["kind"] == "decode":
+        hkv_chunk = 1
+    else:
+        hkv_chunk = max(1, 4 // grp)  # 4 query heads per chunk bounds the score tensor
+    hq_chunk = hkv_chunk * grp
+    q = torch.randn(1, hq_chunk, w["Sq"], w["D"], generator=g).bfloat16().float()
+    k = torch.randn(1, hkv_chunk, w["Sk"], w["D"], generator=g).bfloat16().float()
+    v = torch.randn(1, hkv_chunk, w["Sk"], w["D"], generator=g).bfloat16().float()
+    do = torch.randn_like(q) if w["kind"] == "fwdbwd" else None
+    done = 0
+    t0 = time.perf_counter()
+    while True:
+        if w["kind"] == "fwdbwd":
+            qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+            out, _ = attention_reference(qr, kr, vr, is_causal=w["causal"])
+            out.backward(do)
+        else:
+            attention_reference(q, k, v, is_causal=w["causal"])
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    units_total, unit = work_units(w)
+    frac = hq_chunk / (w["B"] * w["Hq"])
+    units = units_total * frac * done
+    return {
+        "value": round(_rate(units, unit, el), 6),
+        "unit": unit,
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"attention_reference (fp32 torch restatement of the reference CPU path) on "
+                   f"batch row 0, {hq_chunk} query head(s) / {hkv_chunk} KV head(s) of {w['name']}, "
+                   f"{done} repetition(s) in {el:.1f} s; host {os.cpu_count()} CPUs, "
+                   f"torch threads {threads}"),
+    }
+
+
+def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
+    w = WORKLOADS[key]
+    units, unit = work_units(w)
+    ms_step, ms_kernel, details = run_gpu(w, steps, warmup)
+    value = _rate(units, unit, ms_step / 1e3)
+    achieved = _rate(units, unit, ms_kernel / 1e3)
+    bound = "hbm" if w["kind"] == "decode" else "mfma"
+    peak = PEAK_HBM_GBPS if bound == "hbm" else PEAK_BF16_TFLOPS
+    kernel = {"fwd": "fwd_mfma_kernel", "fwdbwd": "fwd + bwd kernels",
+              "decode": "decode_split_kernel + decode_combine_kernel"}[w["kind"]]
+    res = {
+        "workload": key,
+        "config": {k_: w[k_] for k_ in ("name", "B", "Hq", "Hkv", "Sq", "Sk", "D", "causal", "dtype")},
+        "value": round(value, 3),
+        "unit": unit,
+        "ms_per_step": round(ms_step, 5),
+        "roofline": {
+            "bound": bound,
+            "kernel": kernel,
+            "achieved": round(achieved, 3),
+            "peak": peak,
+            "unit": unit,
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "work_per_launch": units,
+        },
+        "details": details,
+    }
+    if cpu_s > 0:
+        res["cpu_baseline"] = run_cpu_baseline(w, cpu_s)
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="fwd",
+                    help="headline workload (default fwd = C2)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU-baseline budget per workload (0 disables)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path is "
+              "built and measured on a single MI355X in this build.", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    head = measure(args.workload, args.steps, args.warmup, args.cpu_seconds)
+    extra = []
+    if not args.no_extra:
+        for key in WORKLOADS:
+            if key == args.workload:
+                continue
+            try:
+                extra.append(measure(key, args.steps, args.warmup, args.cpu_seconds))
+                print(f"# {key}: {extra[-1]['value']} {extra[-1]['unit']}", file=sys.stderr,
+                      flush=True)
+            except (RuntimeError, NotImplementedError) as e:
+                extra.append({"workload": key, "error": str(e)[:300]})
+                print(f"# {key}: failed: {e}", file=sys.stderr, flush=True)
+    w = WORKLOADS[args.workload]
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w["dtype"],
+        "data": "synthetic (seeded N(0,1) on device; C5 V ~ U(-1,1))",
+        "config": {"workload": w["name"], "B": w["B"], "Hq": w["Hq"], "Hkv": w["Hkv"],
+                   "Sq": w["Sq"], "Sk": w["Sk"], "D": w["D"], "causal": w["causal"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "details": head["details"],
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

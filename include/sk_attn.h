@@ -73,8 +73,9 @@ SK_API int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, v
                 int is_causal, float sm_scale, void* stream);
 
 /*
- * Bytes of scratch sk_attn_bwd needs for these dims (row statistics and the
- * fp32 dQ accumulator).  Replaces allocate_delta_buffer
+ * Bytes of scratch sk_attn_bwd needs for these dims (two fp32 row statistics
+ * per query row: delta = rowsum(dO * O) and lse * log2(e)).  Replaces
+ * allocate_delta_buffer
  * (reference: src/stackkernels/_opt/memory/workspace.py:16-23).
  */
 SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
