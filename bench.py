@@ -305,13 +305,32 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
     return res
 
 
+def copy_calibration(steps: int, warmup: int) -> dict:
+    """Time ``y.copy_(x)`` on a 1 GiB buffer: 1 GiB read + 1 GiB written per launch.
+
+    Its FETCH_SIZE / WRITE_SIZE counters give the factor that turns those
+    counters into HBM bytes for the attention kernels."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = 1 << 30
+    x = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream(dev)
+    _, per = _time_loop(lambda i: y.copy_(x), steps, warmup, torch, stream)
+    mean = sum(per) / len(per)
+    return {"workload": "copy", "bytes_read": n, "bytes_written": n, "ms_mean": round(mean, 5),
+            "GB/s": round(2 * n / mean / 1e6, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="fwd",
-                    help="headline workload (default fwd = C2)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["copy"], default="fwd",
+                    help="headline workload (default fwd = C2); 'copy' times a plain 1 GiB "
+                         "device copy, the calibration kernel for the HBM-traffic counters")
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload (0 disables)")
@@ -325,6 +344,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.workload == "copy":
+        print(json.dumps(copy_calibration(args.steps, args.warmup)), flush=True)
+        return 0
     head = measure(args.workload, args.steps, args.warmup, args.cpu_seconds)
     extra = []
     if not args.no_extra:

@@ -100,6 +100,23 @@ __device__ __forceinline__ float to_f32<F16>(uint16_t x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Online-softmax rescale threshold in log2 units: the running exponent offset
+// is raised only when a score exceeds it by more than this, so unnormalised
+// probabilities stay <= 2^8 (exact in bf16/fp16 range, no fp32 overflow).
+constexpr float kRescaleLog2 = 8.0f;
+
+// Work-item index for XCD-aware scheduling.  gfx950 dispatches workgroup i to
+// XCD i % 8 (8 XCDs, each with its own L2); this maps the n workgroups so that
+// XCD x processes the contiguous item range [start(x), start(x) + count(x)).
+constexpr int kNumXcd = 8;
+__device__ __forceinline__ int xcd_work_index(int bid, int n) {
+  const int xcd = bid % kNumXcd;
+  const int r = bid / kNumXcd;
+  const int per = n / kNumXcd;
+  const int rem = n % kNumXcd;
+  return xcd * per + min(xcd, rem) + r;
+}
+
 // max / sum of a value across lanes l and l^32 of a wave64.
 __device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32); }
@@ -112,6 +129,28 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
 
 __device__ __forceinline__ u32x4 lds_read_b128(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Raw buffer loads (gfx9 resource word 3 = 0x00020000: 32-bit untyped data).
+// A load whose byte offset is not below the resource's num_records returns
+// zero; kBufferOob is an offset that is out of range for every resource used
+// here (all tiles are far smaller than 2 GiB).
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+constexpr uint32_t kBufferOob = 0x80000000u;
+
+__device__ __forceinline__ buf_rsrc make_rsrc(const void* base, int num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_bytes,
+                                           0x00020000);
+}
+
+// Bytes a resource must cover for `rows` rows of `d` elements at row stride
+// `stride` elements (16-bit data): through the end of the last row's data.
+__device__ __forceinline__ int tile_bytes(int rows, int64_t stride, int d) {
+  return rows > 0 ? (int)(((int64_t)(rows - 1) * stride + d) * 2) : 0;
+}
+
+__device__ __forceinline__ u32x4 buffer_load_b128(buf_rsrc r, uint32_t offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
 }
 
 __device__ __forceinline__ u32x4 ldg_b128(const uint16_t* p) {

@@ -22,19 +22,31 @@
 //   tiles that straddle the diagonal or the end of the keys; tiles a wave
 //   cannot see are skipped.  Rows that see no key end with O = 0 and
 //   LSE = -inf, as the reference path does (_reference/torch/attention.py:70-73).
-// * Workgroups are issued heaviest-first (highest query block first) so the
-//   causal triangle's long rows do not trail at the end of the grid.
+// * Online-softmax rescaling is lazy: the exponent offset moves only when a
+//   tile's maximum exceeds it by more than 2^8, so the O rescale (DP/2
+//   multiplies per lane) runs on a handful of tiles per row block.
+// * XCD-aware order: each of the 8 XCDs walks a contiguous range of
+//   (head, query block) items, head-major, heaviest query block first, so
+//   the heads an XCD has in flight share its L2 and the causal triangle's
+//   long rows do not trail at the end of the grid.
 #include "sk_common.h"
 #include "sk_kernels.h"
 
 namespace sk {
 
+// LDS tile geometry.  K rows are padded by 8 words (an odd multiple of 4
+// banks), so the 16-byte row reads of 8 consecutive lanes hit 8 disjoint bank
+// quads; V rows by 16 words (8 banks), so the four 32-byte row segments a
+// 16-lane ds_read_b64_tr_b16 group touches are disjoint.
 template <int DP, int BN>
 struct FwdTile {
-  static constexpr int kStride = DP + 16;             // 16-bit words per LDS row
-  static constexpr int kWords = BN * kStride;         // one K or V tile
-  static constexpr int kChunksPerRow = DP / 8;        // 16-byte chunks per row
-  static constexpr int kChunks = BN * kChunksPerRow;  // chunks per tile
+  static constexpr int kKStride = DP + 8;              // 16-bit words per K row
+  static constexpr int kVStride = DP + 16;             // 16-bit words per V row
+  static constexpr int kKWords = BN * kKStride;
+  static constexpr int kVWords = BN * kVStride;
+  static constexpr int kBufWords = kKWords + kVWords;  // one K + V stage
+  static constexpr int kChunksPerRow = DP / 8;         // 16-byte chunks per row
+  static constexpr int kChunks = BN * kChunksPerRow;   // chunks per tile
 };
 
 template <class T, int DP, int BN, int NW, bool CAUSAL>
@@ -49,7 +61,7 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
   constexpr int DB = DP / 32;  // 32-wide head-dim blocks of O^T
   constexpr int KN = BN / 16;  // k-steps over keys for O^T
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * 2 * Tile::kWords];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * Tile::kBufWords];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -57,10 +69,13 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
-  const int bh_count = p.B * p.Hq;
-  const int bid = blockIdx.x;
-  const int mblk = p.n_mblocks - 1 - bid / bh_count;
-  const int bh = bid % bh_count;
+  // Work order.  The dispatcher hands workgroup i to XCD i % 8; remap so each
+  // XCD walks a contiguous run of (head, query block) items, head-major and
+  // heaviest query block first, which keeps the one or two heads it has in
+  // flight resident in that XCD's L2.
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int bh = w / p.n_mblocks;
+  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
   const int b = bh / p.Hq;
   const int hq = bh % p.Hq;
   const int hkv = hq / p.group;
@@ -88,34 +103,40 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
     qreg[s] = x;
   }
 
+  // K/V tiles arrive by buffer loads: a per-tile resource covers the tile's
+  // valid rows, so rows past S_k (and head-dim padding, via an out-of-range
+  // offset) read as zero in hardware, with no branches or 64-bit address math.
   u32x4 kreg[LOADS], vreg[LOADS];
+  uint32_t koff[LOADS], voff[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int c = tid + i * NT;
+    const int r = c / Tile::kChunksPerRow;
+    const int d = (c % Tile::kChunksPerRow) * 8;
+    koff[i] = d < p.D ? (uint32_t)((r * p.k_ss + d) * 2) : kBufferOob;
+    voff[i] = d < p.D ? (uint32_t)((r * p.v_ss + d) * 2) : kBufferOob;
+  }
   auto load_tile = [&](int t) {
     const int n0 = t * BN;
+    const int rows = min(BN, p.Sk - n0);
+    const buf_rsrc kr = make_rsrc(kbase + (int64_t)n0 * p.k_ss, tile_bytes(rows, p.k_ss, p.D));
+    const buf_rsrc vr = make_rsrc(vbase + (int64_t)n0 * p.v_ss, tile_bytes(rows, p.v_ss, p.D));
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * NT;
-      const int r = c / Tile::kChunksPerRow;
-      const int d = (c % Tile::kChunksPerRow) * 8;
-      const int n = n0 + r;
-      u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
-      if (n < p.Sk && d < p.D) {
-        kx = ldg_b128_cached(kbase + (int64_t)n * p.k_ss + d);
-        vx = ldg_b128_cached(vbase + (int64_t)n * p.v_ss + d);
-      }
-      kreg[i] = kx;
-      vreg[i] = vx;
+      kreg[i] = buffer_load_b128(kr, koff[i]);
+      vreg[i] = buffer_load_b128(vr, voff[i]);
     }
   };
   auto store_tile = [&](int buf) {
-    uint16_t* ks = smem + buf * 2 * Tile::kWords;
-    uint16_t* vs = ks + Tile::kWords;
+    uint16_t* ks = smem + buf * Tile::kBufWords;
+    uint16_t* vs = ks + Tile::kKWords;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int c = tid + i * NT;
       const int r = c / Tile::kChunksPerRow;
       const int d = (c % Tile::kChunksPerRow) * 8;
-      *reinterpret_cast<u32x4*>(ks + r * Tile::kStride + d) = kreg[i];
-      *reinterpret_cast<u32x4*>(vs + r * Tile::kStride + d) = vreg[i];
+      *reinterpret_cast<u32x4*>(ks + r * Tile::kKStride + d) = kreg[i];
+      *reinterpret_cast<u32x4*>(vs + r * Tile::kVStride + d) = vreg[i];
     }
   };
 
@@ -132,16 +153,16 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
   __syncthreads();
 
   // Lane-constant parts of the LDS addresses.
-  const int k_off = l32 * Tile::kStride + 8 * hl;  // K row l32, column 8*hl
+  const int k_off = l32 * Tile::kKStride + 8 * hl;  // K row l32, column 8*hl
   const int j16 = lane & 15;
-  const int v_off = (4 * hl + j16 / 4) * Tile::kStride + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+  const int v_off = (4 * hl + j16 / 4) * Tile::kVStride + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
   const bool wave_has_rows = mw < p.Sq;
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < n_tiles) load_tile(t + 1);
-    const uint16_t* ks = smem + buf * 2 * Tile::kWords;
-    const uint16_t* vs = ks + Tile::kWords;
+    const uint16_t* ks = smem + buf * Tile::kBufWords;
+    const uint16_t* vs = ks + Tile::kKWords;
     const int n0 = t * BN;
 
     bool active = wave_has_rows;
@@ -153,7 +174,7 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
         sacc[kb] = f32x16{};
 #pragma unroll
         for (int s = 0; s < KD; ++s) {
-          const u32x4 a = lds_read_b128(ks + k_off + kb * 32 * Tile::kStride + 16 * s);
+          const u32x4 a = lds_read_b128(ks + k_off + kb * 32 * Tile::kKStride + 16 * s);
           sacc[kb] = mfma32<T>(a, qreg[s], sacc[kb]);
         }
       }
@@ -178,11 +199,20 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
       mt = xhalf_max(mt);
-      const float m_new = fmaxf(m_run, mt);
-      const float m_sub = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = fast_exp2((m_run - m_sub) * p.scale_log2);
-      const float neg_m = -m_sub * p.scale_log2;
-      m_run = m_new;
+      // Lazy rescaling: the exponent offset m_run only moves when a score
+      // exceeds it by more than kRescaleLog2 (in log2 units), so P <= 2^8
+      // and the O / l rescale runs on a few tiles instead of every tile.
+      const bool grow = (mt - m_run) * p.scale_log2 > kRescaleLog2;
+      if (__any(grow)) {
+        // Lanes that do not grow keep alpha = 1 (their offset may still be
+        // -inf on a row that has seen no key yet).
+        const float alpha = grow ? fast_exp2((m_run - mt) * p.scale_log2) : 1.f;
+        m_run = grow ? mt : m_run;
+        l_run *= alpha;
+#pragma unroll
+        for (int c = 0; c < DB; ++c) oacc[c] *= alpha;
+      }
+      const float neg_m = (m_run == kNegInf) ? 0.f : -m_run * p.scale_log2;
 
       float psum = 0.f;
       u32x4 pk[KN];
@@ -199,17 +229,15 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
         pk[s2] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
                        pack2<T>(e[6], e[7])};
       }
-      l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int c = 0; c < DB; ++c) oacc[c] *= alpha;
+      l_run += psum;
 
 #pragma unroll
       for (int c = 0; c < DB; ++c) {
 #pragma unroll
         for (int s2 = 0; s2 < KN; ++s2) {
-          const uint16_t* vp = vs + v_off + 16 * s2 * Tile::kStride + 32 * c;
+          const uint16_t* vp = vs + v_off + 16 * s2 * Tile::kVStride + 32 * c;
           const u32x2 lo = lds_read_tr(vp);
-          const u32x2 hi = lds_read_tr(vp + 8 * Tile::kStride);
+          const u32x2 hi = lds_read_tr(vp + 8 * Tile::kVStride);
           const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
           oacc[c] = mfma32<T>(a, pk[s2], oacc[c]);
         }
