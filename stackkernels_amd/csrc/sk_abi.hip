@@ -136,10 +136,15 @@ int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
   p.scale = std::fabs(sm_scale);
   p.scale_log2 = p.scale * 1.4426950408889634f;
   const bool neg = sm_scale < 0.f;
-  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, sk::padded_head_dim(D));
+  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D);
   p.n_mblocks = (Sq + rows - 1) / rows;
   if ((int64_t)p.n_mblocks * B * Hq > 0x7fffffffLL)
     return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p.n_mblocks * B * Hq);
+  // Causal: pair query block j with n_mblocks-1-j in one workgroup when that
+  // still leaves at least two workgroups per CU (256 CUs).
+  p.pair_items = dtype != SK_F32 && is_causal && p.n_mblocks >= 2 &&
+                 (int64_t)((p.n_mblocks + 1) / 2) * B * Hq >= 512;
+  p.n_items = p.pair_items ? (p.n_mblocks + 1) / 2 : p.n_mblocks;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == SK_F32) {

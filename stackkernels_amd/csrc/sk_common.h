@@ -117,9 +117,19 @@ __device__ __forceinline__ int xcd_work_index(int bid, int n) {
   return xcd * per + min(xcd, rem) + r;
 }
 
-// max / sum of a value across lanes l and l^32 of a wave64.
-__device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
-__device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32); }
+// max / sum of a value across lanes l and l^32 of a wave64.  v_permlane32_swap
+// with both operands x leaves, in every lane l, x[l % 32] in one result and
+// x[l % 32 + 32] in the other (a VALU op, no LDS round trip).
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
 
 // Transposed 4 x 16 read from a row-major LDS tile (see header comment).
 __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
@@ -151,6 +161,45 @@ __device__ __forceinline__ int tile_bytes(int rows, int64_t stride, int d) {
 
 __device__ __forceinline__ u32x4 buffer_load_b128(buf_rsrc r, uint32_t offset) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
+}
+
+// Buffer resource as four SGPR words, for inline asm operands.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, int num_bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), num_bytes, 0x00020000};
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane i writes
+// lds_wave_base + 16 * i (lds_wave_base must be wave-uniform).  Out-of-range
+// lanes write zeros.  Completion is counted by vmcnt, and the caller owns the
+// wait: issued as inline asm so the compiler does not add its own
+// conservative vmcnt(0) before every later LDS read (its alias tracking of
+// LDS DMA cannot tell the ring's stages apart).  s_nop covers the M0-write
+// to LDS-DMA hazard.
+__device__ __forceinline__ void buffer_load_lds_b128(i32x4 rsrc, uint32_t lds_wave_base,
+                                                     uint32_t offset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds_wave_base), "v"(offset), "s"(rsrc)
+      : "memory", "m0");
+}
+
+// s_waitcnt with vmcnt <= N and the other counters left open (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 __device__ __forceinline__ u32x4 ldg_b128(const uint16_t* p) {

@@ -4,27 +4,36 @@
 // (src/stackkernels/_core/attention/flash_fwd.py:15-179); same math, a
 // gfx950-first organisation:
 //
-// * A workgroup owns BM = 32*NW query rows of one (batch, query head); each
-//   wave owns 32 of them.  Key/value tiles of BN rows stream through LDS,
-//   double-buffered, loaded by coalesced 16-byte global reads.
+// * A workgroup of NW waves owns BM = 32*NW query rows of one (batch, query
+//   head); each wave owns 32 of them, with its Q rows held in registers.
+//   At D <= 128 a workgroup is 8 waves (two per SIMD) and fills a CU alone.
+// * K/V tiles of BN keys stream through a STAGES-deep ring of LDS stages,
+//   written by buffer_load ... lds (direct to LDS, no register staging).
+//   Each wave issues whole 1 KiB segments; rows past S_k and head-dim
+//   padding come back as zeros from the buffer range check.  One barrier per
+//   tile; loads run STAGES-1 tiles ahead of the math.
+// * LDS tiles are unpadded with a 16-byte-chunk XOR swizzle: chunk c of row r
+//   sits at c ^ (r % 16) in K tiles (the 16-byte row reads of 16 consecutive
+//   rows hit disjoint bank quads) and at c ^ 4 (r % 4) in V tiles (the four
+//   rows x four chunks a 32-lane ds_read_b64_tr_b16 group touches hit
+//   disjoint banks).
 // * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16:
 //   every lane then holds one query column (its l%32) and 16 keys per 32-key
-//   block, so the softmax row max needs one cross-half swap
-//   (v_permlane32_swap) per tile and the row sum none until the end.
+//   block, so the softmax row max needs one v_permlane32_swap per tile and
+//   the row sum none until the end.
 // * The output is accumulated transposed as well, O^T += V^T P^T.  The P^T
 //   operand comes straight from the score registers (the contraction order
 //   over keys is permuted consistently on both sides), and V^T is read from
 //   the row-major V tile with ds_read_b64_tr_b16.
 // * Online softmax in base 2 with |sm_scale|*log2(e) folded into one FMA per
 //   score; a negative sm_scale is applied by negating q's sign bits.
+//   Rescaling is lazy: the exponent offset moves only when a tile's maximum
+//   exceeds it by more than 2^8, so the O rescale runs on a few tiles.
 // * Bottom-right causal masking (key j visible to query i iff
 //   j <= i + Sk - Sq, reference flash_fwd.py:122-128) is applied only on the
 //   tiles that straddle the diagonal or the end of the keys; tiles a wave
 //   cannot see are skipped.  Rows that see no key end with O = 0 and
 //   LSE = -inf, as the reference path does (_reference/torch/attention.py:70-73).
-// * Online-softmax rescaling is lazy: the exponent offset moves only when a
-//   tile's maximum exceeds it by more than 2^8, so the O rescale (DP/2
-//   multiplies per lane) runs on a handful of tiles per row block.
 // * XCD-aware order: each of the 8 XCDs walks a contiguous range of
 //   (head, query block) items, head-major, heaviest query block first, so
 //   the heads an XCD has in flight share its L2 and the causal triangle's
@@ -34,111 +43,129 @@
 
 namespace sk {
 
-// LDS tile geometry.  K rows are padded by 8 words (an odd multiple of 4
-// banks), so the 16-byte row reads of 8 consecutive lanes hit 8 disjoint bank
-// quads; V rows by 16 words (8 banks), so the four 32-byte row segments a
-// 16-lane ds_read_b64_tr_b16 group touches are disjoint.
+// Geometry of one K or V tile in LDS: BN rows of DP 16-bit words, unpadded.
 template <int DP, int BN>
-struct FwdTile {
-  static constexpr int kKStride = DP + 8;              // 16-bit words per K row
-  static constexpr int kVStride = DP + 16;             // 16-bit words per V row
-  static constexpr int kKWords = BN * kKStride;
-  static constexpr int kVWords = BN * kVStride;
-  static constexpr int kBufWords = kKWords + kVWords;  // one K + V stage
-  static constexpr int kChunksPerRow = DP / 8;         // 16-byte chunks per row
-  static constexpr int kChunks = BN * kChunksPerRow;   // chunks per tile
+struct FwdLds {
+  static constexpr int kCpr = DP / 8;                     // 16-byte chunks per row
+  static constexpr int kRowBytes = DP * 2;
+  static constexpr int kTileBytes = BN * kRowBytes;
+  static constexpr int kStageBytes = 2 * kTileBytes;      // K tile, then V tile
+  static constexpr int kSegRows = 1024 / kRowBytes;       // rows per 1 KiB segment
+  static constexpr int kSegs = kTileBytes / 1024;         // segments per tile
 };
 
-template <class T, int DP, int BN, int NW, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(FwdParams p) {
-  using Tile = FwdTile<DP, BN>;
+// Chunk swizzles (XOR on the 16-byte chunk index of a row) for the 64-bank
+// LDS, which serves a 16-byte read for 16 lanes and an 8-byte read for 32
+// lanes per cycle.  K: the 16 rows of a 16-lane ds_read_b128 group (same
+// logical chunk) land on 16 distinct bank quads.  V: the 4 rows x 4 chunks a
+// 32-lane ds_read_b64_tr_b16 group touches land on 16 distinct bank quads.
+// (128-byte rows, D = 64, alternate bank halves, hence the r/2 terms.)
+template <int DP>
+__device__ __forceinline__ int swz_k(int r) {
+  return DP == 64 ? (r >> 1) & 7 : r & 15;
+}
+template <int DP>
+__device__ __forceinline__ int swz_v(int r) {
+  return DP == 64 ? 4 * ((r >> 1) & 1) : 4 * (r & 3);
+}
+
+template <class T, int DP, int BN, int NW, int STAGES, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
+  using L = FwdLds<DP, BN>;
   constexpr int BM = 32 * NW;
-  constexpr int NT = NW * 64;
-  constexpr int LOADS = Tile::kChunks / NT;
-  static_assert(Tile::kChunks % NT == 0, "tile chunks must divide over the workgroup");
   constexpr int KD = DP / 16;  // k-steps over the head dim for S^T
   constexpr int KB = BN / 32;  // 32-key blocks per tile
   constexpr int DB = DP / 32;  // 32-wide head-dim blocks of O^T
   constexpr int KN = BN / 16;  // k-steps over keys for O^T
+  constexpr int LK = L::kSegs / NW;  // K (and V) segments each wave loads per tile
+  static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
+  static_assert(STAGES >= 3 && STAGES <= 4, "3 or 4 stages");
+  static_assert(STAGES - 2 <= 2, "the vmcnt wait covers up to 2 tiles ahead");
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * Tile::kBufWords];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * L::kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
-  // Work order.  The dispatcher hands workgroup i to XCD i % 8; remap so each
-  // XCD walks a contiguous run of (head, query block) items, head-major and
-  // heaviest query block first, which keeps the one or two heads it has in
-  // flight resident in that XCD's L2.
+  // Work item: a (batch, head) and either one query block or, when the host
+  // pairs them (causal), blocks j and n_mblocks-1-j run back to back, so every
+  // workgroup carries the same causal work and the per-item fixed cost is
+  // paid half as often.
   const int w = xcd_work_index(blockIdx.x, gridDim.x);
-  const int bh = w / p.n_mblocks;
-  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
+  const int bh = w / p.n_items;
+  const int item = w - bh * p.n_items;
   const int b = bh / p.Hq;
   const int hq = bh % p.Hq;
   const int hkv = hq / p.group;
-  const int m0 = mblk * BM;
-  const int mw = m0 + wave * 32;
-  const int row = mw + l32;
   const int diag = p.Sk - p.Sq;  // causal offset
 
-  const uint16_t* qb = (const uint16_t*)p.q + b * p.q_sb + hq * p.q_sh;
   const uint16_t* kbase = (const uint16_t*)p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = (const uint16_t*)p.v + b * p.v_sb + hkv * p.v_sh;
 
+  // Per-lane global byte offsets of the chunks this lane loads (tile-relative).
+  uint32_t koff[LK], voff[LK];
+#pragma unroll
+  for (int j = 0; j < LK; ++j) {
+    const int seg = wave + j * NW;
+    const int r = seg * L::kSegRows + lane / L::kCpr;
+    const int pc = lane % L::kCpr;
+    const int kc = pc ^ swz_k<DP>(r);
+    const int vc = pc ^ swz_v<DP>(r);
+    koff[j] = kc * 8 < p.D ? (uint32_t)((r * p.k_ss + kc * 8) * 2) : kBufferOob;
+    voff[j] = vc * 8 < p.D ? (uint32_t)((r * p.v_ss + vc * 8) * 2) : kBufferOob;
+  }
+  auto issue_tile = [&](int t) {
+    const int n0 = t * BN;
+    const int rows = min(BN, p.Sk - n0);
+    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.k_ss, tile_bytes(rows, p.k_ss, p.D));
+    const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.v_ss, tile_bytes(rows, p.v_ss, p.D));
+    const uint32_t st = lds_addr(smem) + (t % STAGES) * L::kStageBytes;
+#pragma unroll
+    for (int j = 0; j < LK; ++j) {
+      const int seg = wave + j * NW;
+      buffer_load_lds_b128(kr, st + seg * 1024, koff[j]);
+      buffer_load_lds_b128(vr, st + L::kTileBytes + seg * 1024, voff[j]);
+    }
+  };
+
+  auto run_item = [&](int mblk) {
+  const int m0 = mblk * BM;
+  const int mw = m0 + wave * 32;
+  const int row = mw + l32;
   int n_end = p.Sk;
   if (CAUSAL) n_end = min(p.Sk, m0 + BM + diag);
   const int n_tiles = n_end > 0 ? (n_end + BN - 1) / BN : 0;
 
-  // Q^T operand: lane holds q[row][16*s + 8*hl .. +7].
+  // Q^T operand: lane holds q[row][16*s + 8*hl .. +7] (zero past S_q and D).
   u32x4 qreg[KD];
+  {
+    const int qrows = max(0, min(32, p.Sq - mw));
+    const buf_rsrc qr = make_rsrc((const uint16_t*)p.q + b * p.q_sb + hq * p.q_sh +
+                                      (int64_t)min(mw, p.Sq) * p.q_ss,
+                                  tile_bytes(qrows, p.q_ss, p.D));
 #pragma unroll
-  for (int s = 0; s < KD; ++s) {
-    const int d0 = 16 * s + 8 * hl;
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (row < p.Sq && d0 < p.D) x = ldg_b128_cached(qb + (int64_t)row * p.q_ss + d0);
-    x ^= p.q_sign;
-    qreg[s] = x;
+    for (int s = 0; s < KD; ++s) {
+      const int d0 = 16 * s + 8 * hl;
+      const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.q_ss + d0) * 2) : kBufferOob;
+      qreg[s] = buffer_load_b128(qr, off) ^ p.q_sign;
+    }
   }
 
-  // K/V tiles arrive by buffer loads: a per-tile resource covers the tile's
-  // valid rows, so rows past S_k (and head-dim padding, via an out-of-range
-  // offset) read as zero in hardware, with no branches or 64-bit address math.
-  u32x4 kreg[LOADS], vreg[LOADS];
-  uint32_t koff[LOADS], voff[LOADS];
+  // Software pipeline, per wave: in iteration t the MFMAs of S(t+1) = K(t+1) Q^T
+  // are interleaved with the exp / pack / row-sum VALU work of the softmax of
+  // tile t, then O += V(t) P(t) runs.  The MFMA unit runs asynchronously to
+  // the VALU, so the softmax hides in the shadow of the next tile's score
+  // MFMAs (a scheduling-group pattern fixes the interleave).  Tiles t and
+  // t+1 are read in iteration t, so loads run PD = STAGES - 2 tiles ahead.
+  constexpr int PD = STAGES - 2;
+  static_assert(PD >= 1, "prefetch distance");
+
 #pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int c = tid + i * NT;
-    const int r = c / Tile::kChunksPerRow;
-    const int d = (c % Tile::kChunksPerRow) * 8;
-    koff[i] = d < p.D ? (uint32_t)((r * p.k_ss + d) * 2) : kBufferOob;
-    voff[i] = d < p.D ? (uint32_t)((r * p.v_ss + d) * 2) : kBufferOob;
-  }
-  auto load_tile = [&](int t) {
-    const int n0 = t * BN;
-    const int rows = min(BN, p.Sk - n0);
-    const buf_rsrc kr = make_rsrc(kbase + (int64_t)n0 * p.k_ss, tile_bytes(rows, p.k_ss, p.D));
-    const buf_rsrc vr = make_rsrc(vbase + (int64_t)n0 * p.v_ss, tile_bytes(rows, p.v_ss, p.D));
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      kreg[i] = buffer_load_b128(kr, koff[i]);
-      vreg[i] = buffer_load_b128(vr, voff[i]);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* ks = smem + buf * Tile::kBufWords;
-    uint16_t* vs = ks + Tile::kKWords;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * NT;
-      const int r = c / Tile::kChunksPerRow;
-      const int d = (c % Tile::kChunksPerRow) * 8;
-      *reinterpret_cast<u32x4*>(ks + r * Tile::kKStride + d) = kreg[i];
-      *reinterpret_cast<u32x4*>(vs + r * Tile::kVStride + d) = vreg[i];
-    }
-  };
+  for (int t = 0; t <= PD; ++t)
+    if (t < n_tiles) issue_tile(t);
 
   f32x16 oacc[DB];
 #pragma unroll
@@ -146,106 +173,229 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
   float m_run = kNegInf;
   float l_run = 0.f;
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
+  // Lane-constant LDS byte offsets.  K operand of k-step s: row l32 (+32 kb),
+  // chunk 2s + hl.  V^T operand of head-dim block c: rows 4*hl + j16/4 (+16 s2,
+  // +8 for the upper half, neither of which changes the row's swizzle), chunk
+  // 4c + 2*((lane/16)%2) + (j16%4)/2, and the 8-byte half (j16%2) of that chunk.
+  int k_lds[KD], v_lds[DB];
+#pragma unroll
+  for (int s = 0; s < KD; ++s) k_lds[s] = l32 * L::kRowBytes + (((2 * s + hl) ^ swz_k<DP>(l32)) * 16);
+  {
+    const int j16 = lane & 15;
+    const int vr = 4 * hl + j16 / 4;
+    const int g = 2 * ((lane >> 4) & 1) + (j16 & 3) / 2;
+#pragma unroll
+    for (int c = 0; c < DB; ++c)
+      v_lds[c] = L::kTileBytes + vr * L::kRowBytes + (((4 * c + g) ^ swz_v<DP>(vr)) * 16) +
+                 8 * (j16 & 1);
   }
-  __syncthreads();
-
-  // Lane-constant parts of the LDS addresses.
-  const int k_off = l32 * Tile::kKStride + 8 * hl;  // K row l32, column 8*hl
-  const int j16 = lane & 15;
-  const int v_off = (4 * hl + j16 / 4) * Tile::kVStride + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
   const bool wave_has_rows = mw < p.Sq;
+  auto active = [&](int t) {
+    return t < n_tiles && wave_has_rows && (!CAUSAL || t * BN <= mw + 31 + diag);
+  };
+  auto stage = [&](int t) { return smem + (t % STAGES) * L::kStageBytes; };
+  // Tile t landed for this wave (vmcnt, with up to max_ahead later tiles still
+  // in flight), then for all (barrier); the barrier also retires every wave's
+  // reads of the stage the next issue refills.
+  auto sync_tile = [&](int t, int max_ahead) {
+    const int ahead = min(max_ahead, n_tiles - 1 - t);  // tiles issued after t
+    if (ahead >= 2)
+      wait_vmcnt<2 * 2 * LK>();
+    else if (ahead == 1)
+      wait_vmcnt<2 * LK>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+  };
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
-    const uint16_t* ks = smem + buf * Tile::kBufWords;
-    const uint16_t* vs = ks + Tile::kKWords;
+  // S^T = K Q^T: lane holds [key n0 + 32*kb + 8*(r/4) + 4*hl + r%4][query row].
+  auto gemm0 = [&](int t, f32x16 (&sd)[KB]) {
+    const uint8_t* st = stage(t);
+    u32x4 a[KD][KB];
+#pragma unroll
+    for (int s = 0; s < KD; ++s)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        a[s][kb] = *reinterpret_cast<const u32x4*>(st + k_lds[s] + kb * 32 * L::kRowBytes);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) sd[kb] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KD; ++s)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sd[kb] = mfma32<T>(a[s][kb], qreg[s], sd[kb]);
+  };
+
+  // Mask tile t's scores where needed; returns the tile's row maximum.
+  auto mask_max = [&](int t, f32x16 (&sc)[KB]) {
     const int n0 = t * BN;
-
-    bool active = wave_has_rows;
-    if (CAUSAL) active = active && (n0 <= mw + 31 + diag);
-    if (active) {
-      f32x16 sacc[KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        sacc[kb] = f32x16{};
-#pragma unroll
-        for (int s = 0; s < KD; ++s) {
-          const u32x4 a = lds_read_b128(ks + k_off + kb * 32 * Tile::kKStride + 16 * s);
-          sacc[kb] = mfma32<T>(a, qreg[s], sacc[kb]);
-        }
-      }
-
-      const bool tail = n0 + BN > p.Sk;
-      const bool straddle = CAUSAL && (n0 + BN - 1 > mw + diag);
-      if (tail || straddle) {
-        int lim = p.Sk - 1;
-        if (CAUSAL) lim = min(lim, row + diag);
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = n0 + 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-            if (key > lim) sacc[kb][r] = kNegInf;
-          }
-      }
-
-      float mt = kNegInf;
+    const bool tail = n0 + BN > p.Sk;
+    const bool straddle = CAUSAL && (n0 + BN - 1 > mw + diag);
+    if (tail || straddle) {
+      int lim = p.Sk - 1;
+      if (CAUSAL) lim = min(lim, row + diag);
+      lim -= n0 + 4 * hl;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
-      mt = xhalf_max(mt);
-      // Lazy rescaling: the exponent offset m_run only moves when a score
-      // exceeds it by more than kRescaleLog2 (in log2 units), so P <= 2^8
-      // and the O / l rescale runs on a few tiles instead of every tile.
-      const bool grow = (mt - m_run) * p.scale_log2 > kRescaleLog2;
-      if (__any(grow)) {
-        // Lanes that do not grow keep alpha = 1 (their offset may still be
-        // -inf on a row that has seen no key yet).
-        const float alpha = grow ? fast_exp2((m_run - mt) * p.scale_log2) : 1.f;
-        m_run = grow ? mt : m_run;
-        l_run *= alpha;
+        for (int r = 0; r < 16; ++r)
+          if (32 * kb + 8 * (r >> 2) + (r & 3) > lim) sc[kb][r] = kNegInf;
+    }
+    float mt = kNegInf;
 #pragma unroll
-        for (int c = 0; c < DB; ++c) oacc[c] *= alpha;
-      }
-      const float neg_m = (m_run == kNegInf) ? 0.f : -m_run * p.scale_log2;
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[kb][r]);
+    return xhalf_max(mt);
+  };
 
-      float psum = 0.f;
-      u32x4 pk[KN];
+  // Lazy rescaling: the exponent offset m_run only moves when a score exceeds
+  // it by more than kRescaleLog2 (in log2 units), so P <= 2^8.  Lanes that do
+  // not grow keep alpha = 1 (their offset may still be -inf on a row that has
+  // seen no key yet).  Returns -m_run * scale * log2(e) for the exponent.
+  auto rescale = [&](float mt) {
+    const bool grow = (mt - m_run) * p.scale_log2 > kRescaleLog2;
+    if (__any(grow)) {
+      const float alpha = grow ? fast_exp2((m_run - mt) * p.scale_log2) : 1.f;
+      m_run = grow ? mt : m_run;
+      l_run *= alpha;
 #pragma unroll
-      for (int s2 = 0; s2 < KN; ++s2) {
-        const int kb = s2 >> 1;
-        const int base = 8 * (s2 & 1);
-        float e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          e[j] = fast_exp2(fmaf(sacc[kb][base + j], p.scale_log2, neg_m));
-          psum += e[j];
-        }
-        pk[s2] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
-                       pack2<T>(e[6], e[7])};
-      }
-      l_run += psum;
+      for (int c = 0; c < DB; ++c) oacc[c] *= alpha;
+    }
+    return (m_run == kNegInf) ? 0.f : -m_run * p.scale_log2;
+  };
 
+  // P^T = exp2(S^T * scale * log2 e - offset), packed as the next MFMA's B operand.
+  u32x4 pk[KN];
+  auto exp_pack = [&](const f32x16 (&sc)[KB], float neg_m) {
+    float psum = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < KN; ++s2) {
+      const int kb = s2 >> 1;
+      const int base = 8 * (s2 & 1);
+      float e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        e[j] = fast_exp2(fmaf(sc[kb][base + j], p.scale_log2, neg_m));
+        psum += e[j];
+      }
+      pk[s2] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
+                     pack2<T>(e[6], e[7])};
+    }
+    l_run += psum;
+  };
+
+  // O^T += V^T P^T: DB*KN MFMAs, each fed by two transposed 8-byte reads that
+  // the scheduling-group pattern issues OLEAD MFMAs ahead.
+  auto gemm1 = [&](int t) {
+    const uint8_t* st = stage(t);
+    constexpr int NM = DB * KN;
+    constexpr int OLEAD = NM < 5 ? NM : 5;
+    u32x4 vt[KN][DB];
+#pragma unroll
+    for (int s2 = 0; s2 < KN; ++s2)
 #pragma unroll
       for (int c = 0; c < DB; ++c) {
+        const uint8_t* vp = st + v_lds[c] + 16 * s2 * L::kRowBytes;
+        const u32x2 lo = lds_read_tr((const uint16_t*)vp);
+        const u32x2 hi = lds_read_tr((const uint16_t*)(vp + 8 * L::kRowBytes));
+        vt[s2][c] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+      }
 #pragma unroll
-        for (int s2 = 0; s2 < KN; ++s2) {
-          const uint16_t* vp = vs + v_off + 16 * s2 * Tile::kVStride + 32 * c;
-          const u32x2 lo = lds_read_tr(vp);
-          const u32x2 hi = lds_read_tr(vp + 8 * Tile::kVStride);
-          const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-          oacc[c] = mfma32<T>(a, pk[s2], oacc[c]);
+    for (int s2 = 0; s2 < KN; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c) oacc[c] = mfma32<T>(vt[s2][c], pk[s2], oacc[c]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * OLEAD, 0);
+#pragma unroll
+    for (int i = 0; i < NM - OLEAD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
+  };
+
+  // Stage A: S(t+1) = K(t+1) Q^T interleaved, MFMA by MFMA, with the softmax
+  // of tile t (exp2, row sum, bf16/fp16 pack).  The order is written out
+  // explicitly and fenced with sched_barrier so the in-order issue keeps the
+  // K read of MFMA i + KLEAD ahead of MFMA i and puts EPM softmax elements
+  // between consecutive MFMAs, where they run while the MFMA unit is busy.
+  auto stage_a = [&](int tn, f32x16 (&nx)[KB], const f32x16 (&sc)[KB], float neg_m) {
+    constexpr int NM = KD * KB;
+    constexpr int KLEAD = NM < 4 ? NM : 4;
+    constexpr int NE = KN * 8;          // softmax elements per lane
+    constexpr int EPM = (NE + NM - 1) / NM;
+    const uint8_t* st = stage(tn);
+    u32x4 a[NM];
+    float e[NE];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < KLEAD; ++i)
+      a[i] = *reinterpret_cast<const u32x4*>(st + k_lds[i / KB] + (i % KB) * 32 * L::kRowBytes);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + KLEAD < NM) {
+        const int n = i + KLEAD;
+        a[n] = *reinterpret_cast<const u32x4*>(st + k_lds[n / KB] + (n % KB) * 32 * L::kRowBytes);
+      }
+      nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
+#pragma unroll
+      for (int k = 0; k < EPM; ++k) {
+        const int x = i * EPM + k;
+        if (x < NE) {
+          const int s2 = x / 8, j = x % 8;
+          e[x] = fast_exp2(fmaf(sc[s2 >> 1][8 * (s2 & 1) + j], p.scale_log2, neg_m));
+          psum += e[x];
+          if (j == 7)
+            pk[s2] = u32x4{pack2<T>(e[x - 7], e[x - 6]), pack2<T>(e[x - 5], e[x - 4]),
+                           pack2<T>(e[x - 3], e[x - 2]), pack2<T>(e[x - 1], e[x])};
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int x = NM * EPM; x < NE; ++x) {
+      const int s2 = x / 8, j = x % 8;
+      e[x] = fast_exp2(fmaf(sc[s2 >> 1][8 * (s2 & 1) + j], p.scale_log2, neg_m));
+      psum += e[x];
+      if (j == 7)
+        pk[s2] = u32x4{pack2<T>(e[x - 7], e[x - 6]), pack2<T>(e[x - 5], e[x - 4]),
+                       pack2<T>(e[x - 3], e[x - 2]), pack2<T>(e[x - 1], e[x])};
+    }
+    l_run += psum;
+  };
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
-    __syncthreads();
+  // Prologue: tiles 0..PD were issued above; iteration t issues tile t+1+PD
+  // into the stage tile t-1 used.  The two score buffers alternate; the loop
+  // is unrolled by two so each iteration names its buffers statically.
+  f32x16 s0[KB], s1[KB];
+  if (n_tiles > 0) {
+    sync_tile(0, PD);
+    if (active(0)) gemm0(0, s0);
+  }
+  auto iteration = [&](int t, f32x16 (&cur)[KB], f32x16 (&nxt)[KB]) {
+    const bool act = active(t);
+    const bool act_next = active(t + 1);
+    float neg_m = 0.f;
+    if (act) neg_m = rescale(mask_max(t, cur));
+    if (t + 1 < n_tiles) {
+      sync_tile(t + 1, PD - 1);
+      if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
+    }
+    // Stage A: S(t+1) MFMAs interleaved with the softmax of tile t.
+    if (act && act_next) {
+      stage_a(t + 1, nxt, cur, neg_m);
+    } else if (act) {
+      exp_pack(cur, neg_m);
+    } else if (act_next) {
+      gemm0(t + 1, nxt);
+    }
+    // Stage B: O += V(t) P(t).
+    if (act) gemm1(t);
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    iteration(t, s0, s1);
+    if (t + 1 < n_tiles) iteration(t + 1, s1, s0);
   }
 
   const float l_tot = xhalf_sum(l_run);
@@ -258,9 +408,9 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
       for (int i = 0; i < 4; ++i) {
         const int d = 32 * c + 8 * i + 4 * hl;
         if (d < p.D) {
-          u32x2 w = {pack2<T>(oacc[c][4 * i] * inv, oacc[c][4 * i + 1] * inv),
+          u32x2 v = {pack2<T>(oacc[c][4 * i] * inv, oacc[c][4 * i + 1] * inv),
                      pack2<T>(oacc[c][4 * i + 2] * inv, oacc[c][4 * i + 3] * inv)};
-          *reinterpret_cast<u32x2*>(ob + d) = w;
+          *reinterpret_cast<u32x2*>(ob + d) = v;
         }
       }
     if (hl == 0) {
@@ -268,46 +418,65 @@ __global__ void __launch_bounds__(NW * 64, DP <= 128 ? 2 : 1) fwd_mfma_kernel(Fw
       p.lse[(int64_t)bh * p.Sq + row] = lse;
     }
   }
+  };  // run_item
+
+  const int first = p.n_mblocks - 1 - item;  // heaviest block first
+  run_item(first);
+  const int second = item;
+  if (p.pair_items && second != first) {
+    __syncthreads();  // every wave is done with the LDS ring before it is refilled
+    run_item(second);
+  }
 }
 
-// gfx950 tile table for the forward kernel: (padded head dim) -> BN, waves.
-// BN = 64 keys per tile up to D = 128 (two 32x32 score blocks per wave per
-// tile), 32 at D = 256 to keep the double-buffered K/V tiles and the
-// accumulators inside the two-waves-per-SIMD budget (256 VGPR+AGPR).
+// gfx950 tile table for the forward kernel, by head dim (padded to 64, 128
+// or 256; other dims run zero-padded in the next size up):
+//   D <= 64 : BN 64, 8 waves (2 per SIMD), 4 stages  (64 KiB LDS)
+//   D <= 128: BN 64, 8 waves (2 per SIMD), 4 stages  (128 KiB LDS)
+//   D <= 256: BN 32, 4 waves (1 per SIMD), 4 stages  (128 KiB LDS)
+// One workgroup per CU.  BN = 64 keeps two 32x32 score blocks per wave per
+// tile (two independent MFMA chains) while the score, operand and O
+// registers fit the 256-register budget of two waves per SIMD.
+struct FwdConfig {
+  int dp, bn, nw;
+};
+
+static FwdConfig fwd_config(int d) {
+  if (d <= 64) return {64, 64, 8};
+  if (d <= 128) return {128, 64, 8};
+  return {256, 32, 4};
+}
+
+int fwd_rows_per_block(int dtype, int d) {
+  (void)dtype;
+  return 32 * fwd_config(d).nw;
+}
+
 template <class T, int DP, int BN, int NW>
 static hipError_t launch_fwd_t(const FwdParams& p, bool causal, hipStream_t s) {
-  const dim3 grid((unsigned)(p.n_mblocks * p.B * p.Hq));
+  const dim3 grid((unsigned)(p.n_items * p.B * p.Hq));
   const dim3 block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, true>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, true>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, false>), grid, block, 0, s, p);
   return hipGetLastError();
-}
-
-int fwd_rows_per_block(int dtype, int dpad) {
-  (void)dtype;
-  (void)dpad;
-  return 128;  // NW = 4 waves x 32 rows
 }
 
 template <class T>
 static hipError_t launch_fwd_dt(const FwdParams& p, bool causal, hipStream_t s) {
-  switch (padded_head_dim(p.D)) {
+  switch (fwd_config(p.D).dp) {
     case 64:
-      return launch_fwd_t<T, 64, 64, 4>(p, causal, s);
-    case 96:
-      return launch_fwd_t<T, 96, 64, 4>(p, causal, s);
+      return launch_fwd_t<T, 64, 64, 8>(p, causal, s);
     case 128:
-      return launch_fwd_t<T, 128, 64, 4>(p, causal, s);
-    case 256:
-      return launch_fwd_t<T, 256, 32, 4>(p, causal, s);
+      return launch_fwd_t<T, 128, 64, 8>(p, causal, s);
     default:
-      return hipErrorInvalidValue;
+      return launch_fwd_t<T, 256, 32, 4>(p, causal, s);
   }
 }
 
 hipError_t launch_fwd_mfma(int dtype, const FwdParams& p, bool causal, hipStream_t s) {
+  if (p.D > 256) return hipErrorInvalidValue;
   if (dtype == BF16::code) return launch_fwd_dt<BF16>(p, causal, s);
   if (dtype == F16::code) return launch_fwd_dt<F16>(p, causal, s);
   return hipErrorInvalidValue;

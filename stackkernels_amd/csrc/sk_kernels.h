@@ -21,6 +21,8 @@ struct FwdParams {
   int64_t o_sb, o_sh, o_ss;
   int B, Hq, Hkv, Sq, Sk, D, group;
   int n_mblocks;     // ceil(Sq / rows per workgroup)
+  int n_items;       // work items per (batch, head): n_mblocks, or ceil(n_mblocks/2) if paired
+  int pair_items;    // 1: item j runs query blocks n_mblocks-1-j and j
   float scale;       // |sm_scale|
   float scale_log2;  // |sm_scale| * log2(e)
   uint32_t q_sign;   // 0, or the sign-bit mask that negates q when sm_scale < 0
@@ -72,8 +74,8 @@ hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s);
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s);
 
-// Rows of queries one forward workgroup covers for (dtype, padded head dim).
-int fwd_rows_per_block(int dtype, int dpad);
+// Rows of queries one forward workgroup covers for (dtype, head dim).
+int fwd_rows_per_block(int dtype, int d);
 // Padded head dim the kernels are compiled for (64, 96, 128 or 256), or 0.
 int padded_head_dim(int d);
 
