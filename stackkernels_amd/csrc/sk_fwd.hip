@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   // between consecutive MFMAs, where they run while the MFMA unit is busy.
   auto stage_a = [&](int tn, f32x16 (&nx)[KB], const f32x16 (&sc)[KB], float neg_m) {
     constexpr int NM = KD * KB;
-    constexpr int KLEAD = NM < 4 ? NM : 4;
+    constexpr int KLEAD = NM < 3 ? NM : 3;
     constexpr int NE = KN * 8;          // softmax elements per lane
     constexpr int EPM = (NE + NM - 1) / NM;
     const uint8_t* st = stage(tn);
