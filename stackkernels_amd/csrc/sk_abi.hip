@@ -63,19 +63,37 @@ int check_ptr(const char* name, const void* p) {
   return SK_OK;
 }
 
-// gfx950 decode split table.  A split is one workgroup per (batch, KV head).
-// One-wave workgroups (groups up to 16 heads) take 18 KB of LDS each, so a CU
-// holds 8 of them; 32- and 64-head groups use 2 and 4 waves.  The table aims
-// for about two full waves of workgroups over the 256 CUs, keeps every split
-// at least 256 keys (8 tiles) so the fixed cost per workgroup stays small,
-// and caps the split count at 1024 (the combine kernel's LDS weight array).
-int plan_splits(int B, int Hq, int Hkv, int Sk) {
+// gfx950 decode split table.  A split is one workgroup per (batch, KV head);
+// the table sizes the split count to the workgroups the chip holds at once:
+// * groups of up to 16 heads: one-wave workgroups, 18 KB of LDS each, eight
+//   per CU; aim for about two rounds of them;
+// * 32- and 64-head groups (D of 64, 128 or 256): the 2- / 4-wave LDS-ring
+//   kernel, whose 5 x 16 KB stages (2 x 32 KB at D = 256) leave room for
+//   160 KB / ring bytes workgroups per CU; aim for exactly one round, so the
+//   ring stays full for the whole call and no split waits for a second
+//   round (a 64-head group writes 32 KB of partials per split, so fewer,
+//   longer splits also keep that traffic small);
+// * other head dims with large groups: the register-staged kernel.
+// Every split keeps at least 256 keys (8 tiles) and the count is capped at
+// 1024 (the combine kernel's LDS weight array).
+int plan_splits(int B, int Hq, int Hkv, int Sk, int D) {
   if (Sk <= 0 || B <= 0 || Hkv <= 0) return 1;
   const int group = Hq / Hkv;
+  const int dpad = sk::padded_head_dim(D);
   const int waves = group <= 16 ? 1 : group <= 32 ? 2 : 4;
-  const int64_t slots = 256LL * 8 / waves;  // resident workgroups on the chip
+  int64_t slots;
+  int rounds;
+  if (group > 16 && (dpad == 64 || dpad == 128 || dpad == 256)) {
+    const int ring = (dpad == 256 ? 2 : 5) * 2 * 32 * dpad * 2;
+    const int per_cu = std::min(160 * 1024 / ring, 16 / waves);
+    slots = 256LL * per_cu;
+    rounds = 1;
+  } else {
+    slots = 256LL * 8 / waves;
+    rounds = 2;
+  }
   const int64_t units = (int64_t)B * Hkv;
-  int64_t splits = (2 * slots + units - 1) / units;
+  int64_t splits = (rounds * slots + units - 1) / units;
   splits = std::min<int64_t>(splits, std::max(1, Sk / 256));
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, 1024));
   return (int)splits;
@@ -218,7 +236,7 @@ int sk_decode_plan(int dtype, int B, int Hq, int Hkv, int Sk, int D, int* num_sp
   int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
   if (rc) return rc;
   if (!num_splits || !workspace_bytes) return fail(SK_EINVAL, "output pointer is NULL");
-  int splits = dtype == SK_F32 ? 1 : plan_splits(B, Hq, Hkv, Sk);
+  int splits = dtype == SK_F32 ? 1 : plan_splits(B, Hq, Hkv, Sk, D);
   if (splits > 1) splits = (Sk + keys_per_split_for(Sk, splits) - 1) / keys_per_split_for(Sk, splits);
   *num_splits = splits;
   *workspace_bytes = decode_ws_bytes(dtype, B, Hq, D, splits);
@@ -254,7 +272,7 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
     return fail(SK_EUNSUPPORTED, "decode supports up to 64 query heads per KV head, got %d", Hq / Hkv);
 
   if (dtype == SK_F32) num_splits = 1;
-  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk);
+  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk, D);
   if (num_splits < 1 || num_splits > 1024)
     return fail(SK_EINVAL, "num_splits=%d outside [1, 1024]", num_splits);
   const int kps = keys_per_split_for(Sk, num_splits);

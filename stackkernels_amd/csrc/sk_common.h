@@ -202,6 +202,20 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Wait until at most `ahead` tiles of LOADS vector-memory loads each are
+// still in flight (ahead in [0, MAXA]; the count must be an immediate).
+template <int LOADS, int MAXA>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+  static_assert(LOADS * MAXA < 64, "vmcnt range");
+  if constexpr (MAXA >= 6) { if (ahead >= 6) { wait_vmcnt<LOADS * 6>(); return; } }
+  if constexpr (MAXA >= 5) { if (ahead == 5) { wait_vmcnt<LOADS * 5>(); return; } }
+  if constexpr (MAXA >= 4) { if (ahead == 4) { wait_vmcnt<LOADS * 4>(); return; } }
+  if constexpr (MAXA >= 3) { if (ahead == 3) { wait_vmcnt<LOADS * 3>(); return; } }
+  if constexpr (MAXA >= 2) { if (ahead == 2) { wait_vmcnt<LOADS * 2>(); return; } }
+  if constexpr (MAXA >= 1) { if (ahead == 1) { wait_vmcnt<LOADS>(); return; } }
+  wait_vmcnt<0>();
+}
+
 __device__ __forceinline__ u32x4 ldg_b128(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
