@@ -282,6 +282,8 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
     peak = PEAK_HBM_GBPS if bound == "hbm" else PEAK_BF16_TFLOPS
     kernel = {"fwd": "fwd_mfma_kernel", "fwdbwd": "fwd + bwd kernels",
               "decode": "decode_split_kernel + decode_combine_kernel"}[w["kind"]]
+    if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
+        kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
     res = {
         "workload": key,
         "config": {k_: w[k_] for k_ in ("name", "B", "Hq", "Hkv", "Sq", "Sk", "D", "causal", "dtype")},
