@@ -218,6 +218,10 @@ int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const
   p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
+  // |s| * 1e-30 * log2(e) rounds to 0 next to any finite score, so a zero
+  // scale still gives P = exp2(-lse * log2 e) exactly while -inf stays -inf.
+  p.abs_scale_log2 = std::max(std::fabs(sm_scale), 1e-30f) * 1.4426950408889634f;
+  p.op_sign = sm_scale < 0.f ? 0x80008000u : 0u;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = hipSuccess;
   if (rows > 0) e = sk::launch_bwd_prep(dtype, p, s);

@@ -10,97 +10,166 @@
 // nothing.  dS = P * (dP - delta), dQ = scale * dS K, dK = scale * dS^T Q,
 // dV = P^T dO.  All products run on v_mfma_f32_32x32x16 with fp32
 // accumulation; P and dS are rounded to the input type for their products.
+// A negative sm_scale is applied by flipping the sign bits of the register
+// operand of the score product (q in the dQ kernel, k in the dK/dV kernel),
+// so the exponent always uses |sm_scale| and a masked score is simply -inf.
 //
-// dK/dV kernel (bwd_dkv_kernel): a workgroup owns 32*NW keys of one
+// Shared organisation (the forward kernel's, adapted):
+// * Four waves per workgroup, one per SIMD, one workgroup per CU: each wave
+//   keeps its 32 rows of the resident operands in registers and has the
+//   whole 512-entry VGPR+AGPR file for operands, two score blocks in flight
+//   and the fp32 accumulators.
+// * The streamed tiles go through a STAGES-deep LDS ring written by
+//   buffer_load ... lds (direct to LDS), two tiles ahead of the math, one
+//   barrier per tile.  Rows past the sequence end and head-dim padding come
+//   back as zeros from the buffer range check.
+// * Streamed tiles are read both row-wise (ds_read_b128, 16 consecutive rows
+//   per 16-lane group) and transposed (ds_read_b64_tr_b16, 4 aligned rows x 4
+//   chunks per 32-lane group).  One XOR swizzle on the 16-byte chunk index
+//   serves both: chunk c of row r sits at c ^ f(r) with f a bijection on
+//   r % 16 whose top two bits differ across every aligned group of 4 rows,
+//   so both read shapes hit 16 distinct bank quads of the 64-bank LDS.
+// * Software pipeline per wave: the score and dP MFMAs of the next block are
+//   interleaved, MFMA by MFMA, with the exp / dS / pack VALU work of the
+//   current block (the MFMA unit runs asynchronously to the VALU), then the
+//   gradient MFMAs of the current block run with their transposed operand
+//   reads issued a few MFMAs ahead.
+// * XCD-aware order: the 8 XCDs each walk a contiguous range of work items,
+//   head-major, so the workgroups that share a head's streamed operand share
+//   an L2.
+//
+// dK/dV kernel (bwd_dkv_kernel): a workgroup owns 128 keys of one
 // (batch, KV head), 32 per wave, and walks every query head of that KV
-// head's group and every query tile that can see its keys, so the GQA sum
-// happens in registers (deterministic, no atomics).  The wave computes
-// S = Q K^T and dP = dO V^T with K and V held in registers as the B operand:
-// each lane then owns one key (its l%32) and 16 queries per 32-query block.
-// P and dS feed dV^T += dO^T P and dK^T += Q^T dS straight from registers,
-// with dO^T / Q^T read transposed from the row-major LDS tiles by
-// ds_read_b64_tr_b16 (the contraction over queries is permuted identically
-// on both operands).  Q / dO tiles and their row statistics stream through
-// double-buffered LDS.  At D = 256 the output head dim is split over two
-// workgroups to keep the accumulators inside the register file.
+// head's group and every 64-query tile that can see its keys, so the GQA sum
+// happens in registers (deterministic, no atomics).  S = Q K^T and
+// dP = dO V^T use K and V from registers as the B operand: each lane then
+// owns one key (its l%32) and 16 queries per 32-query block; P and dS feed
+// dV^T += dO^T P and dK^T += Q^T dS straight from registers, with dO^T / Q^T
+// read transposed from the ring (the contraction over queries is permuted
+// identically on both operands).  Every wave keeps its own copy of the
+// tile's row statistics in the ring.  At D = 256 the output head dim is
+// split over two workgroups to keep the accumulators in the register file.
 //
-// dQ kernel (bwd_dq_kernel): the forward kernel's organisation -- a
-// workgroup owns 32*NW query rows, K/V tiles stream through double-buffered
-// LDS, S^T = K Q^T and dP^T = V dO^T have one query per lane, and
-// dQ^T += K^T dS^T reads K^T transposed from LDS.
+// dQ kernel (bwd_dq_kernel): a workgroup owns 128 query rows, 32 per wave,
+// with Q and dO in registers; K/V tiles stream through the ring;
+// S^T = K Q^T and dP^T = V dO^T give one query per lane, and
+// dQ^T += K^T dS^T reads K^T transposed from the ring.
 #include "sk_common.h"
 #include "sk_kernels.h"
 
 namespace sk {
 
+// One streamed tile of ROWS rows x DP 16-bit words in LDS, unpadded, moved
+// in 1 KiB segments (one wave-wide 16-byte-per-lane DMA each).
 template <int DP, int ROWS>
-struct RowTile {
-  static constexpr int kStride = DP + 16;             // 16-bit words per LDS row
-  static constexpr int kWords = ROWS * kStride;       // one tile
-  static constexpr int kChunksPerRow = DP / 8;        // 16-byte chunks per row
-  static constexpr int kChunks = ROWS * kChunksPerRow;
+struct BwdTile {
+  static constexpr int kCpr = DP / 8;  // 16-byte chunks per row
+  static constexpr int kRowBytes = DP * 2;
+  static constexpr int kTileBytes = ROWS * kRowBytes;
+  static constexpr int kSegRows = 1024 / kRowBytes;
+  static constexpr int kSegs = kTileBytes / 1024;
 };
 
-// A-operand offset of the transposed 4x16 read pattern: lane j of each
-// 16-lane group points at row 4*(l/32) + (j/4), column 16*((l/16)%2) + 4*(j%4).
-__device__ __forceinline__ int tr_offset(int lane, int stride) {
-  const int j16 = lane & 15;
-  return (4 * (lane >> 5) + j16 / 4) * stride + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+// Chunk swizzle for tiles read both row-wise and transposed (see the file
+// comment).  D >= 128 (rows of whole 64-bank lines): f(r) swaps the two bit
+// pairs of r % 16.  D = 64 (two rows per bank line, alternating halves):
+// f depends on r / 2 so that rows of one parity get distinct values.  In
+// both, f(r + 16) = f(r).
+template <int DP>
+__device__ __forceinline__ int swz_rt(int r) {
+  return DP == 64 ? (((r >> 1) & 1) << 2) | ((r >> 2) & 3) : ((r & 3) << 2) | ((r >> 2) & 3);
 }
 
-template <class T, int DP, int DO, int BMQ, int NW, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
-  using Tile = RowTile<DP, BMQ>;
-  constexpr int NT = NW * 64;
-  constexpr int BNK = 32 * NW;
-  constexpr int KD = DP / 16;   // k-steps over the head dim (S, dP)
-  constexpr int QB = BMQ / 32;  // 32-query blocks per tile
-  constexpr int KM = BMQ / 16;  // k-steps over queries (dV, dK)
-  constexpr int DB = DO / 32;   // 32-wide output head-dim blocks
-  constexpr int LOADS = (Tile::kChunks + NT - 1) / NT;
-  constexpr bool kRagged = Tile::kChunks % NT != 0;
-  static_assert(BMQ <= NT, "one thread per row loads the row statistics");
+// Lane-constant byte offsets of a transposed (ds_read_b64_tr_b16) operand
+// read: A[m = l%32 -> head-dim column 32c + m][k = 8*(l/32) + j -> tile rows
+// 4*(l/32) + j (j < 4) and 8 + 4*(l/32) + j - 4 (j >= 4)].  Lane j16 of each
+// 16-lane group addresses row 4*(l/32) + j16/4 (+8 for the upper half),
+// chunk chunk0 + 4c + 2*((l/16)%2) + (j16%4)/2, 8-byte half j16%2.  The
+// upper half needs its own offsets because f(r + 8) != f(r).
+template <int DP, int NC>
+__device__ __forceinline__ void tr_offsets(int lane, int chunk0, int (&lo)[NC], int (&hi)[NC]) {
+  const int j16 = lane & 15;
+  const int r = 4 * (lane >> 5) + j16 / 4;
+  const int g = 2 * ((lane >> 4) & 1) + (j16 & 3) / 2;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = chunk0 + 4 * c + g;
+    lo[c] = r * DP * 2 + ((ch ^ swz_rt<DP>(r)) * 16) + 8 * (j16 & 1);
+    hi[c] = (r + 8) * DP * 2 + ((ch ^ swz_rt<DP>(r + 8)) * 16) + 8 * (j16 & 1);
+  }
+}
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * 2 * Tile::kWords];
-  __shared__ __attribute__((aligned(16))) float stat[2][2][BMQ];  // [buf][lse2 | delta][row]
+__device__ __forceinline__ u32x4 lds_b128(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ u32x4 lds_tr_pair(const uint8_t* lo, const uint8_t* hi) {
+  const u32x2 a = lds_read_tr((const uint16_t*)lo);
+  const u32x2 b = lds_read_tr((const uint16_t*)hi);
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3);
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV
+// ---------------------------------------------------------------------------
+template <class T, int DP, int DO, int BMQ, int NW, int STAGES, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
+  using L = BwdTile<DP, BMQ>;  // Q and dO tiles
+  constexpr int BNK = 32 * NW;
+  constexpr int KD = DP / 16;  // k-steps over the head dim (S, dP)
+  constexpr int QB = BMQ / 32;  // 32-query blocks per tile
+  constexpr int DB = DO / 32;  // 32-wide output head-dim blocks
+  constexpr int LQ = L::kSegs / NW;  // Q (and dO) segments per wave per tile
+  constexpr int kStatBytes = 512;  // per wave: 64 lse*log2e, then 64 delta
+  constexpr int kStageBytes = 2 * L::kTileBytes + NW * kStatBytes;
+  constexpr int kLoads = 2 * LQ + 2;  // DMAs per wave per tile
+  constexpr int PD = STAGES - 2;
+  constexpr int kDSplit = DP / DO;
+  constexpr int RB = L::kRowBytes;
+  static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
+  static_assert(QB >= 1 && BMQ <= 64, "32 or 64 queries per tile");
+  static_assert(PD >= 1 && PD <= 2, "prefetch distance");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
-  constexpr int kDSplit = DP / DO;
-  int bid = blockIdx.x;
-  const int dsp = bid % kDSplit;
-  bid /= kDSplit;
-  const int bk_count = p.B * p.Hkv;
-  const int bk = bid % bk_count;
-  const int nblk = bid / bk_count;
+  // Work item: (batch, KV head) major, then key block (lowest first: under
+  // the causal mask it sees the most queries), then head-dim half.
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int per_head = p.n_nblocks * kDSplit;
+  const int bk = w / per_head;
+  const int rem = w - bk * per_head;
+  const int nblk = rem / kDSplit;
+  const int dsp = rem - nblk * kDSplit;
   const int b = bk / p.Hkv;
-  const int hkv = bk % p.Hkv;
+  const int hkv = bk - b * p.Hkv;
   const int n0 = nblk * BNK;
   const int nw = n0 + 32 * wave;
   const int key = nw + l32;
   const int diag = p.Sk - p.Sq;
   const int d_out0 = dsp * DO;
 
-  // K and V rows of this lane's key as the B operand: k[key][16*s + 8*hl .. +7].
+  // K (sign-flipped for a negative scale) and V rows of this lane's key as
+  // the B operand: k[key][16*s + 8*hl .. +7].
   u32x4 kreg[KD], vreg[KD];
   {
-    const int64_t krow = ((int64_t)bk * p.Sk + key) * p.D;
-    const uint16_t* kp = (const uint16_t*)p.k + krow;
-    const uint16_t* vp = (const uint16_t*)p.v + krow;
+    const int krows = max(0, min(32, p.Sk - nw));
+    const int64_t k0 = ((int64_t)bk * p.Sk + min(nw, p.Sk)) * p.D;
+    // Wave-uniform; readfirstlane keeps the resource in SGPRs (no waterfall loop).
+    const int bytes = __builtin_amdgcn_readfirstlane(tile_bytes(krows, p.D, p.D));
+    const buf_rsrc kr = make_rsrc((const uint16_t*)p.k + k0, bytes);
+    const buf_rsrc vr = make_rsrc((const uint16_t*)p.v + k0, bytes);
 #pragma unroll
     for (int s = 0; s < KD; ++s) {
       const int d0 = 16 * s + 8 * hl;
-      u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
-      if (key < p.Sk && d0 < p.D) {
-        kx = ldg_b128_cached(kp + d0);
-        vx = ldg_b128_cached(vp + d0);
-      }
-      kreg[s] = kx;
-      vreg[s] = vx;
+      const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.D + d0) * 2) : kBufferOob;
+      kreg[s] = buffer_load_b128(kr, off) ^ p.op_sign;
+      vreg[s] = buffer_load_b128(vr, off);
     }
   }
 
@@ -109,52 +178,44 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
   if (CAUSAL) m_begin = max(0, n0 - diag) / BMQ * BMQ;
   const int n_mt = m_begin < p.Sq ? (p.Sq - m_begin + BMQ - 1) / BMQ : 0;
   const int n_it = p.group * n_mt;
+  const int n_blk = n_it * QB;
 
-  u32x4 qld[LOADS], gld[LOADS];
-  float st_l = 0.f, st_d = 0.f;
-  auto load_tile = [&](int it) {
-    const int gi = it / n_mt;
-    const int m0 = m_begin + (it - gi * n_mt) * BMQ;
+  uint32_t goff[LQ];
+#pragma unroll
+  for (int j = 0; j < LQ; ++j) {
+    const int seg = wave + j * NW;
+    const int r = seg * L::kSegRows + lane / L::kCpr;
+    const int c = (lane % L::kCpr) ^ swz_rt<DP>(r);
+    goff[j] = c * 8 < p.D ? (uint32_t)((r * p.D + c * 8) * 2) : kBufferOob;
+  }
+  auto tile_head = [&](int it) { return it / n_mt; };
+  auto tile_m0 = [&](int it, int gi) { return m_begin + (it - gi * n_mt) * BMQ; };
+  auto issue_tile = [&](int it) {
+    const int gi = tile_head(it);
+    const int m0 = tile_m0(it, gi);
     const int64_t bh = (int64_t)b * p.Hq + hkv * p.group + gi;
-    const uint16_t* qb = (const uint16_t*)p.q + bh * p.Sq * p.D;
-    const uint16_t* gb = (const uint16_t*)p.dout + bh * p.Sq * p.D;
+    const int bytes = tile_bytes(min(BMQ, p.Sq - m0), p.D, p.D);
+    const int64_t q0 = (bh * p.Sq + m0) * p.D;
+    const i32x4 qr = make_rsrc_words((const uint16_t*)p.q + q0, bytes);
+    const i32x4 gr = make_rsrc_words((const uint16_t*)p.dout + q0, bytes);
+    const uint32_t st = lds_addr(smem) + (it % STAGES) * kStageBytes;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * NT;
-      const int r = c / Tile::kChunksPerRow;
-      const int d = (c % Tile::kChunksPerRow) * 8;
-      const int m = m0 + r;
-      u32x4 qx = {0u, 0u, 0u, 0u}, gx = {0u, 0u, 0u, 0u};
-      if ((!kRagged || c < Tile::kChunks) && m < p.Sq && d < p.D) {
-        qx = ldg_b128_cached(qb + (int64_t)m * p.D + d);
-        gx = ldg_b128_cached(gb + (int64_t)m * p.D + d);
-      }
-      qld[i] = qx;
-      gld[i] = gx;
+    for (int j = 0; j < LQ; ++j) {
+      const int seg = wave + j * NW;
+      buffer_load_lds_b128(qr, st + seg * 1024, goff[j]);
+      buffer_load_lds_b128(gr, st + L::kTileBytes + seg * 1024, goff[j]);
     }
-    if (tid < BMQ) {
-      const int m = m0 + tid;
-      st_l = m < p.Sq ? p.lse_log2[bh * p.Sq + m] : __builtin_inff();
-      st_d = m < p.Sq ? p.delta[bh * p.Sq + m] : 0.f;
-    }
+    const int sbytes = min(64, p.Sq - m0) * 4;
+    const i32x4 lr = make_rsrc_words(p.lse_log2 + bh * p.Sq + m0, sbytes);
+    const i32x4 dr = make_rsrc_words(p.delta + bh * p.Sq + m0, sbytes);
+    const uint32_t sb = st + 2 * L::kTileBytes + wave * kStatBytes;
+    buffer_load_lds_b32(lr, sb, lane * 4);
+    buffer_load_lds_b32(dr, sb + 256, lane * 4);
   };
-  auto store_tile = [&](int buf) {
-    uint16_t* qs = smem + buf * 2 * Tile::kWords;
-    uint16_t* gs = qs + Tile::kWords;
+
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * NT;
-      if (kRagged && c >= Tile::kChunks) continue;
-      const int r = c / Tile::kChunksPerRow;
-      const int d = (c % Tile::kChunksPerRow) * 8;
-      *reinterpret_cast<u32x4*>(qs + r * Tile::kStride + d) = qld[i];
-      *reinterpret_cast<u32x4*>(gs + r * Tile::kStride + d) = gld[i];
-    }
-    if (tid < BMQ) {
-      stat[buf][0][tid] = st_l;
-      stat[buf][1][tid] = st_d;
-    }
-  };
+  for (int t = 0; t <= PD; ++t)
+    if (t < n_it) issue_tile(t);
 
   f32x16 dkacc[DB], dvacc[DB];
 #pragma unroll
@@ -163,95 +224,180 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     dvacc[c] = f32x16{};
   }
 
-  if (n_it > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  const int a_off = l32 * Tile::kStride + 8 * hl;
-  const int t_off = tr_offset(lane, Tile::kStride) + d_out0;
-
-  for (int it = 0; it < n_it; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < n_it) load_tile(it + 1);
-    const int gi = it / n_mt;
-    const int m0 = m_begin + (it - gi * n_mt) * BMQ;
-    const uint16_t* qs = smem + buf * 2 * Tile::kWords;
-    const uint16_t* gs = qs + Tile::kWords;
-    const float* lsp = stat[buf][0];
-    const float* dlp = stat[buf][1];
-
-    bool active = nw < p.Sk;
-    if (CAUSAL) active = active && (m0 + BMQ - 1 + diag >= nw);
-    if (active) {
-      // S = Q K^T and dP = dO V^T: lane holds [query 32*qb + 8*(r/4) + 4*hl + r%4][key l32].
-      f32x16 sacc[QB], pacc[QB];
+  // Row-wise A operand of S / dP: query row l32 (+32 per block), chunk 2s + hl.
+  int qa_lds[KD];
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        sacc[qb] = f32x16{};
-        pacc[qb] = f32x16{};
+  for (int s = 0; s < KD; ++s) qa_lds[s] = l32 * RB + (((2 * s + hl) ^ swz_rt<DP>(l32)) * 16);
+  int tr_lo[DB], tr_hi[DB];
+  tr_offsets<DP, DB>(lane, d_out0 / 8, tr_lo, tr_hi);
+
+  const float c_log2 = p.abs_scale_log2;
+  auto stage = [&](int it) { return smem + (it % STAGES) * kStageBytes; };
+  auto block_m = [&](int u) {
+    const int it = u / QB;
+    return tile_m0(it, tile_head(it)) + 32 * (u % QB);
+  };
+  auto active = [&](int u) {
+    if (u >= n_blk || nw >= p.Sk) return false;
+    return !CAUSAL || nw <= block_m(u) + 31 + diag;
+  };
+  auto sync_tile = [&](int it, int max_ahead) {
+    wait_tiles<kLoads, PD>(min(max_ahead, n_it - 1 - it));
+    __syncthreads();
+  };
+
+  // S = Q K^T and dP = dO V^T of block u (no interleave): lane holds
+  // [query 8*(r/4) + 4*hl + r%4][key l32].
+  auto block_sdp = [&](int u, f32x16& sc, f32x16& pc) {
+    const uint8_t* st = stage(u / QB) + (u % QB) * 32 * RB;
+    sc = f32x16{};
+    pc = f32x16{};
 #pragma unroll
-        for (int s = 0; s < KD; ++s) {
-          const u32x4 a = lds_read_b128(qs + a_off + 32 * qb * Tile::kStride + 16 * s);
-          sacc[qb] = mfma32<T>(a, kreg[s], sacc[qb]);
-        }
+    for (int s = 0; s < KD; ++s) {
+      sc = mfma32<T>(lds_b128(st + qa_lds[s]), kreg[s], sc);
+      pc = mfma32<T>(lds_b128(st + L::kTileBytes + qa_lds[s]), vreg[s], pc);
+    }
+  };
+
+  // Causal mask of a block on the diagonal: key > query + diag -> -inf.
+  auto premask = [&](int u, f32x16& sc) {
+    const int mq = block_m(u);
+    if (!CAUSAL || nw + 31 <= mq + diag) return;
+    const int lim = key - diag - mq - 4 * hl;  // masked iff 8*(r/4) + r%4 < lim
 #pragma unroll
-        for (int s = 0; s < KD; ++s) {
-          const u32x4 a = lds_read_b128(gs + a_off + 32 * qb * Tile::kStride + 16 * s);
-          pacc[qb] = mfma32<T>(a, vreg[s], pacc[qb]);
-        }
+    for (int r = 0; r < 16; ++r)
+      if (8 * (r >> 2) + (r & 3) < lim) sc[r] = kNegInf;
+  };
+
+  // Row statistics of block u for this lane's 16 queries.
+  auto load_stats = [&](int u, f32x4 (&lv)[4], f32x4 (&dv)[4]) {
+    const uint8_t* sb = stage(u / QB) + 2 * L::kTileBytes + wave * kStatBytes + 128 * (u % QB);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lv[i] = *reinterpret_cast<const f32x4*>(sb + 4 * (8 * i + 4 * hl));
+      dv[i] = *reinterpret_cast<const f32x4*>(sb + 256 + 4 * (8 * i + 4 * hl));
+    }
+  };
+
+  // P and dS of one element, packed eight at a time into the B operands of
+  // the k-step s2 = r / 8 (queries permuted as the transposed reads are).
+  u32x4 pk[2], dsk[2];
+  float pe[16], de[16];
+  auto elem = [&](int r, const f32x16& sc, const f32x16& pc, const f32x4 (&lv)[4],
+                  const f32x4 (&dv)[4]) {
+    pe[r] = fast_exp2(fmaf(sc[r], c_log2, -lv[r >> 2][r & 3]));
+    de[r] = pe[r] * (pc[r] - dv[r >> 2][r & 3]);
+    if ((r & 7) == 7) {
+      const int b8 = r - 7;
+      pk[r >> 3] = u32x4{pack2<T>(pe[b8], pe[b8 + 1]), pack2<T>(pe[b8 + 2], pe[b8 + 3]),
+                         pack2<T>(pe[b8 + 4], pe[b8 + 5]), pack2<T>(pe[b8 + 6], pe[b8 + 7])};
+      dsk[r >> 3] = u32x4{pack2<T>(de[b8], de[b8 + 1]), pack2<T>(de[b8 + 2], de[b8 + 3]),
+                          pack2<T>(de[b8 + 4], de[b8 + 5]), pack2<T>(de[b8 + 6], de[b8 + 7])};
+    }
+  };
+  auto block_valu = [&](int u, const f32x16& sc, const f32x16& pc) {
+    f32x4 lv[4], dv[4];
+    load_stats(u, lv, dv);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) elem(r, sc, pc, lv, dv);
+  };
+
+  // Stage A: S / dP MFMAs of block un (alternating, so each accumulator's
+  // chain has one independent MFMA between its links) interleaved with the
+  // P / dS elements of block uc; fenced per MFMA so the in-order issue keeps
+  // the LDS read KLEAD MFMAs ahead and EPM elements between MFMAs.
+  auto stage_a = [&](int un, f32x16& sn, f32x16& pn, int uc, const f32x16& sc,
+                     const f32x16& pc) {
+    constexpr int NM = 2 * KD;
+    constexpr int KLEAD = 3;
+    constexpr int EPM = (16 + NM - 1) / NM;
+    const uint8_t* st = stage(un / QB) + (un % QB) * 32 * RB;
+    f32x4 lv[4], dv[4];
+    load_stats(uc, lv, dv);
+    u32x4 a[NM];
+#pragma unroll
+    for (int i = 0; i < KLEAD; ++i)
+      a[i] = lds_b128(st + (i & 1) * L::kTileBytes + qa_lds[i >> 1]);
+    sn = f32x16{};
+    pn = f32x16{};
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + KLEAD < NM) {
+        const int n = i + KLEAD;
+        a[n] = lds_b128(st + (n & 1) * L::kTileBytes + qa_lds[n >> 1]);
       }
-
-      const bool straddle = CAUSAL && (nw + 31 > m0 + diag);
-      u32x4 pk[KM], dsk[KM];
+      if (i & 1)
+        pn = mfma32<T>(a[i], vreg[i >> 1], pn);
+      else
+        sn = mfma32<T>(a[i], kreg[i >> 1], sn);
 #pragma unroll
-      for (int s2 = 0; s2 < KM; ++s2) {
-        const int qb = s2 >> 1;
-        const int base = 8 * (s2 & 1);
-        const int q0 = 32 * qb + 2 * base + 4 * hl;  // first query of register group base/4
-        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lsp + q0);
-        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lsp + q0 + 8);
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(dlp + q0);
-        const f32x4 d1 = *reinterpret_cast<const f32x4*>(dlp + q0 + 8);
-        float pv[8], dv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = base + j;
-          const float lj = j < 4 ? l0[j & 3] : l1[j & 3];
-          const float dj = j < 4 ? d0[j & 3] : d1[j & 3];
-          float pe = fast_exp2(fmaf(sacc[qb][r], p.scale_log2, -lj));
-          if (straddle) {
-            const int query = m0 + q0 + 8 * (j >> 2) + (j & 3);
-            if (key > query + diag) pe = 0.f;
-          }
-          pv[j] = pe;
-          dv[j] = pe * (pacc[qb][r] - dj);
-        }
-        pk[s2] = u32x4{pack2<T>(pv[0], pv[1]), pack2<T>(pv[2], pv[3]), pack2<T>(pv[4], pv[5]),
-                       pack2<T>(pv[6], pv[7])};
-        dsk[s2] = u32x4{pack2<T>(dv[0], dv[1]), pack2<T>(dv[2], dv[3]), pack2<T>(dv[4], dv[5]),
-                        pack2<T>(dv[6], dv[7])};
-      }
+      for (int k = 0; k < EPM; ++k)
+        if (i * EPM + k < 16) elem(i * EPM + k, sc, pc, lv, dv);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-      // dV^T += dO^T P and dK^T += Q^T dS: lane holds [d 32*c + 8*(r/4) + 4*hl + r%4][key l32].
+  // Stage B: dV^T += dO^T P and dK^T += Q^T dS for block u: lane holds
+  // [d d_out0 + 32*c + 8*(r/4) + 4*hl + r%4][key l32].
+  auto stage_b = [&](int u) {
+    const uint8_t* st = stage(u / QB) + (u % QB) * 32 * RB;
+    constexpr int NM = 2 * 2 * DB;
+    constexpr int OLEAD = NM < 4 ? NM : 4;
+    u32x4 go[2][DB], qo[2][DB];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int c = 0; c < DB; ++c) {
+        const uint8_t* r0 = st + 16 * s2 * RB;
+        go[s2][c] = lds_tr_pair(r0 + L::kTileBytes + tr_lo[c], r0 + L::kTileBytes + tr_hi[c]);
+        qo[s2][c] = lds_tr_pair(r0 + tr_lo[c], r0 + tr_hi[c]);
+      }
 #pragma unroll
-        for (int s2 = 0; s2 < KM; ++s2) {
-          const int off = t_off + 16 * s2 * Tile::kStride + 32 * c;
-          const u32x2 glo = lds_read_tr(gs + off);
-          const u32x2 ghi = lds_read_tr(gs + off + 8 * Tile::kStride);
-          dvacc[c] = mfma32<T>(u32x4{glo[0], glo[1], ghi[0], ghi[1]}, pk[s2], dvacc[c]);
-          const u32x2 qlo = lds_read_tr(qs + off);
-          const u32x2 qhi = lds_read_tr(qs + off + 8 * Tile::kStride);
-          dkacc[c] = mfma32<T>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, dsk[s2], dkacc[c]);
-        }
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c) {
+        dvacc[c] = mfma32<T>(go[s2][c], pk[s2], dvacc[c]);
+        dkacc[c] = mfma32<T>(qo[s2][c], dsk[s2], dkacc[c]);
+      }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * OLEAD, 0);
+#pragma unroll
+    for (int i = 0; i < NM - OLEAD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
+  };
+
+  // Block pipeline.  Iteration u: mask block u, cross into the next tile if
+  // block u + 1 starts one (wait + barrier, then refill the stage tile
+  // it - 1 used), stage A (S/dP of u + 1 with the VALU of u), stage B of u.
+  f32x16 sA, pA, sB, pB;
+  if (n_blk > 0) {
+    sync_tile(0, PD);
+    if (active(0)) block_sdp(0, sA, pA);
+  }
+  auto iteration = [&](int u, f32x16& cs, f32x16& cp, f32x16& ns, f32x16& np) {
+    const bool act = active(u);
+    const bool act_next = active(u + 1);
+    if (act) premask(u, cs);
+    if ((u + 1) % QB == 0) {
+      const int it = (u + 1) / QB;
+      if (it < n_it) {
+        sync_tile(it, PD - 1);
+        if (it + PD < n_it) issue_tile(it + PD);
       }
     }
-
-    if (it + 1 < n_it) store_tile(buf ^ 1);
-    __syncthreads();
+    if (act && act_next)
+      stage_a(u + 1, ns, np, u, cs, cp);
+    else if (act)
+      block_valu(u, cs, cp);
+    else if (act_next)
+      block_sdp(u + 1, ns, np);
+    if (act) stage_b(u);
+  };
+  for (int u = 0; u < n_blk; u += 2) {
+    iteration(u, sA, pA, sB, pB);
+    if (u + 1 < n_blk) iteration(u + 1, sB, pB, sA, pA);
   }
 
   if (key >= p.Sk) return;
@@ -275,173 +421,264 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     }
 }
 
-template <class T, int DP, int BN, int NW, bool CAUSAL>
+// ---------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------
+template <class T, int DP, int BN, int NW, int STAGES, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
-  using Tile = RowTile<DP, BN>;
+  using L = BwdTile<DP, BN>;  // K and V tiles
   constexpr int BM = 32 * NW;
-  constexpr int NT = NW * 64;
-  constexpr int LOADS = Tile::kChunks / NT;
-  static_assert(Tile::kChunks % NT == 0, "tile chunks must divide over the workgroup");
-  constexpr int KD = DP / 16;
-  constexpr int KB = BN / 32;
-  constexpr int DB = DP / 32;
-  constexpr int KN = BN / 16;
+  constexpr int KD = DP / 16;  // k-steps over the head dim (S^T, dP^T)
+  constexpr int KB = BN / 32;  // 32-key blocks per tile
+  constexpr int DB = DP / 32;  // 32-wide head-dim blocks of dQ^T
+  constexpr int KN = BN / 16;  // k-steps over keys (dQ^T)
+  constexpr int LK = L::kSegs / NW;
+  constexpr int kStageBytes = 2 * L::kTileBytes;  // K tile, then V tile
+  constexpr int PD = STAGES - 2;
+  constexpr int RB = L::kRowBytes;
+  static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
+  static_assert(PD >= 1 && PD <= 2, "prefetch distance");
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * 2 * Tile::kWords];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
-  const int bh_count = p.B * p.Hq;
-  const int mblk = p.n_mblocks - 1 - (int)blockIdx.x / bh_count;
-  const int bh = blockIdx.x % bh_count;
+  // Work item: (batch, query head) major, heaviest query block first.
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int bh = w / p.n_mblocks;
+  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
   const int b = bh / p.Hq;
-  const int hq = bh % p.Hq;
-  const int hkv = hq / p.group;
+  const int hkv = (bh - b * p.Hq) / p.group;
   const int m0 = mblk * BM;
   const int mw = m0 + 32 * wave;
   const int row = mw + l32;
   const int diag = p.Sk - p.Sq;
 
-  const uint16_t* kbase = (const uint16_t*)p.k + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
-  const uint16_t* vbase = (const uint16_t*)p.v + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+  const int64_t kv0 = ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+  const uint16_t* kbase = (const uint16_t*)p.k + kv0;
+  const uint16_t* vbase = (const uint16_t*)p.v + kv0;
 
+  uint32_t goff[LK];
+#pragma unroll
+  for (int j = 0; j < LK; ++j) {
+    const int seg = wave + j * NW;
+    const int r = seg * L::kSegRows + lane / L::kCpr;
+    const int c = (lane % L::kCpr) ^ swz_rt<DP>(r);
+    goff[j] = c * 8 < p.D ? (uint32_t)((r * p.D + c * 8) * 2) : kBufferOob;
+  }
+  auto issue_tile = [&](int t) {
+    const int n0 = t * BN;
+    const int bytes = tile_bytes(min(BN, p.Sk - n0), p.D, p.D);
+    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.D, bytes);
+    const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.D, bytes);
+    const uint32_t st = lds_addr(smem) + (t % STAGES) * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < LK; ++j) {
+      const int seg = wave + j * NW;
+      buffer_load_lds_b128(kr, st + seg * 1024, goff[j]);
+      buffer_load_lds_b128(vr, st + L::kTileBytes + seg * 1024, goff[j]);
+    }
+  };
+
+  // Q (sign-flipped for a negative scale) and dO rows as the B operand:
+  // lane holds q[row][16*s + 8*hl .. +7] (zero past S_q and D).
   u32x4 qreg[KD], greg[KD];
   {
-    const int64_t qrow = ((int64_t)bh * p.Sq + row) * p.D;
+    const int qrows = max(0, min(32, p.Sq - mw));
+    const int64_t q0 = ((int64_t)bh * p.Sq + min(mw, p.Sq)) * p.D;
+    // Wave-uniform; readfirstlane keeps the resource in SGPRs (no waterfall loop).
+    const int bytes = __builtin_amdgcn_readfirstlane(tile_bytes(qrows, p.D, p.D));
+    const buf_rsrc qr = make_rsrc((const uint16_t*)p.q + q0, bytes);
+    const buf_rsrc gr = make_rsrc((const uint16_t*)p.dout + q0, bytes);
 #pragma unroll
     for (int s = 0; s < KD; ++s) {
       const int d0 = 16 * s + 8 * hl;
-      u32x4 qx = {0u, 0u, 0u, 0u}, gx = {0u, 0u, 0u, 0u};
-      if (row < p.Sq && d0 < p.D) {
-        qx = ldg_b128_cached((const uint16_t*)p.q + qrow + d0);
-        gx = ldg_b128_cached((const uint16_t*)p.dout + qrow + d0);
-      }
-      qreg[s] = qx;
-      greg[s] = gx;
+      const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.D + d0) * 2) : kBufferOob;
+      qreg[s] = buffer_load_b128(qr, off) ^ p.op_sign;
+      greg[s] = buffer_load_b128(gr, off);
     }
   }
-  const float lse2 = row < p.Sq ? p.lse_log2[(int64_t)bh * p.Sq + row] : __builtin_inff();
-  const float dl = row < p.Sq ? p.delta[(int64_t)bh * p.Sq + row] : 0.f;
+  float lse2 = __builtin_inff(), dl = 0.f;
+  if (row < p.Sq) {
+    lse2 = p.lse_log2[(int64_t)bh * p.Sq + row];
+    dl = p.delta[(int64_t)bh * p.Sq + row];
+  }
 
   int n_end = p.Sk;
   if (CAUSAL) n_end = min(p.Sk, m0 + BM + diag);
   const int n_tiles = n_end > 0 ? (n_end + BN - 1) / BN : 0;
 
-  u32x4 kld[LOADS], vld[LOADS];
-  auto load_tile = [&](int t) {
-    const int nn = t * BN;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * NT;
-      const int r = c / Tile::kChunksPerRow;
-      const int d = (c % Tile::kChunksPerRow) * 8;
-      const int n = nn + r;
-      u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
-      if (n < p.Sk && d < p.D) {
-        kx = ldg_b128_cached(kbase + (int64_t)n * p.D + d);
-        vx = ldg_b128_cached(vbase + (int64_t)n * p.D + d);
-      }
-      kld[i] = kx;
-      vld[i] = vx;
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* ks = smem + buf * 2 * Tile::kWords;
-    uint16_t* vs = ks + Tile::kWords;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * NT;
-      const int r = c / Tile::kChunksPerRow;
-      const int d = (c % Tile::kChunksPerRow) * 8;
-      *reinterpret_cast<u32x4*>(ks + r * Tile::kStride + d) = kld[i];
-      *reinterpret_cast<u32x4*>(vs + r * Tile::kStride + d) = vld[i];
-    }
-  };
+  for (int t = 0; t <= PD; ++t)
+    if (t < n_tiles) issue_tile(t);
 
   f32x16 dqacc[DB];
 #pragma unroll
   for (int c = 0; c < DB; ++c) dqacc[c] = f32x16{};
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
+  // Row-wise A operand of S^T / dP^T: key row l32 (+32 kb), chunk 2s + hl.
+  int k_lds[KD];
+#pragma unroll
+  for (int s = 0; s < KD; ++s) k_lds[s] = l32 * RB + (((2 * s + hl) ^ swz_rt<DP>(l32)) * 16);
+  int kt_lo[DB], kt_hi[DB];
+  tr_offsets<DP, DB>(lane, 0, kt_lo, kt_hi);
 
-  const int a_off = l32 * Tile::kStride + 8 * hl;
-  const int t_off = tr_offset(lane, Tile::kStride);
+  const float c_log2 = p.abs_scale_log2;
   const bool wave_has_rows = mw < p.Sq;
+  auto active = [&](int t) {
+    return t < n_tiles && wave_has_rows && (!CAUSAL || t * BN <= mw + 31 + diag);
+  };
+  auto stage = [&](int t) { return smem + (t % STAGES) * kStageBytes; };
+  auto sync_tile = [&](int t, int max_ahead) {
+    wait_tiles<2 * LK, PD>(min(max_ahead, n_tiles - 1 - t));
+    __syncthreads();
+  };
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
-    const uint16_t* ks = smem + buf * 2 * Tile::kWords;
-    const uint16_t* vs = ks + Tile::kWords;
-    const int nn = t * BN;
-
-    bool active = wave_has_rows;
-    if (CAUSAL) active = active && (nn <= mw + 31 + diag);
-    if (active) {
-      // S^T = K Q^T, dP^T = V dO^T: lane holds [key nn + 32*kb + 8*(r/4) + 4*hl + r%4][query row].
-      f32x16 sacc[KB], pacc[KB];
+  // S^T = K Q^T and dP^T = V dO^T of tile t (no interleave): lane holds
+  // [key t*BN + 32*kb + 8*(r/4) + 4*hl + r%4][query row].
+  auto gemm_sdp = [&](int t, f32x16 (&sd)[KB], f32x16 (&pd)[KB]) {
+    const uint8_t* st = stage(t);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      sd[kb] = f32x16{};
+      pd[kb] = f32x16{};
+    }
+#pragma unroll
+    for (int s = 0; s < KD; ++s)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        sacc[kb] = f32x16{};
-        pacc[kb] = f32x16{};
-#pragma unroll
-        for (int s = 0; s < KD; ++s) {
-          const u32x4 a = lds_read_b128(ks + a_off + 32 * kb * Tile::kStride + 16 * s);
-          sacc[kb] = mfma32<T>(a, qreg[s], sacc[kb]);
-        }
-#pragma unroll
-        for (int s = 0; s < KD; ++s) {
-          const u32x4 a = lds_read_b128(vs + a_off + 32 * kb * Tile::kStride + 16 * s);
-          pacc[kb] = mfma32<T>(a, greg[s], pacc[kb]);
-        }
+        sd[kb] = mfma32<T>(lds_b128(st + k_lds[s] + kb * 32 * RB), qreg[s], sd[kb]);
+        pd[kb] = mfma32<T>(lds_b128(st + L::kTileBytes + k_lds[s] + kb * 32 * RB), greg[s], pd[kb]);
       }
+  };
 
-      const bool edge = (nn + BN > p.Sk) || (CAUSAL && (nn + BN - 1 > mw + diag));
-      int lim = p.Sk - 1;
-      if (CAUSAL) lim = min(lim, row + diag);
-      u32x4 dsk[KN];
+  // Keys past S_k and, under the causal mask, keys past row + diag -> -inf.
+  auto premask = [&](int t, f32x16 (&sd)[KB]) {
+    const int n0 = t * BN;
+    const bool tail = n0 + BN > p.Sk;
+    const bool straddle = CAUSAL && (n0 + BN - 1 > mw + diag);
+    if (!(tail || straddle)) return;
+    int lim = p.Sk - 1;
+    if (CAUSAL) lim = min(lim, row + diag);
+    lim -= n0 + 4 * hl;
 #pragma unroll
-      for (int s2 = 0; s2 < KN; ++s2) {
-        const int kb = s2 >> 1;
-        const int base = 8 * (s2 & 1);
-        float dv[8];
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = base + j;
-          float pe = fast_exp2(fmaf(sacc[kb][r], p.scale_log2, -lse2));
-          if (edge) {
-            const int kk = nn + 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-            if (kk > lim) pe = 0.f;
-          }
-          dv[j] = pe * (pacc[kb][r] - dl);
-        }
-        dsk[s2] = u32x4{pack2<T>(dv[0], dv[1]), pack2<T>(dv[2], dv[3]), pack2<T>(dv[4], dv[5]),
-                        pack2<T>(dv[6], dv[7])};
-      }
+      for (int r = 0; r < 16; ++r)
+        if (32 * kb + 8 * (r >> 2) + (r & 3) > lim) sd[kb][r] = kNegInf;
+  };
 
-      // dQ^T += K^T dS^T: lane holds [d 32*c + 8*(r/4) + 4*hl + r%4][query row].
-#pragma unroll
-      for (int c = 0; c < DB; ++c) {
-#pragma unroll
-        for (int s2 = 0; s2 < KN; ++s2) {
-          const int off = t_off + 16 * s2 * Tile::kStride + 32 * c;
-          const u32x2 lo = lds_read_tr(ks + off);
-          const u32x2 hi = lds_read_tr(ks + off + 8 * Tile::kStride);
-          dqacc[c] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, dsk[s2], dqacc[c]);
-        }
-      }
+  // dS^T of one element, packed eight at a time into the B operand of k-step
+  // x / 8 (keys permuted as the transposed K reads are).
+  u32x4 dsk[KN];
+  float de[KN * 8];
+  auto elem = [&](int x, const f32x16 (&sd)[KB], const f32x16 (&pd)[KB]) {
+    const int kb = x >> 4, r = x & 15;
+    const float pe = fast_exp2(fmaf(sd[kb][r], c_log2, -lse2));
+    de[x] = pe * (pd[kb][r] - dl);
+    if ((x & 7) == 7) {
+      const int b8 = x - 7;
+      dsk[x >> 3] = u32x4{pack2<T>(de[b8], de[b8 + 1]), pack2<T>(de[b8 + 2], de[b8 + 3]),
+                          pack2<T>(de[b8 + 4], de[b8 + 5]), pack2<T>(de[b8 + 6], de[b8 + 7])};
     }
+  };
+  auto tile_valu = [&](const f32x16 (&sd)[KB], const f32x16 (&pd)[KB]) {
+#pragma unroll
+    for (int x = 0; x < KN * 8; ++x) elem(x, sd, pd);
+  };
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
-    __syncthreads();
+  // Stage A: S^T / dP^T MFMAs of tile tn interleaved with the dS elements of
+  // the current tile, fenced per MFMA (see the dK/dV kernel).  MFMA order
+  // cycles over the 2*KB accumulators so consecutive links of one chain are
+  // 2*KB MFMAs apart.
+  auto stage_a = [&](int tn, f32x16 (&sn)[KB], f32x16 (&pn)[KB], const f32x16 (&sd)[KB],
+                     const f32x16 (&pd)[KB]) {
+    constexpr int NM = 2 * KD * KB;
+    constexpr int KLEAD = 3;
+    constexpr int NE = KN * 8;
+    constexpr int EPM = (NE + NM - 1) / NM;
+    const uint8_t* st = stage(tn);
+    auto addr = [&](int i) {
+      const int j = i % (2 * KB);
+      return st + (j / KB) * L::kTileBytes + k_lds[i / (2 * KB)] + (j % KB) * 32 * RB;
+    };
+    u32x4 a[NM];
+#pragma unroll
+    for (int i = 0; i < KLEAD; ++i) a[i] = lds_b128(addr(i));
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      sn[kb] = f32x16{};
+      pn[kb] = f32x16{};
+    }
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + KLEAD < NM) a[i + KLEAD] = lds_b128(addr(i + KLEAD));
+      const int j = i % (2 * KB), s = i / (2 * KB);
+      if (j / KB == 0)
+        sn[j % KB] = mfma32<T>(a[i], qreg[s], sn[j % KB]);
+      else
+        pn[j % KB] = mfma32<T>(a[i], greg[s], pn[j % KB]);
+#pragma unroll
+      for (int k = 0; k < EPM; ++k)
+        if (i * EPM + k < NE) elem(i * EPM + k, sd, pd);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Stage B: dQ^T += K^T dS^T for tile t: lane holds
+  // [d 32*c + 8*(r/4) + 4*hl + r%4][query row].
+  auto gemm_dq = [&](int t) {
+    const uint8_t* st = stage(t);
+    constexpr int NM = DB * KN;
+    constexpr int OLEAD = NM < 5 ? NM : 5;
+    u32x4 kt[KN][DB];
+#pragma unroll
+    for (int s2 = 0; s2 < KN; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c)
+        kt[s2][c] = lds_tr_pair(st + 16 * s2 * RB + kt_lo[c], st + 16 * s2 * RB + kt_hi[c]);
+#pragma unroll
+    for (int s2 = 0; s2 < KN; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c) dqacc[c] = mfma32<T>(kt[s2][c], dsk[s2], dqacc[c]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * OLEAD, 0);
+#pragma unroll
+    for (int i = 0; i < NM - OLEAD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
+  };
+
+  f32x16 s0[KB], p0[KB], s1[KB], p1[KB];
+  if (n_tiles > 0) {
+    sync_tile(0, PD);
+    if (active(0)) gemm_sdp(0, s0, p0);
+  }
+  auto iteration = [&](int t, f32x16 (&cs)[KB], f32x16 (&cp)[KB], f32x16 (&ns)[KB],
+                       f32x16 (&np)[KB]) {
+    const bool act = active(t);
+    const bool act_next = active(t + 1);
+    if (act) premask(t, cs);
+    if (t + 1 < n_tiles) {
+      sync_tile(t + 1, PD - 1);
+      if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
+    }
+    if (act && act_next)
+      stage_a(t + 1, ns, np, cs, cp);
+    else if (act)
+      tile_valu(cs, cp);
+    else if (act_next)
+      gemm_sdp(t + 1, ns, np);
+    if (act) gemm_dq(t);
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    iteration(t, s0, p0, s1, p1);
+    if (t + 1 < n_tiles) iteration(t + 1, s1, p1, s0, p0);
   }
 
   if (row >= p.Sq) return;
@@ -460,56 +697,51 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
     }
 }
 
-// gfx950 tile table for the backward: (padded head dim) ->
-//   dK/dV: output head-dim width DO per workgroup, query tile BMQ, waves NW;
-//   dQ:    key tile BN, waves NW.
-// Four waves per workgroup, one workgroup per CU: the K/V (or Q/dO) operands
-// in registers plus the fp32 accumulators need most of the 512 VGPR+AGPR
-// file of a one-wave-per-SIMD launch.
+// gfx950 tile table for the backward, by head dim (padded to 64, 128 or 256;
+// other dims run zero-padded in the next size up).  Four waves (one per
+// SIMD), 4 ring stages, one workgroup per CU:
+//   dK/dV: 128 keys per workgroup; query tiles of 64 rows (32 at D = 256,
+//          where the output head dim is also split over two workgroups);
+//          ring 4 x (Q + dO + stats) = 72 / 136 / 136 KiB.
+//   dQ:    128 query rows per workgroup; key tiles of 64 rows (32 at
+//          D = 256); ring 4 x (K + V) = 64 / 128 / 128 KiB.
 template <class T, int DP, int DO, int BMQ, int BN>
 static hipError_t launch_bwd_t(const BwdParams& p, bool causal, hipStream_t s) {
   constexpr int NW = 4;
-  const int nb = (p.Sk + 32 * NW - 1) / (32 * NW);
-  const int64_t g_kv = (int64_t)nb * p.B * p.Hkv * (DP / DO);
+  constexpr int STAGES = 4;
   BwdParams q = p;
+  q.n_nblocks = (p.Sk + 32 * NW - 1) / (32 * NW);
   q.n_mblocks = (p.Sq + 32 * NW - 1) / (32 * NW);
+  const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (DP / DO);
   const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
   if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   if (g_kv > 0) {
     if (causal)
-      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, BMQ, NW, true>), dim3((unsigned)g_kv),
+      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, BMQ, NW, STAGES, true>), dim3((unsigned)g_kv),
                          dim3(NW * 64), 0, s, q);
     else
-      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, BMQ, NW, false>), dim3((unsigned)g_kv),
+      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, BMQ, NW, STAGES, false>), dim3((unsigned)g_kv),
                          dim3(NW * 64), 0, s, q);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (g_q > 0) {
     if (causal)
-      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, BN, NW, true>), dim3((unsigned)g_q), dim3(NW * 64),
-                         0, s, q);
+      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, BN, NW, STAGES, true>), dim3((unsigned)g_q),
+                         dim3(NW * 64), 0, s, q);
     else
-      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, BN, NW, false>), dim3((unsigned)g_q), dim3(NW * 64),
-                         0, s, q);
+      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, BN, NW, STAGES, false>), dim3((unsigned)g_q),
+                         dim3(NW * 64), 0, s, q);
   }
   return hipGetLastError();
 }
 
 template <class T>
 static hipError_t launch_bwd_dt(const BwdParams& p, bool causal, hipStream_t s) {
-  switch (padded_head_dim(p.D)) {
-    case 64:
-      return launch_bwd_t<T, 64, 64, 64, 64>(p, causal, s);
-    case 96:
-      return launch_bwd_t<T, 96, 96, 64, 64>(p, causal, s);
-    case 128:
-      return launch_bwd_t<T, 128, 128, 64, 64>(p, causal, s);
-    case 256:
-      return launch_bwd_t<T, 256, 128, 32, 32>(p, causal, s);
-    default:
-      return hipErrorInvalidValue;
-  }
+  if (p.D <= 64) return launch_bwd_t<T, 64, 64, 64, 64>(p, causal, s);
+  if (p.D <= 128) return launch_bwd_t<T, 128, 128, 64, 64>(p, causal, s);
+  if (p.D <= 256) return launch_bwd_t<T, 256, 128, 32, 32>(p, causal, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s) {

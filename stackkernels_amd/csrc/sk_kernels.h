@@ -61,7 +61,12 @@ struct BwdParams {
   float* lse_log2;  // [B*Hq*Sq] fp32 scratch: lse * log2(e) (+inf for empty rows)
   float* dq_acc;    // [B*Hq*Sq*D] fp32 scratch (dQ accumulator) or null
   int B, Hq, Hkv, Sq, Sk, D, group;
-  float scale, scale_log2;
+  float scale, scale_log2;  // signed sm_scale and sm_scale * log2(e)
+  // MFMA kernels: the score exponent uses |sm_scale| * log2(e) (never 0, so a
+  // masked -inf score stays -inf), and op_sign flips the sign bits of the
+  // register-resident score operand when sm_scale < 0.
+  float abs_scale_log2;
+  uint32_t op_sign;
   int n_mblocks, n_nblocks;
 };
 
