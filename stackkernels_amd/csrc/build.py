@@ -9,6 +9,7 @@ streams.  Usage: ``python -m stackkernels_amd.csrc.build`` or ``build()``.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -50,6 +51,25 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+# Kernels that stream tiles with buffer_load ... lds and count their own loads
+# with s_waitcnt vmcnt.  A register spill would add scratch loads to that
+# count, so the waits would no longer cover the tiles: such a build is refused.
+RING_KERNELS = ("fwd_mfma_kernel", "bwd_dkv_kernel", "bwd_dq_kernel", "decode_ring_kernel")
+
+
+def _check_no_scratch(src: str, remarks: str) -> None:
+    name = None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0 and any(k in name for k in RING_KERNELS):
+            raise RuntimeError(f"{src}: kernel {name} spills {m.group(1)} bytes/lane to scratch; "
+                               "its manual vmcnt waits require a spill-free build")
+
+
 def lib_path() -> str:
     return os.path.join(HERE, LIB_NAME)
 
@@ -63,12 +83,14 @@ def build(verbose: bool = False, jobs: int = 5) -> str:
 
     def compile_one(src: str) -> str:
         obj = os.path.join(out_dir, src.replace(".hip", ".o"))
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{HERE}", "-c", os.path.join(HERE, src), "-o", obj]
+        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{HERE}", "-c", os.path.join(HERE, src), "-o", obj,
+               "-Rpass-analysis=kernel-resource-usage"]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+        _check_no_scratch(src, res.stderr)
         return obj
 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:

@@ -129,6 +129,7 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
   static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
   static_assert(QB >= 1 && BMQ <= 64, "32 or 64 queries per tile");
   static_assert(PD >= 1 && PD <= 2, "prefetch distance");
+  static_assert((STAGES & (STAGES - 1)) == 0, "the ring index is a mask");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStageBytes];
 
@@ -188,17 +189,27 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     const int c = (lane % L::kCpr) ^ swz_rt<DP>(r);
     goff[j] = c * 8 < p.D ? (uint32_t)((r * p.D + c * 8) * 2) : kBufferOob;
   }
-  auto tile_head = [&](int it) { return it / n_mt; };
-  auto tile_m0 = [&](int it, int gi) { return m_begin + (it - gi * n_mt) * BMQ; };
-  auto issue_tile = [&](int it) {
-    const int gi = tile_head(it);
-    const int m0 = tile_m0(it, gi);
-    const int64_t bh = (int64_t)b * p.Hq + hkv * p.group + gi;
+  // Tile cursors, (query head gi, first row m0), advanced one tile at a time
+  // (no divisions in the loop): the tile to issue next and the tile whose
+  // blocks are being computed.
+  int issue_gi = 0, issue_m0 = m_begin;
+  int cur_gi = 0, cur_m0 = m_begin;
+  auto advance = [&](int& gi, int& m0) {
+    m0 += BMQ;
+    if (m0 >= p.Sq) {
+      m0 = m_begin;
+      ++gi;
+    }
+  };
+  auto stage = [&](int it) { return smem + (it & (STAGES - 1)) * kStageBytes; };
+  auto issue_next = [&](int it) {
+    const int64_t bh = (int64_t)b * p.Hq + hkv * p.group + issue_gi;
+    const int m0 = issue_m0;
     const int bytes = tile_bytes(min(BMQ, p.Sq - m0), p.D, p.D);
     const int64_t q0 = (bh * p.Sq + m0) * p.D;
     const i32x4 qr = make_rsrc_words((const uint16_t*)p.q + q0, bytes);
     const i32x4 gr = make_rsrc_words((const uint16_t*)p.dout + q0, bytes);
-    const uint32_t st = lds_addr(smem) + (it % STAGES) * kStageBytes;
+    const uint32_t st = lds_addr(stage(it));
 #pragma unroll
     for (int j = 0; j < LQ; ++j) {
       const int seg = wave + j * NW;
@@ -211,11 +222,12 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     const uint32_t sb = st + 2 * L::kTileBytes + wave * kStatBytes;
     buffer_load_lds_b32(lr, sb, lane * 4);
     buffer_load_lds_b32(dr, sb + 256, lane * 4);
+    advance(issue_gi, issue_m0);
   };
 
 #pragma unroll
   for (int t = 0; t <= PD; ++t)
-    if (t < n_it) issue_tile(t);
+    if (t < n_it) issue_next(t);
 
   f32x16 dkacc[DB], dvacc[DB];
 #pragma unroll
@@ -232,36 +244,30 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
   tr_offsets<DP, DB>(lane, d_out0 / 8, tr_lo, tr_hi);
 
   const float c_log2 = p.abs_scale_log2;
-  auto stage = [&](int it) { return smem + (it % STAGES) * kStageBytes; };
-  auto block_m = [&](int u) {
-    const int it = u / QB;
-    return tile_m0(it, tile_head(it)) + 32 * (u % QB);
-  };
-  auto active = [&](int u) {
-    if (u >= n_blk || nw >= p.Sk) return false;
-    return !CAUSAL || nw <= block_m(u) + 31 + diag;
-  };
   auto sync_tile = [&](int it, int max_ahead) {
     wait_tiles<kLoads, PD>(min(max_ahead, n_it - 1 - it));
     __syncthreads();
   };
 
-  // S = Q K^T and dP = dO V^T of block u (no interleave): lane holds
-  // [query 8*(r/4) + 4*hl + r%4][key l32].
-  auto block_sdp = [&](int u, f32x16& sc, f32x16& pc) {
-    const uint8_t* st = stage(u / QB) + (u % QB) * 32 * RB;
+  // Every block runs the same straight-line code.  Under the causal mask a
+  // block the wave cannot see at all, or sees in part, is masked instead of
+  // skipped: its P and dS are exactly zero, so it adds nothing.  Waves whose
+  // keys all lie past S_k compute unused values.
+
+  // S = Q K^T and dP = dO V^T of the block whose rows start at `rows` (no
+  // interleave): lane holds [query 8*(r/4) + 4*hl + r%4][key l32].
+  auto block_sdp = [&](const uint8_t* rows, f32x16& sc, f32x16& pc) {
     sc = f32x16{};
     pc = f32x16{};
 #pragma unroll
     for (int s = 0; s < KD; ++s) {
-      sc = mfma32<T>(lds_b128(st + qa_lds[s]), kreg[s], sc);
-      pc = mfma32<T>(lds_b128(st + L::kTileBytes + qa_lds[s]), vreg[s], pc);
+      sc = mfma32<T>(lds_b128(rows + qa_lds[s]), kreg[s], sc);
+      pc = mfma32<T>(lds_b128(rows + L::kTileBytes + qa_lds[s]), vreg[s], pc);
     }
   };
 
-  // Causal mask of a block on the diagonal: key > query + diag -> -inf.
-  auto premask = [&](int u, f32x16& sc) {
-    const int mq = block_m(u);
+  // Causal mask of the block of queries mq..mq+31: key > query + diag -> -inf.
+  auto premask = [&](int mq, f32x16& sc) {
     if (!CAUSAL || nw + 31 <= mq + diag) return;
     const int lim = key - diag - mq - 4 * hl;  // masked iff 8*(r/4) + r%4 < lim
 #pragma unroll
@@ -269,14 +275,17 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
       if (8 * (r >> 2) + (r & 3) < lim) sc[r] = kNegInf;
   };
 
-  // Row statistics of block u for this lane's 16 queries.
-  auto load_stats = [&](int u, f32x4 (&lv)[4], f32x4 (&dv)[4]) {
-    const uint8_t* sb = stage(u / QB) + 2 * L::kTileBytes + wave * kStatBytes + 128 * (u % QB);
+  // Row statistics of a block (stats = its tile's stat area + 128 * block)
+  // for this lane's 16 queries.
+  auto load_stats = [&](const uint8_t* stats, f32x4 (&lv)[4], f32x4 (&dv)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      lv[i] = *reinterpret_cast<const f32x4*>(sb + 4 * (8 * i + 4 * hl));
-      dv[i] = *reinterpret_cast<const f32x4*>(sb + 256 + 4 * (8 * i + 4 * hl));
+      lv[i] = *reinterpret_cast<const f32x4*>(stats + 4 * (8 * i + 4 * hl));
+      dv[i] = *reinterpret_cast<const f32x4*>(stats + 256 + 4 * (8 * i + 4 * hl));
     }
+  };
+  auto stats_of = [&](int it, int blk) {
+    return stage(it) + 2 * L::kTileBytes + wave * kStatBytes + 128 * blk;
   };
 
   // P and dS of one element, packed eight at a time into the B operands of
@@ -295,36 +304,36 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
                           pack2<T>(de[b8 + 4], de[b8 + 5]), pack2<T>(de[b8 + 6], de[b8 + 7])};
     }
   };
-  auto block_valu = [&](int u, const f32x16& sc, const f32x16& pc) {
+  auto block_valu = [&](const uint8_t* stats, const f32x16& sc, const f32x16& pc) {
     f32x4 lv[4], dv[4];
-    load_stats(u, lv, dv);
+    load_stats(stats, lv, dv);
 #pragma unroll
     for (int r = 0; r < 16; ++r) elem(r, sc, pc, lv, dv);
   };
 
-  // Stage A: S / dP MFMAs of block un (alternating, so each accumulator's
-  // chain has one independent MFMA between its links) interleaved with the
-  // P / dS elements of block uc; fenced per MFMA so the in-order issue keeps
-  // the LDS read KLEAD MFMAs ahead and EPM elements between MFMAs.
-  auto stage_a = [&](int un, f32x16& sn, f32x16& pn, int uc, const f32x16& sc,
-                     const f32x16& pc) {
+  // Stage A: S / dP MFMAs of the next block (alternating, so each
+  // accumulator's chain has one independent MFMA between its links)
+  // interleaved with the P / dS elements of the current block; fenced per
+  // MFMA so the in-order issue keeps the LDS read KLEAD MFMAs ahead and EPM
+  // elements between MFMAs.
+  auto stage_a = [&](const uint8_t* rows_n, f32x16& sn, f32x16& pn, const uint8_t* stats,
+                     const f32x16& sc, const f32x16& pc) {
     constexpr int NM = 2 * KD;
     constexpr int KLEAD = 3;
     constexpr int EPM = (16 + NM - 1) / NM;
-    const uint8_t* st = stage(un / QB) + (un % QB) * 32 * RB;
     f32x4 lv[4], dv[4];
-    load_stats(uc, lv, dv);
+    load_stats(stats, lv, dv);
     u32x4 a[NM];
 #pragma unroll
     for (int i = 0; i < KLEAD; ++i)
-      a[i] = lds_b128(st + (i & 1) * L::kTileBytes + qa_lds[i >> 1]);
+      a[i] = lds_b128(rows_n + (i & 1) * L::kTileBytes + qa_lds[i >> 1]);
     sn = f32x16{};
     pn = f32x16{};
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       if (i + KLEAD < NM) {
         const int n = i + KLEAD;
-        a[n] = lds_b128(st + (n & 1) * L::kTileBytes + qa_lds[n >> 1]);
+        a[n] = lds_b128(rows_n + (n & 1) * L::kTileBytes + qa_lds[n >> 1]);
       }
       if (i & 1)
         pn = mfma32<T>(a[i], vreg[i >> 1], pn);
@@ -337,10 +346,9 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     }
   };
 
-  // Stage B: dV^T += dO^T P and dK^T += Q^T dS for block u: lane holds
-  // [d d_out0 + 32*c + 8*(r/4) + 4*hl + r%4][key l32].
-  auto stage_b = [&](int u) {
-    const uint8_t* st = stage(u / QB) + (u % QB) * 32 * RB;
+  // Stage B: dV^T += dO^T P and dK^T += Q^T dS for the block whose rows
+  // start at `rows`: lane holds [d d_out0 + 32*c + 8*(r/4) + 4*hl + r%4][key l32].
+  auto stage_b = [&](const uint8_t* rows) {
     constexpr int NM = 2 * 2 * DB;
     constexpr int OLEAD = NM < 4 ? NM : 4;
     u32x4 go[2][DB], qo[2][DB];
@@ -348,7 +356,7 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int c = 0; c < DB; ++c) {
-        const uint8_t* r0 = st + 16 * s2 * RB;
+        const uint8_t* r0 = rows + 16 * s2 * RB;
         go[s2][c] = lds_tr_pair(r0 + L::kTileBytes + tr_lo[c], r0 + L::kTileBytes + tr_hi[c]);
         qo[s2][c] = lds_tr_pair(r0 + tr_lo[c], r0 + tr_hi[c]);
       }
@@ -368,36 +376,53 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
     __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
   };
 
-  // Block pipeline.  Iteration u: mask block u, cross into the next tile if
-  // block u + 1 starts one (wait + barrier, then refill the stage tile
-  // it - 1 used), stage A (S/dP of u + 1 with the VALU of u), stage B of u.
-  f32x16 sA, pA, sB, pB;
-  if (n_blk > 0) {
-    sync_tile(0, PD);
-    if (active(0)) block_sdp(0, sA, pA);
-  }
-  auto iteration = [&](int u, f32x16& cs, f32x16& cp, f32x16& ns, f32x16& np) {
-    const bool act = active(u);
-    const bool act_next = active(u + 1);
-    if (act) premask(u, cs);
-    if ((u + 1) % QB == 0) {
-      const int it = (u + 1) / QB;
-      if (it < n_it) {
-        sync_tile(it, PD - 1);
-        if (it + PD < n_it) issue_tile(it + PD);
-      }
-    }
-    if (act && act_next)
-      stage_a(u + 1, ns, np, u, cs, cp);
-    else if (act)
-      block_valu(u, cs, cp);
-    else if (act_next)
-      block_sdp(u + 1, ns, np);
-    if (act) stage_b(u);
+  // Crossing into tile it: its loads landed (vmcnt, then barrier; the barrier
+  // also retires every wave's reads of tile it - 2's stage), then tile
+  // it + PD is issued into that stage.
+  auto enter_tile = [&](int it) {
+    sync_tile(it, PD - 1);
+    if (it + PD < n_it) issue_next(it + PD);
   };
-  for (int u = 0; u < n_blk; u += 2) {
-    iteration(u, sA, pA, sB, pB);
-    if (u + 1 < n_blk) iteration(u + 1, sB, pB, sA, pA);
+
+  f32x16 sA, pA, sB, pB;
+  if constexpr (QB == 2) {
+    // Block pipeline with fixed register roles: block 0 of a tile (rows
+    // 0-31) in (sA, pA), block 1 in (sB, pB), so no scores move between
+    // registers.  One tile per iteration.
+    if (n_it > 0) {
+      sync_tile(0, PD);
+      block_sdp(stage(0), sA, pA);
+    }
+    for (int it = 0; it < n_it; ++it) {
+      const uint8_t* st = stage(it);
+      premask(cur_m0, sA);
+      stage_a(st + 32 * RB, sB, pB, stats_of(it, 0), sA, pA);
+      stage_b(st);
+      premask(cur_m0 + 32, sB);
+      if (it + 1 < n_it) {
+        enter_tile(it + 1);
+        stage_a(stage(it + 1), sA, pA, stats_of(it, 1), sB, pB);
+      } else {
+        block_valu(stats_of(it, 1), sB, pB);
+      }
+      stage_b(st + 32 * RB);
+      advance(cur_gi, cur_m0);
+    }
+  } else {
+    // One 32-query block per tile (D = 256), run in order without the
+    // interleave: the register file holds one score block next to the
+    // larger K/V operands.  Loads run PD + 1 tiles ahead.
+    (void)sB;
+    (void)pB;
+    for (int it = 0; it < n_it; ++it) {
+      sync_tile(it, PD);
+      if (it + PD + 1 < n_it) issue_next(it + PD + 1);
+      block_sdp(stage(it), sA, pA);
+      premask(cur_m0, sA);
+      block_valu(stats_of(it, 0), sA, pA);
+      stage_b(stage(it));
+      advance(cur_gi, cur_m0);
+    }
   }
 
   if (key >= p.Sk) return;
@@ -438,6 +463,7 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
   constexpr int RB = L::kRowBytes;
   static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
   static_assert(PD >= 1 && PD <= 2, "prefetch distance");
+  static_assert((STAGES & (STAGES - 1)) == 0, "the ring index is a mask");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStageBytes];
 
@@ -475,7 +501,7 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
     const int bytes = tile_bytes(min(BN, p.Sk - n0), p.D, p.D);
     const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.D, bytes);
     const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.D, bytes);
-    const uint32_t st = lds_addr(smem) + (t % STAGES) * kStageBytes;
+    const uint32_t st = lds_addr(smem) + (t & (STAGES - 1)) * kStageBytes;
 #pragma unroll
     for (int j = 0; j < LK; ++j) {
       const int seg = wave + j * NW;
@@ -528,11 +554,7 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
   tr_offsets<DP, DB>(lane, 0, kt_lo, kt_hi);
 
   const float c_log2 = p.abs_scale_log2;
-  const bool wave_has_rows = mw < p.Sq;
-  auto active = [&](int t) {
-    return t < n_tiles && wave_has_rows && (!CAUSAL || t * BN <= mw + 31 + diag);
-  };
-  auto stage = [&](int t) { return smem + (t % STAGES) * kStageBytes; };
+  auto stage = [&](int t) { return smem + (t & (STAGES - 1)) * kStageBytes; };
   auto sync_tile = [&](int t, int max_ahead) {
     wait_tiles<2 * LK, PD>(min(max_ahead, n_tiles - 1 - t));
     __syncthreads();
@@ -654,31 +676,46 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
     __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
   };
 
+  // Every tile runs the same straight-line code.  Keys a wave cannot see
+  // (past its rows' diagonal or past S_k) are masked, not skipped: their dS
+  // is exactly zero.  Waves with no rows (past S_q) compute unused values.
   f32x16 s0[KB], p0[KB], s1[KB], p1[KB];
-  if (n_tiles > 0) {
-    sync_tile(0, PD);
-    if (active(0)) gemm_sdp(0, s0, p0);
-  }
-  auto iteration = [&](int t, f32x16 (&cs)[KB], f32x16 (&cp)[KB], f32x16 (&ns)[KB],
-                       f32x16 (&np)[KB]) {
-    const bool act = active(t);
-    const bool act_next = active(t + 1);
-    if (act) premask(t, cs);
-    if (t + 1 < n_tiles) {
-      sync_tile(t + 1, PD - 1);
-      if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
+  if constexpr (DP <= 128) {
+    // Fixed register roles: even tiles in s0/p0, odd tiles in s1/p1.
+    if (n_tiles > 0) {
+      sync_tile(0, PD);
+      gemm_sdp(0, s0, p0);
     }
-    if (act && act_next)
-      stage_a(t + 1, ns, np, cs, cp);
-    else if (act)
-      tile_valu(cs, cp);
-    else if (act_next)
-      gemm_sdp(t + 1, ns, np);
-    if (act) gemm_dq(t);
-  };
-  for (int t = 0; t < n_tiles; t += 2) {
-    iteration(t, s0, p0, s1, p1);
-    if (t + 1 < n_tiles) iteration(t + 1, s1, p1, s0, p0);
+    auto iteration = [&](int t, f32x16 (&cs)[KB], f32x16 (&cp)[KB], f32x16 (&ns)[KB],
+                         f32x16 (&np)[KB]) {
+      premask(t, cs);
+      if (t + 1 < n_tiles) {
+        sync_tile(t + 1, PD - 1);
+        if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
+        stage_a(t + 1, ns, np, cs, cp);
+      } else {
+        tile_valu(cs, cp);
+      }
+      gemm_dq(t);
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+      iteration(t, s0, p0, s1, p1);
+      if (t + 1 < n_tiles) iteration(t + 1, s1, p1, s0, p0);
+    }
+  } else {
+    // D = 256: tiles run in order without the interleave (the register file
+    // holds one score tile next to the larger Q/dO operands); loads run
+    // PD + 1 tiles ahead.
+    (void)s1;
+    (void)p1;
+    for (int t = 0; t < n_tiles; ++t) {
+      sync_tile(t, PD);
+      if (t + PD + 1 < n_tiles) issue_tile(t + PD + 1);
+      gemm_sdp(t, s0, p0);
+      premask(t, s0);
+      tile_valu(s0, p0);
+      gemm_dq(t);
+    }
   }
 
   if (row >= p.Sq) return;
