@@ -449,8 +449,8 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
-template <class T, int DP, int BN, int NW, int STAGES, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
+template <class T, int DP, int BN, int NW, int STAGES, int OCC, bool PIPE, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
   using L = BwdTile<DP, BN>;  // K and V tiles
   constexpr int BM = 32 * NW;
   constexpr int KD = DP / 16;  // k-steps over the head dim (S^T, dP^T)
@@ -680,7 +680,7 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
   // (past its rows' diagonal or past S_k) are masked, not skipped: their dS
   // is exactly zero.  Waves with no rows (past S_q) compute unused values.
   f32x16 s0[KB], p0[KB], s1[KB], p1[KB];
-  if constexpr (DP <= 128) {
+  if constexpr (PIPE) {
     // Fixed register roles: even tiles in s0/p0, odd tiles in s1/p1.
     if (n_tiles > 0) {
       sync_tile(0, PD);
@@ -703,9 +703,9 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
       if (t + 1 < n_tiles) iteration(t + 1, s1, p1, s0, p0);
     }
   } else {
-    // D = 256: tiles run in order without the interleave (the register file
-    // holds one score tile next to the larger Q/dO operands); loads run
-    // PD + 1 tiles ahead.
+    // Tiles in order without the interleave: the other resident wave of the
+    // SIMD (two workgroups per CU), or at D = 256 nothing, overlaps the VALU
+    // work with MFMAs; one score tile is live.  Loads run PD + 1 tiles ahead.
     (void)s1;
     (void)p1;
     for (int t = 0; t < n_tiles; ++t) {
@@ -742,10 +742,26 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dq_kernel(BwdParams p) {
 //          ring 4 x (Q + dO + stats) = 72 / 136 / 136 KiB.
 //   dQ:    128 query rows per workgroup; key tiles of 64 rows (32 at
 //          D = 256); ring 4 x (K + V) = 64 / 128 / 128 KiB.
-template <class T, int DP, int DO, int BMQ, int BN>
+// dQ kernel table by padded head dim: key tile, workgroups per CU, and
+// whether a wave interleaves its own softmax with the next tile's MFMAs.
+template <int DP>
+struct DqConfig {
+  static constexpr int kBn = 32;
+  static constexpr int kOcc = 2;
+  static constexpr bool kPipe = false;
+};
+template <>
+struct DqConfig<256> {
+  static constexpr int kBn = 32;
+  static constexpr int kOcc = 1;
+  static constexpr bool kPipe = false;
+};
+
+template <class T, int DP, int DO, int BMQ>
 static hipError_t launch_bwd_t(const BwdParams& p, bool causal, hipStream_t s) {
   constexpr int NW = 4;
   constexpr int STAGES = 4;
+  using QC = DqConfig<DP>;
   BwdParams q = p;
   q.n_nblocks = (p.Sk + 32 * NW - 1) / (32 * NW);
   q.n_mblocks = (p.Sq + 32 * NW - 1) / (32 * NW);
@@ -764,20 +780,20 @@ static hipError_t launch_bwd_t(const BwdParams& p, bool causal, hipStream_t s) {
   }
   if (g_q > 0) {
     if (causal)
-      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, BN, NW, STAGES, true>), dim3((unsigned)g_q),
-                         dim3(NW * 64), 0, s, q);
+      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, true>),
+                         dim3((unsigned)g_q), dim3(NW * 64), 0, s, q);
     else
-      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, BN, NW, STAGES, false>), dim3((unsigned)g_q),
-                         dim3(NW * 64), 0, s, q);
+      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, false>),
+                         dim3((unsigned)g_q), dim3(NW * 64), 0, s, q);
   }
   return hipGetLastError();
 }
 
 template <class T>
 static hipError_t launch_bwd_dt(const BwdParams& p, bool causal, hipStream_t s) {
-  if (p.D <= 64) return launch_bwd_t<T, 64, 64, 64, 64>(p, causal, s);
-  if (p.D <= 128) return launch_bwd_t<T, 128, 128, 64, 64>(p, causal, s);
-  if (p.D <= 256) return launch_bwd_t<T, 256, 128, 32, 32>(p, causal, s);
+  if (p.D <= 64) return launch_bwd_t<T, 64, 64, 64>(p, causal, s);
+  if (p.D <= 128) return launch_bwd_t<T, 128, 128, 64>(p, causal, s);
+  if (p.D <= 256) return launch_bwd_t<T, 256, 128, 32>(p, causal, s);
   return hipErrorInvalidValue;
 }
 
