@@ -112,30 +112,51 @@ __device__ __forceinline__ u32x4 lds_tr_pair(const uint8_t* lo, const uint8_t* h
 // ---------------------------------------------------------------------------
 // dK / dV
 // ---------------------------------------------------------------------------
-template <class T, int DP, int DO, int BMQ, int NW, int STAGES, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
+// Eight waves: key group kg = wave % 4 (32 keys) and role = wave / 4, so the
+// two waves of a key group share a SIMD.  Role 0 holds K and computes
+// S = Q K^T, P and dV^T += dO^T P for query tile j; role 1 holds V and
+// finishes tile j - 1 (dS = P (dP - delta) with the P role 0 left in LDS,
+// dK^T += Q^T dS) before computing dP = dO V^T of tile j, so the two waves of
+// a SIMD alternate VALU and MFMA phases.  Each wave keeps half of a key
+// group's accumulators, so both fit the 256 registers of a two-waves-per-SIMD
+// launch and every MFMA result lands in VGPRs.
+//
+// LDS is region-major -- all Q tiles, all dO tiles, the row statistics, the
+// P exchange -- and the step loop is unrolled by the ring depth, so every
+// LDS access is a lane-constant register plus a compile-time offset.
+template <class T, int DP, int DO, int STAGES, bool CAUSAL>
+__global__ void __launch_bounds__(512, 1) bwd_dkv_kernel(BwdParams p) {
+  constexpr int NW = 8;
+  constexpr int BMQ = 32;  // queries per tile (one 32x32 score block per wave)
   using L = BwdTile<DP, BMQ>;  // Q and dO tiles
-  constexpr int BNK = 32 * NW;
+  constexpr int BNK = 128;
   constexpr int KD = DP / 16;  // k-steps over the head dim (S, dP)
-  constexpr int QB = BMQ / 32;  // 32-query blocks per tile
   constexpr int DB = DO / 32;  // 32-wide output head-dim blocks
-  constexpr int LQ = L::kSegs / NW;  // Q (and dO) segments per wave per tile
-  constexpr int kStatBytes = 512;  // per wave: 64 lse*log2e, then 64 delta
-  constexpr int kStageBytes = 2 * L::kTileBytes + NW * kStatBytes;
-  constexpr int kLoads = 2 * LQ + 2;  // DMAs per wave per tile
-  constexpr int PD = STAGES - 2;
-  constexpr int kDSplit = DP / DO;
+  constexpr int LS = 2 * L::kSegs / NW;  // Q + dO segments per wave per tile
+  constexpr int QT = L::kTileBytes;
   constexpr int RB = L::kRowBytes;
-  static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
-  static_assert(QB >= 1 && BMQ <= 64, "32 or 64 queries per tile");
-  static_assert(PD >= 1 && PD <= 2, "prefetch distance");
-  static_assert((STAGES & (STAGES - 1)) == 0, "the ring index is a mask");
+  constexpr int kStatStage = NW * 256;  // per stage: each wave's 64 floats
+  constexpr bool kPF32 = DP <= 128;  // P exchanged in fp32 (else 16-bit)
+  constexpr int kPBlock = kPF32 ? 4096 : 2048;  // one key group's 32x32 P
+  constexpr int kQReg = 0;
+  constexpr int kDReg = STAGES * QT;
+  constexpr int kSReg = 2 * STAGES * QT;
+  constexpr int kPReg = kSReg + STAGES * kStatStage;
+  constexpr int kLds = kPReg + 2 * 4 * kPBlock;
+  constexpr int kLoads = LS + 1;  // DMAs per wave per tile
+  constexpr int PD = 2;  // tiles issued ahead
+  constexpr int kDSplit = DP / DO;
+  static_assert(STAGES == 4, "the unrolled step loop assumes a 4-deep ring");
+  static_assert((2 * L::kSegs) % NW == 0, "tile segments must divide over the waves");
+  static_assert(3 * QT + 16 * RB < 65536, "stage offsets must fit the ds immediate");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = wave & 3;
+  const int role = wave >> 2;
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
@@ -150,27 +171,26 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
   const int b = bk / p.Hkv;
   const int hkv = bk - b * p.Hkv;
   const int n0 = nblk * BNK;
-  const int nw = n0 + 32 * wave;
+  const int nw = n0 + 32 * kg;
   const int key = nw + l32;
   const int diag = p.Sk - p.Sq;
   const int d_out0 = dsp * DO;
 
-  // K (sign-flipped for a negative scale) and V rows of this lane's key as
-  // the B operand: k[key][16*s + 8*hl .. +7].
-  u32x4 kreg[KD], vreg[KD];
+  // Resident B operand, rows of this lane's key: K (sign-flipped for a
+  // negative scale) for role 0, V for role 1: x[key][16*s + 8*hl .. +7].
+  u32x4 kv[KD];
   {
     const int krows = max(0, min(32, p.Sk - nw));
     const int64_t k0 = ((int64_t)bk * p.Sk + min(nw, p.Sk)) * p.D;
-    // Wave-uniform; readfirstlane keeps the resource in SGPRs (no waterfall loop).
     const int bytes = __builtin_amdgcn_readfirstlane(tile_bytes(krows, p.D, p.D));
-    const buf_rsrc kr = make_rsrc((const uint16_t*)p.k + k0, bytes);
-    const buf_rsrc vr = make_rsrc((const uint16_t*)p.v + k0, bytes);
+    const uint16_t* src = (const uint16_t*)(role == 0 ? p.k : p.v) + k0;
+    const uint32_t sgn = role == 0 ? p.op_sign : 0u;
+    const buf_rsrc r = make_rsrc(src, bytes);
 #pragma unroll
     for (int s = 0; s < KD; ++s) {
       const int d0 = 16 * s + 8 * hl;
       const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.D + d0) * 2) : kBufferOob;
-      kreg[s] = buffer_load_b128(kr, off) ^ p.op_sign;
-      vreg[s] = buffer_load_b128(vr, off);
+      kv[s] = buffer_load_b128(r, off) ^ sgn;
     }
   }
 
@@ -179,269 +199,243 @@ __global__ void __launch_bounds__(NW * 64, 1) bwd_dkv_kernel(BwdParams p) {
   if (CAUSAL) m_begin = max(0, n0 - diag) / BMQ * BMQ;
   const int n_mt = m_begin < p.Sq ? (p.Sq - m_begin + BMQ - 1) / BMQ : 0;
   const int n_it = p.group * n_mt;
-  const int n_blk = n_it * QB;
 
-  uint32_t goff[LQ];
+  // DMA: segment j of this wave is segment wave + 8j of the tile pair (Q
+  // segments first, then dO); its LDS target and lane source offsets.
+  uint32_t goff[LS];
 #pragma unroll
-  for (int j = 0; j < LQ; ++j) {
-    const int seg = wave + j * NW;
+  for (int j = 0; j < LS; ++j) {
+    const int seg = (wave + j * NW) % L::kSegs;
     const int r = seg * L::kSegRows + lane / L::kCpr;
     const int c = (lane % L::kCpr) ^ swz_rt<DP>(r);
     goff[j] = c * 8 < p.D ? (uint32_t)((r * p.D + c * 8) * 2) : kBufferOob;
   }
-  // Tile cursors, (query head gi, first row m0), advanced one tile at a time
-  // (no divisions in the loop): the tile to issue next and the tile whose
-  // blocks are being computed.
-  int issue_gi = 0, issue_m0 = m_begin;
-  int cur_gi = 0, cur_m0 = m_begin;
-  auto advance = [&](int& gi, int& m0) {
-    m0 += BMQ;
-    if (m0 >= p.Sq) {
-      m0 = m_begin;
-      ++gi;
-    }
-  };
-  auto stage = [&](int it) { return smem + (it & (STAGES - 1)) * kStageBytes; };
-  auto issue_next = [&](int it) {
-    const int64_t bh = (int64_t)b * p.Hq + hkv * p.group + issue_gi;
-    const int m0 = issue_m0;
-    const int bytes = tile_bytes(min(BMQ, p.Sq - m0), p.D, p.D);
-    const int64_t q0 = (bh * p.Sq + m0) * p.D;
-    const i32x4 qr = make_rsrc_words((const uint16_t*)p.q + q0, bytes);
-    const i32x4 gr = make_rsrc_words((const uint16_t*)p.dout + q0, bytes);
-    const uint32_t st = lds_addr(stage(it));
+  // Issue cursor: query head, first row, and that row's index in [B*Hq*Sq].
+  const int64_t bh0 = (int64_t)b * p.Hq + hkv * p.group;
+  int iss_gi = 0, iss_m0 = m_begin;
+  int64_t iss_row = bh0 * p.Sq + m_begin;
+  const float* stat_src = role == 0 ? p.lse_log2 : p.delta;  // role 0: lse*log2e
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int stg) {
+    const int bytes = tile_bytes(min(BMQ, p.Sq - iss_m0), p.D, p.D);
+    const int64_t e0 = iss_row * p.D;
+    const i32x4 qr = make_rsrc_words((const uint16_t*)p.q + e0, bytes);
+    const i32x4 gr = make_rsrc_words((const uint16_t*)p.dout + e0, bytes);
 #pragma unroll
-    for (int j = 0; j < LQ; ++j) {
+    for (int j = 0; j < LS; ++j) {
       const int seg = wave + j * NW;
-      buffer_load_lds_b128(qr, st + seg * 1024, goff[j]);
-      buffer_load_lds_b128(gr, st + L::kTileBytes + seg * 1024, goff[j]);
+      const bool is_do = seg >= L::kSegs;  // wave-uniform
+      const int sseg = is_do ? seg - L::kSegs : seg;
+      buffer_load_lds_b128(is_do ? gr : qr,
+                           lds0 + (is_do ? kDReg : kQReg) + stg * QT + sseg * 1024, goff[j]);
     }
-    const int sbytes = min(64, p.Sq - m0) * 4;
-    const i32x4 lr = make_rsrc_words(p.lse_log2 + bh * p.Sq + m0, sbytes);
-    const i32x4 dr = make_rsrc_words(p.delta + bh * p.Sq + m0, sbytes);
-    const uint32_t sb = st + 2 * L::kTileBytes + wave * kStatBytes;
-    buffer_load_lds_b32(lr, sb, lane * 4);
-    buffer_load_lds_b32(dr, sb + 256, lane * 4);
-    advance(issue_gi, issue_m0);
+    const i32x4 sr = make_rsrc_words(stat_src + iss_row, min(64, p.Sq - iss_m0) * 4);
+    buffer_load_lds_b32(sr, lds0 + kSReg + stg * kStatStage + wave * 256, lane * 4);
+    iss_m0 += BMQ;
+    iss_row += BMQ;
+    if (iss_m0 >= p.Sq) {
+      iss_m0 = m_begin;
+      ++iss_gi;
+      iss_row = (bh0 + iss_gi) * p.Sq + m_begin;
+    }
   };
 
+  f32x16 acc[DB];  // role 0: dV^T, role 1: dK^T
 #pragma unroll
-  for (int t = 0; t <= PD; ++t)
-    if (t < n_it) issue_next(t);
+  for (int c = 0; c < DB; ++c) acc[c] = f32x16{};
 
-  f32x16 dkacc[DB], dvacc[DB];
+  // Lane-constant LDS byte addresses.  Row-wise A operand (query row l32,
+  // chunk 2s + hl) of S (role 0: Q region) or dP (role 1: dO region);
+  // transposed operand of dV (role 0: dO region) or dK (role 1: Q region).
+  const int row_reg = role == 0 ? kQReg : kDReg;
+  const int tr_reg = role == 0 ? kDReg : kQReg;
+  int row_lds[KD];
 #pragma unroll
-  for (int c = 0; c < DB; ++c) {
-    dkacc[c] = f32x16{};
-    dvacc[c] = f32x16{};
-  }
-
-  // Row-wise A operand of S / dP: query row l32 (+32 per block), chunk 2s + hl.
-  int qa_lds[KD];
-#pragma unroll
-  for (int s = 0; s < KD; ++s) qa_lds[s] = l32 * RB + (((2 * s + hl) ^ swz_rt<DP>(l32)) * 16);
+  for (int s = 0; s < KD; ++s)
+    row_lds[s] = row_reg + l32 * RB + (((2 * s + hl) ^ swz_rt<DP>(l32)) * 16);
   int tr_lo[DB], tr_hi[DB];
   tr_offsets<DP, DB>(lane, d_out0 / 8, tr_lo, tr_hi);
-
+#pragma unroll
+  for (int c = 0; c < DB; ++c) {
+    tr_lo[c] += tr_reg;
+    tr_hi[c] += tr_reg;
+  }
+  // This wave's statistics copy (queries 8*i + 4*hl .. +3 at +32*i) and its
+  // key group's P block (16-byte chunk k of every lane at +1024*k).
+  const int stat_lds = kSReg + wave * 256 + 16 * hl;
+  const int p_lds = kPReg + kg * kPBlock + lane * 16;
   const float c_log2 = p.abs_scale_log2;
-  auto sync_tile = [&](int it, int max_ahead) {
-    wait_tiles<kLoads, PD>(min(max_ahead, n_it - 1 - it));
-    __syncthreads();
+
+  auto ld128 = [&](int addr) { return *reinterpret_cast<const u32x4*>(smem + addr); };
+  auto ldf4 = [&](int addr) { return *reinterpret_cast<const f32x4*>(smem + addr); };
+  // x[query][key] = X Y^T over the row-wise operand of stage stg and the
+  // register operand: lane holds [query 8*(r/4) + 4*hl + r%4][key l32].
+  auto score = [&](int stg) {
+    u32x4 a[KD];
+#pragma unroll
+    for (int s = 0; s < KD; ++s) a[s] = ld128(row_lds[s] + stg * QT);
+    f32x16 sc = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KD; ++s) sc = mfma32<T>(a[s], kv[s], sc);
+    return sc;
+  };
+  // acc^T += X^T G, X^T read transposed from stage stg, G the packed B
+  // operand (P or dS) of the two 16-query k-steps.
+  auto accumulate = [&](int stg, const u32x4 (&g)[2]) {
+    u32x4 x[2][DB];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c) {
+        const int o = stg * QT + 16 * s2 * RB;
+        x[s2][c] = lds_tr_pair(smem + tr_lo[c] + o, smem + tr_hi[c] + o);
+      }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c) acc[c] = mfma32<T>(x[s2][c], g[s2], acc[c]);
+  };
+  auto pack16 = [&](const float (&v)[16], u32x4 (&g)[2]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      g[s2] = u32x4{pack2<T>(v[8 * s2], v[8 * s2 + 1]), pack2<T>(v[8 * s2 + 2], v[8 * s2 + 3]),
+                    pack2<T>(v[8 * s2 + 4], v[8 * s2 + 5]), pack2<T>(v[8 * s2 + 6], v[8 * s2 + 7])};
   };
 
-  // Every block runs the same straight-line code.  Under the causal mask a
-  // block the wave cannot see at all, or sees in part, is masked instead of
-  // skipped: its P and dS are exactly zero, so it adds nothing.  Waves whose
-  // keys all lie past S_k compute unused values.
-
-  // S = Q K^T and dP = dO V^T of the block whose rows start at `rows` (no
-  // interleave): lane holds [query 8*(r/4) + 4*hl + r%4][key l32].
-  auto block_sdp = [&](const uint8_t* rows, f32x16& sc, f32x16& pc) {
-    sc = f32x16{};
-    pc = f32x16{};
+  // Role 0, tile in stage stg (P buffer pb): S, causal mask, P =
+  // exp2(S*scale*log2e - lse*log2e), published for role 1, dV^T += dO^T P.
+  int cur_gi = 0, cur_m0 = m_begin;  // role 0's tile
+  auto step0 = [&](int stg, int pbi) {
+    f32x16 sc = score(stg);
+    if (CAUSAL && nw + 31 > cur_m0 + diag) {
+      const int lim = key - diag - cur_m0 - 4 * hl;  // masked iff 8*(r/4) + r%4 < lim
 #pragma unroll
-    for (int s = 0; s < KD; ++s) {
-      sc = mfma32<T>(lds_b128(rows + qa_lds[s]), kreg[s], sc);
-      pc = mfma32<T>(lds_b128(rows + L::kTileBytes + qa_lds[s]), vreg[s], pc);
+      for (int r = 0; r < 16; ++r)
+        if (8 * (r >> 2) + (r & 3) < lim) sc[r] = kNegInf;
     }
-  };
-
-  // Causal mask of the block of queries mq..mq+31: key > query + diag -> -inf.
-  auto premask = [&](int mq, f32x16& sc) {
-    if (!CAUSAL || nw + 31 <= mq + diag) return;
-    const int lim = key - diag - mq - 4 * hl;  // masked iff 8*(r/4) + r%4 < lim
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (8 * (r >> 2) + (r & 3) < lim) sc[r] = kNegInf;
-  };
-
-  // Row statistics of a block (stats = its tile's stat area + 128 * block)
-  // for this lane's 16 queries.
-  auto load_stats = [&](const uint8_t* stats, f32x4 (&lv)[4], f32x4 (&dv)[4]) {
+    float pe[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      lv[i] = *reinterpret_cast<const f32x4*>(stats + 4 * (8 * i + 4 * hl));
-      dv[i] = *reinterpret_cast<const f32x4*>(stats + 256 + 4 * (8 * i + 4 * hl));
+      const f32x4 lv = ldf4(stat_lds + stg * kStatStage + 32 * i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pe[4 * i + k] = fast_exp2(fmaf(sc[4 * i + k], c_log2, -lv[k]));
+    }
+    u32x4 pk[2];
+    pack16(pe, pk);
+    uint8_t* pb = smem + p_lds + pbi * 4 * kPBlock;
+    if constexpr (kPF32) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<f32x4*>(pb + 1024 * k) = f32x4{pe[4 * k], pe[4 * k + 1], pe[4 * k + 2], pe[4 * k + 3]};
+    } else {
+      *reinterpret_cast<u32x4*>(pb) = pk[0];
+      *reinterpret_cast<u32x4*>(pb + 1024) = pk[1];
+    }
+    accumulate(stg, pk);
+    cur_m0 += BMQ;
+    if (cur_m0 >= p.Sq) {
+      cur_m0 = m_begin;
+      ++cur_gi;
     }
   };
-  auto stats_of = [&](int it, int blk) {
-    return stage(it) + 2 * L::kTileBytes + wave * kStatBytes + 128 * blk;
-  };
-
-  // P and dS of one element, packed eight at a time into the B operands of
-  // the k-step s2 = r / 8 (queries permuted as the transposed reads are).
-  u32x4 pk[2], dsk[2];
-  float pe[16], de[16];
-  auto elem = [&](int r, const f32x16& sc, const f32x16& pc, const f32x4 (&lv)[4],
-                  const f32x4 (&dv)[4]) {
-    pe[r] = fast_exp2(fmaf(sc[r], c_log2, -lv[r >> 2][r & 3]));
-    de[r] = pe[r] * (pc[r] - dv[r >> 2][r & 3]);
-    if ((r & 7) == 7) {
-      const int b8 = r - 7;
-      pk[r >> 3] = u32x4{pack2<T>(pe[b8], pe[b8 + 1]), pack2<T>(pe[b8 + 2], pe[b8 + 3]),
-                         pack2<T>(pe[b8 + 4], pe[b8 + 5]), pack2<T>(pe[b8 + 6], pe[b8 + 7])};
-      dsk[r >> 3] = u32x4{pack2<T>(de[b8], de[b8 + 1]), pack2<T>(de[b8 + 2], de[b8 + 3]),
-                          pack2<T>(de[b8 + 4], de[b8 + 5]), pack2<T>(de[b8 + 6], de[b8 + 7])};
-    }
-  };
-  auto block_valu = [&](const uint8_t* stats, const f32x16& sc, const f32x16& pc) {
-    f32x4 lv[4], dv[4];
-    load_stats(stats, lv, dv);
+  // Role 1, tile in stage stg (P buffer pbi): dS = P (dP - delta) with the
+  // dP of that tile (computed one step earlier, or here at D = 256 where
+  // registers are short), then dK^T += Q^T dS.
+  constexpr bool kSkew = DP <= 128;
+  f32x16 dp = f32x16{};
+  auto step1 = [&](int stg, int pbi) {
+    if constexpr (!kSkew) dp = score(stg);
+    const uint8_t* pb = smem + p_lds + pbi * 4 * kPBlock;
+    float pr[16];
+    if constexpr (kPF32) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) elem(r, sc, pc, lv, dv);
-  };
-
-  // Stage A: S / dP MFMAs of the next block (alternating, so each
-  // accumulator's chain has one independent MFMA between its links)
-  // interleaved with the P / dS elements of the current block; fenced per
-  // MFMA so the in-order issue keeps the LDS read KLEAD MFMAs ahead and EPM
-  // elements between MFMAs.
-  auto stage_a = [&](const uint8_t* rows_n, f32x16& sn, f32x16& pn, const uint8_t* stats,
-                     const f32x16& sc, const f32x16& pc) {
-    constexpr int NM = 2 * KD;
-    constexpr int KLEAD = 3;
-    constexpr int EPM = (16 + NM - 1) / NM;
-    f32x4 lv[4], dv[4];
-    load_stats(stats, lv, dv);
-    u32x4 a[NM];
+      for (int k = 0; k < 4; ++k) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(pb + 1024 * k);
 #pragma unroll
-    for (int i = 0; i < KLEAD; ++i)
-      a[i] = lds_b128(rows_n + (i & 1) * L::kTileBytes + qa_lds[i >> 1]);
-    sn = f32x16{};
-    pn = f32x16{};
-#pragma unroll
-    for (int i = 0; i < NM; ++i) {
-      if (i + KLEAD < NM) {
-        const int n = i + KLEAD;
-        a[n] = lds_b128(rows_n + (n & 1) * L::kTileBytes + qa_lds[n >> 1]);
+        for (int e = 0; e < 4; ++e) pr[4 * k + e] = v[e];
       }
-      if (i & 1)
-        pn = mfma32<T>(a[i], vreg[i >> 1], pn);
-      else
-        sn = mfma32<T>(a[i], kreg[i >> 1], sn);
+    } else {
 #pragma unroll
-      for (int k = 0; k < EPM; ++k)
-        if (i * EPM + k < 16) elem(i * EPM + k, sc, pc, lv, dv);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(pb + 1024 * h);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pr[8 * h + e] = to_f32<T>((uint16_t)((e & 1) ? (v[e >> 1] >> 16) : (v[e >> 1] & 0xffffu)));
+      }
     }
+    float de[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 dv = ldf4(stat_lds + stg * kStatStage + 32 * i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) de[4 * i + k] = pr[4 * i + k] * (dp[4 * i + k] - dv[k]);
+    }
+    u32x4 dsk[2];
+    pack16(de, dsk);
+    accumulate(stg, dsk);
   };
 
-  // Stage B: dV^T += dO^T P and dK^T += Q^T dS for the block whose rows
-  // start at `rows`: lane holds [d d_out0 + 32*c + 8*(r/4) + 4*hl + r%4][key l32].
-  auto stage_b = [&](const uint8_t* rows) {
-    constexpr int NM = 2 * 2 * DB;
-    constexpr int OLEAD = NM < 4 ? NM : 4;
-    u32x4 go[2][DB], qo[2][DB];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int c = 0; c < DB; ++c) {
-        const uint8_t* r0 = rows + 16 * s2 * RB;
-        go[s2][c] = lds_tr_pair(r0 + L::kTileBytes + tr_lo[c], r0 + L::kTileBytes + tr_hi[c]);
-        qo[s2][c] = lds_tr_pair(r0 + tr_lo[c], r0 + tr_hi[c]);
-      }
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int c = 0; c < DB; ++c) {
-        dvacc[c] = mfma32<T>(go[s2][c], pk[s2], dvacc[c]);
-        dkacc[c] = mfma32<T>(qo[s2][c], dsk[s2], dkacc[c]);
-      }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * OLEAD, 0);
-#pragma unroll
-    for (int i = 0; i < NM - OLEAD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
+  // Step j: role 0 works on tile j; role 1 finishes tile j - 1 and computes
+  // dP of tile j.  At the start of a step, tile j has landed (vmcnt, then the
+  // barrier, which also publishes role 0's P of tile j - 1 and retires every
+  // read of tile j - 2), and tile j + 2 is issued into tile j - 2's stage.
+  // Tile t lives in stage t % 4 and its P in buffer t % 2.  Steps 0 and n_it
+  // (one role idle) are peeled; the steps in between run unconditionally in
+  // a loop unrolled by 4, so stages and buffers are compile-time constants
+  // and no accumulator moves between registers.
+  auto begin_step = [&](int j, int issue_stage) {
+    if (j + 1 < n_it)
+      wait_vmcnt<kLoads>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    if (j + PD < n_it) issue(issue_stage);
   };
-
-  // Crossing into tile it: its loads landed (vmcnt, then barrier; the barrier
-  // also retires every wave's reads of tile it - 2's stage), then tile
-  // it + PD is issued into that stage.
-  auto enter_tile = [&](int it) {
-    sync_tile(it, PD - 1);
-    if (it + PD < n_it) issue_next(it + PD);
-  };
-
-  f32x16 sA, pA, sB, pB;
-  if constexpr (QB == 2) {
-    // Block pipeline with fixed register roles: block 0 of a tile (rows
-    // 0-31) in (sA, pA), block 1 in (sB, pB), so no scores move between
-    // registers.  One tile per iteration.
-    if (n_it > 0) {
-      sync_tile(0, PD);
-      block_sdp(stage(0), sA, pA);
-    }
-    for (int it = 0; it < n_it; ++it) {
-      const uint8_t* st = stage(it);
-      premask(cur_m0, sA);
-      stage_a(st + 32 * RB, sB, pB, stats_of(it, 0), sA, pA);
-      stage_b(st);
-      premask(cur_m0 + 32, sB);
-      if (it + 1 < n_it) {
-        enter_tile(it + 1);
-        stage_a(stage(it + 1), sA, pA, stats_of(it, 1), sB, pB);
-      } else {
-        block_valu(stats_of(it, 1), sB, pB);
+  // Each role runs its own copy of the step loop (the same barriers in the
+  // same order), so its accumulators stay in place across steps.
+  auto run = [&](auto role_step) {
+    issue(0);
+    if (n_it > 1) issue(1);
+    begin_step(0, PD);
+    role_step(0, -1);
+    for (int j0 = 1; j0 < n_it; j0 += STAGES) {
+#pragma unroll
+      for (int u = 0; u < STAGES; ++u) {
+        const int j = j0 + u;
+        if (j >= n_it) break;
+        const int stg = (1 + u) % STAGES;  // j % 4
+        begin_step(j, (stg + PD) % STAGES);
+        role_step(stg, (stg + STAGES - 1) % STAGES);
       }
-      stage_b(st + 32 * RB);
-      advance(cur_gi, cur_m0);
     }
-  } else {
-    // One 32-query block per tile (D = 256), run in order without the
-    // interleave: the register file holds one score block next to the
-    // larger K/V operands.  Loads run PD + 1 tiles ahead.
-    (void)sB;
-    (void)pB;
-    for (int it = 0; it < n_it; ++it) {
-      sync_tile(it, PD);
-      if (it + PD + 1 < n_it) issue_next(it + PD + 1);
-      block_sdp(stage(it), sA, pA);
-      premask(cur_m0, sA);
-      block_valu(stats_of(it, 0), sA, pA);
-      stage_b(stage(it));
-      advance(cur_gi, cur_m0);
+    __syncthreads();  // role 0's P of the last tile
+  };
+  if (n_it > 0) {
+    if (role == 0) {
+      run([&](int stg, int) { step0(stg, stg & 1); });
+    } else {
+      run([&](int stg, int prev) {
+        if (prev >= 0) step1(prev, prev & 1);
+        if (kSkew) dp = score(stg);
+      });
+      step1((n_it - 1) % STAGES, (n_it - 1) & 1);
     }
   }
 
   if (key >= p.Sk) return;
   const int64_t krow = ((int64_t)bk * p.Sk + key) * p.D;
-  uint16_t* dkp = (uint16_t*)p.dk + krow;
-  uint16_t* dvp = (uint16_t*)p.dv + krow;
+  uint16_t* outp = (uint16_t*)(role == 0 ? p.dv : p.dk) + krow;
+  const float osc = role == 0 ? 1.f : p.scale;
 #pragma unroll
   for (int c = 0; c < DB; ++c)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = d_out0 + 32 * c + 8 * i + 4 * hl;
       if (d < p.D) {
-        const f32x16& kk = dkacc[c];
-        const f32x16& vv = dvacc[c];
-        *reinterpret_cast<u32x2*>(dkp + d) =
-            u32x2{pack2<T>(kk[4 * i] * p.scale, kk[4 * i + 1] * p.scale),
-                  pack2<T>(kk[4 * i + 2] * p.scale, kk[4 * i + 3] * p.scale)};
-        *reinterpret_cast<u32x2*>(dvp + d) =
-            u32x2{pack2<T>(vv[4 * i], vv[4 * i + 1]), pack2<T>(vv[4 * i + 2], vv[4 * i + 3])};
+        const f32x16& a = acc[c];
+        *reinterpret_cast<u32x2*>(outp + d) =
+            u32x2{pack2<T>(a[4 * i] * osc, a[4 * i + 1] * osc),
+                  pack2<T>(a[4 * i + 2] * osc, a[4 * i + 3] * osc)};
       }
     }
 }
@@ -757,24 +751,24 @@ struct DqConfig<256> {
   static constexpr bool kPipe = false;
 };
 
-template <class T, int DP, int DO, int BMQ>
+template <class T, int DP, int DO>
 static hipError_t launch_bwd_t(const BwdParams& p, bool causal, hipStream_t s) {
-  constexpr int NW = 4;
+  constexpr int NW = 4;  // dQ waves per workgroup
   constexpr int STAGES = 4;
   using QC = DqConfig<DP>;
   BwdParams q = p;
-  q.n_nblocks = (p.Sk + 32 * NW - 1) / (32 * NW);
+  q.n_nblocks = (p.Sk + 127) / 128;
   q.n_mblocks = (p.Sq + 32 * NW - 1) / (32 * NW);
   const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (DP / DO);
   const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
   if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   if (g_kv > 0) {
     if (causal)
-      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, BMQ, NW, STAGES, true>), dim3((unsigned)g_kv),
-                         dim3(NW * 64), 0, s, q);
+      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, STAGES, true>), dim3((unsigned)g_kv), dim3(512),
+                         0, s, q);
     else
-      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, BMQ, NW, STAGES, false>), dim3((unsigned)g_kv),
-                         dim3(NW * 64), 0, s, q);
+      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, STAGES, false>), dim3((unsigned)g_kv), dim3(512),
+                         0, s, q);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -791,9 +785,9 @@ static hipError_t launch_bwd_t(const BwdParams& p, bool causal, hipStream_t s) {
 
 template <class T>
 static hipError_t launch_bwd_dt(const BwdParams& p, bool causal, hipStream_t s) {
-  if (p.D <= 64) return launch_bwd_t<T, 64, 64, 64>(p, causal, s);
-  if (p.D <= 128) return launch_bwd_t<T, 128, 128, 64>(p, causal, s);
-  if (p.D <= 256) return launch_bwd_t<T, 256, 128, 32>(p, causal, s);
+  if (p.D <= 64) return launch_bwd_t<T, 64, 64>(p, causal, s);
+  if (p.D <= 128) return launch_bwd_t<T, 128, 128>(p, causal, s);
+  if (p.D <= 256) return launch_bwd_t<T, 256, 128>(p, causal, s);
   return hipErrorInvalidValue;
 }
 
