@@ -78,11 +78,15 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   constexpr int DB = DP / 32;  // 32-wide head-dim blocks of O^T
   constexpr int KN = BN / 16;  // k-steps over keys for O^T
   constexpr int LK = L::kSegs / NW;  // K (and V) segments each wave loads per tile
+  constexpr int KT = L::kTileBytes;
+  constexpr int RB = L::kRowBytes;
+  constexpr int kVReg = STAGES * KT;  // LDS: all K stages, then all V stages
+  constexpr int PD = STAGES - 2;      // tiles issued ahead of the one computed
   static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
-  static_assert(STAGES >= 3 && STAGES <= 4, "3 or 4 stages");
-  static_assert(STAGES - 2 <= 2, "the vmcnt wait covers up to 2 tiles ahead");
+  static_assert(STAGES == 4, "the unrolled tile loop assumes a 4-deep ring");
+  static_assert(3 * KT + (BN - 8) * RB < 65536, "stage offsets must fit the ds immediate");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * L::kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGES * KT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -104,6 +108,7 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
 
   const uint16_t* kbase = (const uint16_t*)p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = (const uint16_t*)p.v + b * p.v_sb + hkv * p.v_sh;
+  const uint32_t lds0 = lds_addr(smem);
 
   // Per-lane global byte offsets of the chunks this lane loads (tile-relative).
   uint32_t koff[LK], voff[LK];
@@ -117,19 +122,24 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     koff[j] = kc * 8 < p.D ? (uint32_t)((r * p.k_ss + kc * 8) * 2) : kBufferOob;
     voff[j] = vc * 8 < p.D ? (uint32_t)((r * p.v_ss + vc * 8) * 2) : kBufferOob;
   }
-  auto issue_tile = [&](int t) {
-    const int n0 = t * BN;
-    const int rows = min(BN, p.Sk - n0);
-    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.k_ss, tile_bytes(rows, p.k_ss, p.D));
-    const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.v_ss, tile_bytes(rows, p.v_ss, p.D));
-    const uint32_t st = lds_addr(smem) + (t % STAGES) * L::kStageBytes;
+
+  // Lane-constant LDS byte addresses (stage 0).  K operand of k-step s: row
+  // l32 (+32 kb), chunk 2s + hl.  V^T operand of head-dim block c: rows
+  // 4*hl + j16/4 (+16 s2, +8 for the upper half, neither of which changes the
+  // row's swizzle), chunk 4c + 2*((lane/16)%2) + (j16%4)/2, and the 8-byte
+  // half (j16%2) of that chunk.  Stage st adds st * KT.
+  int k_lds[KD], v_lds[DB];
 #pragma unroll
-    for (int j = 0; j < LK; ++j) {
-      const int seg = wave + j * NW;
-      buffer_load_lds_b128(kr, st + seg * 1024, koff[j]);
-      buffer_load_lds_b128(vr, st + L::kTileBytes + seg * 1024, voff[j]);
-    }
-  };
+  for (int s = 0; s < KD; ++s) k_lds[s] = l32 * RB + (((2 * s + hl) ^ swz_k<DP>(l32)) * 16);
+  {
+    const int j16 = lane & 15;
+    const int vr = 4 * hl + j16 / 4;
+    const int g = 2 * ((lane >> 4) & 1) + (j16 & 3) / 2;
+#pragma unroll
+    for (int c = 0; c < DB; ++c)
+      v_lds[c] = kVReg + vr * RB + (((4 * c + g) ^ swz_v<DP>(vr)) * 16) + 8 * (j16 & 1);
+  }
+  auto ld128 = [&](int addr) { return *reinterpret_cast<const u32x4*>(smem + addr); };
 
   auto run_item = [&](int mblk) {
   const int m0 = mblk * BM;
@@ -154,15 +164,34 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     }
   }
 
+  // Issue cursor: the next K/V tile's first key and base pointers.
+  int iss_n0 = 0;
+  const uint16_t* iss_k = kbase;
+  const uint16_t* iss_v = vbase;
+  auto issue_tile = [&](int stg) {
+    const int bytes_k = tile_bytes(min(BN, p.Sk - iss_n0), p.k_ss, p.D);
+    const int bytes_v = tile_bytes(min(BN, p.Sk - iss_n0), p.v_ss, p.D);
+    const i32x4 kr = make_rsrc_words(iss_k, bytes_k);
+    const i32x4 vr = make_rsrc_words(iss_v, bytes_v);
+#pragma unroll
+    for (int j = 0; j < LK; ++j) {
+      const int seg = wave + j * NW;
+      buffer_load_lds_b128(kr, lds0 + stg * KT + seg * 1024, koff[j]);
+      buffer_load_lds_b128(vr, lds0 + kVReg + stg * KT + seg * 1024, voff[j]);
+    }
+    iss_n0 += BN;
+    iss_k += (int64_t)BN * p.k_ss;
+    iss_v += (int64_t)BN * p.v_ss;
+  };
+
   // Software pipeline, per wave: in iteration t the MFMAs of S(t+1) = K(t+1) Q^T
   // are interleaved with the exp / pack / row-sum VALU work of the softmax of
   // tile t, then O += V(t) P(t) runs.  The MFMA unit runs asynchronously to
   // the VALU, so the softmax hides in the shadow of the next tile's score
   // MFMAs (a scheduling-group pattern fixes the interleave).  Tiles t and
   // t+1 are read in iteration t, so loads run PD = STAGES - 2 tiles ahead.
-  constexpr int PD = STAGES - 2;
-  static_assert(PD >= 1, "prefetch distance");
-
+  // Tile t lives in stage t % 4; the tile loop is unrolled by 4 so every
+  // stage offset is a compile-time immediate.
 #pragma unroll
   for (int t = 0; t <= PD; ++t)
     if (t < n_tiles) issue_tile(t);
@@ -173,27 +202,10 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   float m_run = kNegInf;
   float l_run = 0.f;
 
-  // Lane-constant LDS byte offsets.  K operand of k-step s: row l32 (+32 kb),
-  // chunk 2s + hl.  V^T operand of head-dim block c: rows 4*hl + j16/4 (+16 s2,
-  // +8 for the upper half, neither of which changes the row's swizzle), chunk
-  // 4c + 2*((lane/16)%2) + (j16%4)/2, and the 8-byte half (j16%2) of that chunk.
-  int k_lds[KD], v_lds[DB];
-#pragma unroll
-  for (int s = 0; s < KD; ++s) k_lds[s] = l32 * L::kRowBytes + (((2 * s + hl) ^ swz_k<DP>(l32)) * 16);
-  {
-    const int j16 = lane & 15;
-    const int vr = 4 * hl + j16 / 4;
-    const int g = 2 * ((lane >> 4) & 1) + (j16 & 3) / 2;
-#pragma unroll
-    for (int c = 0; c < DB; ++c)
-      v_lds[c] = L::kTileBytes + vr * L::kRowBytes + (((4 * c + g) ^ swz_v<DP>(vr)) * 16) +
-                 8 * (j16 & 1);
-  }
   const bool wave_has_rows = mw < p.Sq;
   auto active = [&](int t) {
     return t < n_tiles && wave_has_rows && (!CAUSAL || t * BN <= mw + 31 + diag);
   };
-  auto stage = [&](int t) { return smem + (t % STAGES) * L::kStageBytes; };
   // Tile t landed for this wave (vmcnt, with up to max_ahead later tiles still
   // in flight), then for all (barrier); the barrier also retires every wave's
   // reads of the stage the next issue refills.
@@ -208,15 +220,14 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     __syncthreads();
   };
 
-  // S^T = K Q^T: lane holds [key n0 + 32*kb + 8*(r/4) + 4*hl + r%4][query row].
-  auto gemm0 = [&](int t, f32x16 (&sd)[KB]) {
-    const uint8_t* st = stage(t);
+  // S^T = K Q^T of the tile in stage stg: lane holds
+  // [key n0 + 32*kb + 8*(r/4) + 4*hl + r%4][query row].
+  auto gemm0 = [&](int stg, f32x16 (&sd)[KB]) {
     u32x4 a[KD][KB];
 #pragma unroll
     for (int s = 0; s < KD; ++s)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        a[s][kb] = *reinterpret_cast<const u32x4*>(st + k_lds[s] + kb * 32 * L::kRowBytes);
+      for (int kb = 0; kb < KB; ++kb) a[s][kb] = ld128(k_lds[s] + stg * KT + kb * 32 * RB);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) sd[kb] = f32x16{};
 #pragma unroll
@@ -233,12 +244,22 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     if (tail || straddle) {
       int lim = p.Sk - 1;
       if (CAUSAL) lim = min(lim, row + diag);
-      lim -= n0 + 4 * hl;
+      // Element offset o (32*kb + 8*(r/4) + r%4) is masked iff o > lim - n0 - 4*hl.
+      // keep = all-ones iff visible; one bitfield insert per element selects
+      // the score or -inf (no per-element condition registers).
+      const int nlim = n0 + 4 * hl - lim - 1;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (32 * kb + 8 * (r >> 2) + (r & 3) > lim) sc[kb][r] = kNegInf;
+        for (int r = 0; r < 16; ++r) {
+          const int o = 32 * kb + 8 * (r >> 2) + (r & 3);
+          const uint32_t keep = (uint32_t)((o + nlim) >> 31);
+          // (Copy the element out first: a bit_cast of a vector-element
+          // lvalue reads the vector's first element.)
+          const float x = sc[kb][r];
+          sc[kb][r] = __builtin_bit_cast(
+              float, (keep & __builtin_bit_cast(uint32_t, x)) | (~keep & 0xff800000u));
+        }
     }
     float mt = kNegInf;
 #pragma unroll
@@ -284,10 +305,10 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     l_run += psum;
   };
 
-  // O^T += V^T P^T: DB*KN MFMAs, each fed by two transposed 8-byte reads that
-  // the scheduling-group pattern issues OLEAD MFMAs ahead.
-  auto gemm1 = [&](int t) {
-    const uint8_t* st = stage(t);
+  // O^T += V^T P^T for the tile in stage stg: DB*KN MFMAs, each fed by two
+  // transposed 8-byte reads that the scheduling-group pattern issues OLEAD
+  // MFMAs ahead.
+  auto gemm1 = [&](int stg) {
     constexpr int NM = DB * KN;
     constexpr int OLEAD = NM < 5 ? NM : 5;
     u32x4 vt[KN][DB];
@@ -295,9 +316,9 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     for (int s2 = 0; s2 < KN; ++s2)
 #pragma unroll
       for (int c = 0; c < DB; ++c) {
-        const uint8_t* vp = st + v_lds[c] + 16 * s2 * L::kRowBytes;
-        const u32x2 lo = lds_read_tr((const uint16_t*)vp);
-        const u32x2 hi = lds_read_tr((const uint16_t*)(vp + 8 * L::kRowBytes));
+        const int a = v_lds[c] + stg * KT + 16 * s2 * RB;
+        const u32x2 lo = lds_read_tr((const uint16_t*)(smem + a));
+        const u32x2 hi = lds_read_tr((const uint16_t*)(smem + a + 8 * RB));
         vt[s2][c] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
       }
 #pragma unroll
@@ -318,26 +339,22 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   // explicitly and fenced with sched_barrier so the in-order issue keeps the
   // K read of MFMA i + KLEAD ahead of MFMA i and puts EPM softmax elements
   // between consecutive MFMAs, where they run while the MFMA unit is busy.
-  auto stage_a = [&](int tn, f32x16 (&nx)[KB], const f32x16 (&sc)[KB], float neg_m) {
+  auto stage_a = [&](int stg_n, f32x16 (&nx)[KB], const f32x16 (&sc)[KB], float neg_m) {
     constexpr int NM = KD * KB;
     constexpr int KLEAD = NM < 3 ? NM : 3;
     constexpr int NE = KN * 8;          // softmax elements per lane
     constexpr int EPM = (NE + NM - 1) / NM;
-    const uint8_t* st = stage(tn);
+    auto addr = [&](int i) { return k_lds[i / KB] + stg_n * KT + (i % KB) * 32 * RB; };
     u32x4 a[NM];
     float e[NE];
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < KLEAD; ++i)
-      a[i] = *reinterpret_cast<const u32x4*>(st + k_lds[i / KB] + (i % KB) * 32 * L::kRowBytes);
+    for (int i = 0; i < KLEAD; ++i) a[i] = ld128(addr(i));
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
-      if (i + KLEAD < NM) {
-        const int n = i + KLEAD;
-        a[n] = *reinterpret_cast<const u32x4*>(st + k_lds[n / KB] + (n % KB) * 32 * L::kRowBytes);
-      }
+      if (i + KLEAD < NM) a[i + KLEAD] = ld128(addr(i + KLEAD));
       nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
 #pragma unroll
       for (int k = 0; k < EPM; ++k) {
@@ -366,36 +383,40 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   };
 
   // Prologue: tiles 0..PD were issued above; iteration t issues tile t+1+PD
-  // into the stage tile t-1 used.  The two score buffers alternate; the loop
-  // is unrolled by two so each iteration names its buffers statically.
+  // into the stage tile t-1 used.  Even tiles' scores live in s0, odd tiles'
+  // in s1; with the 4-way unroll both the stage and the score buffer of
+  // every iteration are compile-time constants.
   f32x16 s0[KB], s1[KB];
   if (n_tiles > 0) {
     sync_tile(0, PD);
     if (active(0)) gemm0(0, s0);
   }
-  auto iteration = [&](int t, f32x16 (&cur)[KB], f32x16 (&nxt)[KB]) {
-    const bool act = active(t);
-    const bool act_next = active(t + 1);
-    float neg_m = 0.f;
-    if (act) neg_m = rescale(mask_max(t, cur));
-    if (t + 1 < n_tiles) {
-      sync_tile(t + 1, PD - 1);
-      if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
+  for (int t0 = 0; t0 < n_tiles; t0 += STAGES) {
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u) {
+      const int t = t0 + u;
+      if (t >= n_tiles) break;
+      f32x16(&cur)[KB] = (u & 1) ? s1 : s0;
+      f32x16(&nxt)[KB] = (u & 1) ? s0 : s1;
+      const bool act = active(t);
+      const bool act_next = active(t + 1);
+      float neg_m = 0.f;
+      if (act) neg_m = rescale(mask_max(t, cur));
+      if (t + 1 < n_tiles) {
+        sync_tile(t + 1, PD - 1);
+        if (t + 1 + PD < n_tiles) issue_tile((u + 1 + PD) % STAGES);
+      }
+      // Stage A: S(t+1) MFMAs interleaved with the softmax of tile t.
+      if (act && act_next) {
+        stage_a((u + 1) % STAGES, nxt, cur, neg_m);
+      } else if (act) {
+        exp_pack(cur, neg_m);
+      } else if (act_next) {
+        gemm0((u + 1) % STAGES, nxt);
+      }
+      // Stage B: O += V(t) P(t).
+      if (act) gemm1(u);
     }
-    // Stage A: S(t+1) MFMAs interleaved with the softmax of tile t.
-    if (act && act_next) {
-      stage_a(t + 1, nxt, cur, neg_m);
-    } else if (act) {
-      exp_pack(cur, neg_m);
-    } else if (act_next) {
-      gemm0(t + 1, nxt);
-    }
-    // Stage B: O += V(t) P(t).
-    if (act) gemm1(t);
-  };
-  for (int t = 0; t < n_tiles; t += 2) {
-    iteration(t, s0, s1);
-    if (t + 1 < n_tiles) iteration(t + 1, s1, s0);
   }
 
   const float l_tot = xhalf_sum(l_run);
