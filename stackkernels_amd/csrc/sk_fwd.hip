@@ -69,8 +69,8 @@ __device__ __forceinline__ int swz_v(int r) {
   return DP == 64 ? 4 * ((r >> 1) & 1) : 4 * (r & 3);
 }
 
-template <class T, int DP, int BN, int NW, int STAGES, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
+template <class T, int DP, int BN, int NW, int STAGES, int OCC, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   using L = FwdLds<DP, BN>;
   constexpr int BM = 32 * NW;
   constexpr int KD = DP / 16;  // k-steps over the head dim for S^T
@@ -81,7 +81,6 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   constexpr int KT = L::kTileBytes;
   constexpr int RB = L::kRowBytes;
   constexpr int kVReg = STAGES * KT;  // LDS: all K stages, then all V stages
-  constexpr int PD = STAGES - 2;      // tiles issued ahead of the one computed
   static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
   static_assert(STAGES == 4, "the unrolled tile loop assumes a 4-deep ring");
   static_assert(3 * KT + (BN - 8) * RB < 65536, "stage offsets must fit the ds immediate");
@@ -164,37 +163,31 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     }
   }
 
-  // Issue cursor: the next K/V tile's first key and base pointers.
-  int iss_n0 = 0;
+  // Issue cursors of K and V (first key, base pointer).  K and V tiles are
+  // issued on separate schedules: group g carries K(g+1) and V(g).  A K
+  // tile past the end is issued with an empty range (zeros), so every group
+  // has the same number of loads.
+  int k_n0 = 0, v_n0 = 0;
   const uint16_t* iss_k = kbase;
   const uint16_t* iss_v = vbase;
-  auto issue_tile = [&](int stg) {
-    const int bytes_k = tile_bytes(min(BN, p.Sk - iss_n0), p.k_ss, p.D);
-    const int bytes_v = tile_bytes(min(BN, p.Sk - iss_n0), p.v_ss, p.D);
-    const i32x4 kr = make_rsrc_words(iss_k, bytes_k);
-    const i32x4 vr = make_rsrc_words(iss_v, bytes_v);
+  auto issue_k = [&](int stg) {
+    const int bytes = tile_bytes(max(0, min(BN, p.Sk - k_n0)), p.k_ss, p.D);
+    const i32x4 kr = make_rsrc_words(iss_k, bytes);
 #pragma unroll
-    for (int j = 0; j < LK; ++j) {
-      const int seg = wave + j * NW;
-      buffer_load_lds_b128(kr, lds0 + stg * KT + seg * 1024, koff[j]);
-      buffer_load_lds_b128(vr, lds0 + kVReg + stg * KT + seg * 1024, voff[j]);
-    }
-    iss_n0 += BN;
+    for (int j = 0; j < LK; ++j)
+      buffer_load_lds_b128(kr, lds0 + stg * KT + (wave + j * NW) * 1024, koff[j]);
+    k_n0 += BN;
     iss_k += (int64_t)BN * p.k_ss;
+  };
+  auto issue_v = [&](int stg) {
+    const int bytes = tile_bytes(max(0, min(BN, p.Sk - v_n0)), p.v_ss, p.D);
+    const i32x4 vr = make_rsrc_words(iss_v, bytes);
+#pragma unroll
+    for (int j = 0; j < LK; ++j)
+      buffer_load_lds_b128(vr, lds0 + kVReg + stg * KT + (wave + j * NW) * 1024, voff[j]);
+    v_n0 += BN;
     iss_v += (int64_t)BN * p.v_ss;
   };
-
-  // Software pipeline, per wave: in iteration t the MFMAs of S(t+1) = K(t+1) Q^T
-  // are interleaved with the exp / pack / row-sum VALU work of the softmax of
-  // tile t, then O += V(t) P(t) runs.  The MFMA unit runs asynchronously to
-  // the VALU, so the softmax hides in the shadow of the next tile's score
-  // MFMAs (a scheduling-group pattern fixes the interleave).  Tiles t and
-  // t+1 are read in iteration t, so loads run PD = STAGES - 2 tiles ahead.
-  // Tile t lives in stage t % 4; the tile loop is unrolled by 4 so every
-  // stage offset is a compile-time immediate.
-#pragma unroll
-  for (int t = 0; t <= PD; ++t)
-    if (t < n_tiles) issue_tile(t);
 
   f32x16 oacc[DB];
 #pragma unroll
@@ -206,14 +199,11 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
   auto active = [&](int t) {
     return t < n_tiles && wave_has_rows && (!CAUSAL || t * BN <= mw + 31 + diag);
   };
-  // Tile t landed for this wave (vmcnt, with up to max_ahead later tiles still
-  // in flight), then for all (barrier); the barrier also retires every wave's
-  // reads of the stage the next issue refills.
-  auto sync_tile = [&](int t, int max_ahead) {
-    const int ahead = min(max_ahead, n_tiles - 1 - t);  // tiles issued after t
-    if (ahead >= 2)
-      wait_vmcnt<2 * 2 * LK>();
-    else if (ahead == 1)
+  // Group g landed for this wave (vmcnt, with group g + 1 possibly still in
+  // flight), then for all (barrier); the barrier also retires every wave's
+  // reads of the stages the next issue refills.
+  auto sync_group = [&](int g) {
+    if (g + 1 < n_tiles)
       wait_vmcnt<2 * LK>();
     else
       wait_vmcnt<0>();
@@ -285,25 +275,9 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     return (m_run == kNegInf) ? 0.f : -m_run * p.scale_log2;
   };
 
-  // P^T = exp2(S^T * scale * log2 e - offset), packed as the next MFMA's B operand.
+  // P^T = exp2(S^T * scale * log2 e - offset), packed by stage A as the B
+  // operand of the O^T product.
   u32x4 pk[KN];
-  auto exp_pack = [&](const f32x16 (&sc)[KB], float neg_m) {
-    float psum = 0.f;
-#pragma unroll
-    for (int s2 = 0; s2 < KN; ++s2) {
-      const int kb = s2 >> 1;
-      const int base = 8 * (s2 & 1);
-      float e[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        e[j] = fast_exp2(fmaf(sc[kb][base + j], p.scale_log2, neg_m));
-        psum += e[j];
-      }
-      pk[s2] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
-                     pack2<T>(e[6], e[7])};
-    }
-    l_run += psum;
-  };
 
   // O^T += V^T P^T for the tile in stage stg: DB*KN MFMAs, each fed by two
   // transposed 8-byte reads that the scheduling-group pattern issues OLEAD
@@ -382,14 +356,44 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
     l_run += psum;
   };
 
-  // Prologue: tiles 0..PD were issued above; iteration t issues tile t+1+PD
-  // into the stage tile t-1 used.  Even tiles' scores live in s0, odd tiles'
-  // in s1; with the 4-way unroll both the stage and the score buffer of
-  // every iteration are compile-time constants.
+  // Pipeline.  Every wave runs, per tile t, stage A (S(t+1) MFMAs interleaved
+  // with the softmax of tile t) then O += V(t) P(t).  Barrier k -- after
+  // which group k (K(k+1), V(k)) is visible and group k + 2 is issued into
+  // the stages K(k-1) and V(k-2) used -- sits before stage A of tile k for
+  // waves 0-3 and between stage A and the O product of tile k-1 for waves
+  // 4-7.  So between two barriers waves 0-3 run stage A(k) then O(k) while
+  // waves 4-7 run O(k-1) then stage A(k): the two waves that share a SIMD
+  // (w, w+4) run their VALU-heavy and MFMA-only halves at opposite times.
+  // K tile x is read at stage A(x-1), V tile x at O(x), which for waves 4-7
+  // runs after barrier x+1; so each ring holds 4 tiles and every load has
+  // two tiles' time to land.  Stage indices are tile % 4; the loop is
+  // unrolled by 4 so they are compile-time constants.  Even tiles' scores
+  // live in s0, odd in s1.  A wave that sees tile t always runs stage A: on
+  // its last visible tile the S(t+1) it computes from a stale or empty stage
+  // is never read.
   f32x16 s0[KB], s1[KB];
+  const bool late = wave >= NW / 2;  // waves 4-7 (wave-uniform)
+  auto barrier_issue = [&](int k, int u_k) {  // barrier k; u_k = k % 4
+    sync_group(k);
+    if (k + 2 < n_tiles) {
+      issue_k((u_k + 3) % STAGES);
+      issue_v((u_k + 2) % STAGES);
+    }
+  };
   if (n_tiles > 0) {
-    sync_tile(0, PD);
-    if (active(0)) gemm0(0, s0);
+    issue_k(0);
+    issue_k(1);
+    issue_v(0);  // group 0
+    if (n_tiles > 1) {
+      issue_k(2);
+      issue_v(1);  // group 1
+      wait_vmcnt<2 * 2 * LK>();
+    } else {
+      wait_vmcnt<2 * LK>();
+    }
+    __syncthreads();  // K(0)
+    gemm0(0, s0);
+    if (late) barrier_issue(0, 0);
   }
   for (int t0 = 0; t0 < n_tiles; t0 += STAGES) {
 #pragma unroll
@@ -398,26 +402,14 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
       if (t >= n_tiles) break;
       f32x16(&cur)[KB] = (u & 1) ? s1 : s0;
       f32x16(&nxt)[KB] = (u & 1) ? s0 : s1;
+      if (!late) barrier_issue(t, u);
       const bool act = active(t);
-      const bool act_next = active(t + 1);
-      float neg_m = 0.f;
-      if (act) neg_m = rescale(mask_max(t, cur));
-      if (t + 1 < n_tiles) {
-        sync_tile(t + 1, PD - 1);
-        if (t + 1 + PD < n_tiles) issue_tile((u + 1 + PD) % STAGES);
-      }
-      // Stage A: S(t+1) MFMAs interleaved with the softmax of tile t.
-      if (act && act_next) {
-        stage_a((u + 1) % STAGES, nxt, cur, neg_m);
-      } else if (act) {
-        exp_pack(cur, neg_m);
-      } else if (act_next) {
-        gemm0((u + 1) % STAGES, nxt);
-      }
-      // Stage B: O += V(t) P(t).
+      if (act) stage_a((u + 1) % STAGES, nxt, cur, rescale(mask_max(t, cur)));
+      if (late) barrier_issue(t + 1, (u + 1) % STAGES);
       if (act) gemm1(u);
     }
   }
+  if (n_tiles > 0 && !late) __syncthreads();  // barrier n_tiles of waves 0-3
 
   const float l_tot = xhalf_sum(l_run);
   if (row < p.Sq) {
@@ -459,13 +451,13 @@ __global__ void __launch_bounds__(NW * 64, 1) fwd_mfma_kernel(FwdParams p) {
 // tile (two independent MFMA chains) while the score, operand and O
 // registers fit the 256-register budget of two waves per SIMD.
 struct FwdConfig {
-  int dp, bn, nw;
+  int dp, bn, nw, occ;
 };
 
 static FwdConfig fwd_config(int d) {
-  if (d <= 64) return {64, 64, 8};
-  if (d <= 128) return {128, 64, 8};
-  return {256, 32, 4};
+  if (d <= 64) return {64, 64, 8, 1};
+  if (d <= 128) return {128, 64, 8, 1};
+  return {256, 32, 4, 1};
 }
 
 int fwd_rows_per_block(int dtype, int d) {
@@ -473,14 +465,14 @@ int fwd_rows_per_block(int dtype, int d) {
   return 32 * fwd_config(d).nw;
 }
 
-template <class T, int DP, int BN, int NW>
+template <class T, int DP, int BN, int NW, int OCC>
 static hipError_t launch_fwd_t(const FwdParams& p, bool causal, hipStream_t s) {
   const dim3 grid((unsigned)(p.n_items * p.B * p.Hq));
   const dim3 block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, true>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false>), grid, block, 0, s, p);
   return hipGetLastError();
 }
 
@@ -488,11 +480,11 @@ template <class T>
 static hipError_t launch_fwd_dt(const FwdParams& p, bool causal, hipStream_t s) {
   switch (fwd_config(p.D).dp) {
     case 64:
-      return launch_fwd_t<T, 64, 64, 8>(p, causal, s);
+      return launch_fwd_t<T, 64, 64, 8, 1>(p, causal, s);
     case 128:
-      return launch_fwd_t<T, 128, 64, 8>(p, causal, s);
+      return launch_fwd_t<T, 128, 64, 8, 1>(p, causal, s);
     default:
-      return launch_fwd_t<T, 256, 32, 4>(p, causal, s);
+      return launch_fwd_t<T, 256, 32, 4, 1>(p, causal, s);
   }
 }
 
