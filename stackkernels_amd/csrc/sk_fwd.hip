@@ -311,49 +311,61 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   // Stage A: S(t+1) = K(t+1) Q^T interleaved, MFMA by MFMA, with the softmax
   // of tile t (exp2, row sum, bf16/fp16 pack).  The order is written out
   // explicitly and fenced with sched_barrier so the in-order issue keeps the
-  // K read of MFMA i + KLEAD ahead of MFMA i and puts EPM softmax elements
-  // between consecutive MFMAs, where they run while the MFMA unit is busy.
+  // K read of MFMA i + KLEAD ahead of MFMA i and puts softmax work between
+  // consecutive MFMAs, where it runs while the MFMA unit is busy.  The
+  // softmax is itself software-pipelined over groups of EPM elements: the
+  // slot after MFMA i holds the FMA of group i+2, the exp2 of group i+1 and
+  // the sum / pack of group i, so no instruction in a slot waits on another
+  // one in the same slot.
   auto stage_a = [&](int stg_n, f32x16 (&nx)[KB], const f32x16 (&sc)[KB], float neg_m) {
     constexpr int NM = KD * KB;
     constexpr int KLEAD = NM < 3 ? NM : 3;
     constexpr int NE = KN * 8;          // softmax elements per lane
     constexpr int EPM = (NE + NM - 1) / NM;
+    constexpr int NG = (NE + EPM - 1) / EPM;  // element groups (<= NM)
+    static_assert(NG <= NM && NG >= 2, "softmax groups must fit the MFMA slots");
     auto addr = [&](int i) { return k_lds[i / KB] + stg_n * KT + (i % KB) * 32 * RB; };
+    auto score = [&](int x) { return sc[x >> 4][x & 15]; };  // element x: block x/16, register x%16
     u32x4 a[NM];
-    float e[NE];
-    float psum = 0.f;
+    float y[NE], e[NE];
+    float psum[2] = {0.f, 0.f};
+    auto step1 = [&](int g) {
+#pragma unroll
+      for (int k = 0; k < EPM; ++k)
+        if (g * EPM + k < NE) y[g * EPM + k] = fmaf(score(g * EPM + k), p.scale_log2, neg_m);
+    };
+    auto step2 = [&](int g) {
+#pragma unroll
+      for (int k = 0; k < EPM; ++k)
+        if (g * EPM + k < NE) e[g * EPM + k] = fast_exp2(y[g * EPM + k]);
+    };
+    auto step3 = [&](int g) {
+#pragma unroll
+      for (int k = 0; k < EPM; ++k) {
+        const int x = g * EPM + k;
+        if (x < NE) {
+          psum[x & 1] += e[x];
+          if (x & 1) pk[x >> 3][(x & 7) >> 1] = pack2<T>(e[x - 1], e[x]);
+        }
+      }
+    };
 #pragma unroll
     for (int i = 0; i < KLEAD; ++i) a[i] = ld128(addr(i));
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
+    step1(0);
+    step1(1);
+    step2(0);
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       if (i + KLEAD < NM) a[i + KLEAD] = ld128(addr(i + KLEAD));
       nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
-#pragma unroll
-      for (int k = 0; k < EPM; ++k) {
-        const int x = i * EPM + k;
-        if (x < NE) {
-          const int s2 = x / 8, j = x % 8;
-          e[x] = fast_exp2(fmaf(sc[s2 >> 1][8 * (s2 & 1) + j], p.scale_log2, neg_m));
-          psum += e[x];
-          if (j == 7)
-            pk[s2] = u32x4{pack2<T>(e[x - 7], e[x - 6]), pack2<T>(e[x - 5], e[x - 4]),
-                           pack2<T>(e[x - 3], e[x - 2]), pack2<T>(e[x - 1], e[x])};
-        }
-      }
+      if (i + 2 < NG) step1(i + 2);
+      if (i + 1 < NG) step2(i + 1);
+      if (i < NG) step3(i);
       __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int x = NM * EPM; x < NE; ++x) {
-      const int s2 = x / 8, j = x % 8;
-      e[x] = fast_exp2(fmaf(sc[s2 >> 1][8 * (s2 & 1) + j], p.scale_log2, neg_m));
-      psum += e[x];
-      if (j == 7)
-        pk[s2] = u32x4{pack2<T>(e[x - 7], e[x - 6]), pack2<T>(e[x - 5], e[x - 4]),
-                       pack2<T>(e[x - 3], e[x - 2]), pack2<T>(e[x - 1], e[x])};
-    }
-    l_run += psum;
+    l_run += psum[0] + psum[1];
   };
 
   // Pipeline.  Every wave runs, per tile t, stage A (S(t+1) MFMAs interleaved
