@@ -41,6 +41,18 @@ METRIC = "attn fwd/bwd TFLOP/s (% bf16 MFMA peak); flash_decode KV GB/s (% HBM p
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 
+# HBM bytes per step of each workload's kernels, from two rocprofv3 --pmc runs
+# (FETCH_SIZE, then WRITE_SIZE; profiles/hbm_traffic_counters.md), each scaled by
+# what the same counter reads for a 1 GiB device copy (FETCH_SIZE x 2,
+# WRITE_SIZE x 1).  Counter runs cannot share a process with the timed loops,
+# so these are recorded figures of the current kernels, not live ones.
+HBM_TRAFFIC_BYTES = {
+    "fwd": 786_890_745,
+    "fwdbwd": 788_786_752,
+    "decode": 8_612_428_279,
+    "decode_mqa": 572_983_785,
+}
+
 
 def causal_pairs(sq: int, sk: int, causal: bool) -> int:
     """Unmasked (i, j) pairs per (batch, head) under the bottom-right mask."""
@@ -153,27 +165,49 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
     return fwdbwd
 
 
-def _time_loop(fn, steps: int, warmup: int, torch, stream):
+def _time_loop(fn, steps: int, warmup: int, torch, stream, per_step: bool = False):
     """Run ``fn(i)`` warmup + steps times; return (total ms / steps, sorted per-step ms).
 
-    Each step is bracketed by its own event pair on the launch stream; while the
-    host keeps the queue full, the pair measures exactly that step's kernels."""
+    The total is one event pair around the ``steps`` back-to-back steps.  With
+    ``per_step`` each step is also bracketed by its own event pair on the launch
+    stream, which measures exactly that step's kernels while the host keeps the
+    queue full; the extra event packets add a few microseconds between steps,
+    so the total of such a loop is not used as the step time."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+           for _ in range(steps if per_step else 0)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0.record(stream)
     for i in range(steps):
-        evs[i][0].record(stream)
+        if per_step:
+            evs[i][0].record(stream)
         fn(i)
-        evs[i][1].record(stream)
+        if per_step:
+            evs[i][1].record(stream)
     t1.record(stream)
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps, sorted(a.elapsed_time(b) for a, b in evs)
+
+
+def _warm_device(torch, dev, ms: float = 300.0):
+    """Bring the GPU out of its idle clocks right before a timed loop: about
+    ``ms`` of plain bf16 matmuls (not a step of any workload).  After an idle
+    spell the first ~20 ms of attention kernels otherwise run up to 15% slow
+    while the power controller settles."""
+    a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
+    a = (a @ a) * 1e-3  # the first product may load the BLAS library: not part of the budget
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            a = (a @ a) * 1e-3
+        torch.cuda.synchronize()
+    for _ in range(20):  # left in the queue: no idle gap before the caller's first launch
+        a = (a @ a) * 1e-3
 
 
 def run_gpu(w: dict, steps: int, warmup: int):
@@ -213,9 +247,10 @@ def run_gpu(w: dict, steps: int, warmup: int):
             flash_attn_bwd(do, q, k, v, o, lse, is_causal=w["causal"])
 
     stream = torch.cuda.current_stream(dev)
-    ms_step, _ = _time_loop(step, steps, warmup, torch, stream)
     launch = _abi_launcher(w, inputs, do, torch, dev)
-    _, per = _time_loop(launch, steps, warmup, torch, stream)
+    _warm_device(torch, dev)
+    ms_step, _ = _time_loop(step, steps, warmup, torch, stream)
+    _, per = _time_loop(launch, steps, warmup, torch, stream, per_step=True)
     details["launch_ms_median"] = round(per[len(per) // 2], 5)
     details["launch_ms_min"] = round(per[0], 5)
     mean = sum(per) / len(per)
@@ -297,7 +332,8 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
             "peak": peak,
             "unit": unit,
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": HBM_TRAFFIC_BYTES.get(key),
+            "traffic_unit": "bytes per step (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
             "work_per_launch": units,
         },
         "details": details,
@@ -319,7 +355,7 @@ def copy_calibration(steps: int, warmup: int) -> dict:
     x = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     y = torch.empty_like(x)
     stream = torch.cuda.current_stream(dev)
-    _, per = _time_loop(lambda i: y.copy_(x), steps, warmup, torch, stream)
+    _, per = _time_loop(lambda i: y.copy_(x), steps, warmup, torch, stream, per_step=True)
     mean = sum(per) / len(per)
     return {"workload": "copy", "bytes_read": n, "bytes_written": n, "ms_mean": round(mean, 5),
             "GB/s": round(2 * n / mean / 1e6, 1)}

@@ -15,11 +15,10 @@
 // so the exponent always uses |sm_scale| and a masked score is simply -inf.
 //
 // Shared organisation (the forward kernel's, adapted):
-// * Four waves per workgroup, one per SIMD, one workgroup per CU: each wave
-//   keeps its 32 rows of the resident operands in registers and has the
-//   whole 512-entry VGPR+AGPR file for operands, two score blocks in flight
-//   and the fp32 accumulators.
-// * The streamed tiles go through a STAGES-deep LDS ring written by
+// * Two waves per SIMD (256 registers each; the dQ kernel at D = 256 runs
+//   one), so every MFMA accumulates in VGPRs and the two waves of a SIMD
+//   overlap one's VALU work with the other's MFMAs.
+// * The streamed tiles go through a 4-deep LDS ring written by
 //   buffer_load ... lds (direct to LDS), two tiles ahead of the math, one
 //   barrier per tile.  Rows past the sequence end and head-dim padding come
 //   back as zeros from the buffer range check.
@@ -29,31 +28,28 @@
 //   serves both: chunk c of row r sits at c ^ f(r) with f a bijection on
 //   r % 16 whose top two bits differ across every aligned group of 4 rows,
 //   so both read shapes hit 16 distinct bank quads of the 64-bank LDS.
-// * Software pipeline per wave: the score and dP MFMAs of the next block are
-//   interleaved, MFMA by MFMA, with the exp / dS / pack VALU work of the
-//   current block (the MFMA unit runs asynchronously to the VALU), then the
-//   gradient MFMAs of the current block run with their transposed operand
-//   reads issued a few MFMAs ahead.
 // * XCD-aware order: the 8 XCDs each walk a contiguous range of work items,
 //   head-major, so the workgroups that share a head's streamed operand share
 //   an L2.
 //
-// dK/dV kernel (bwd_dkv_kernel): a workgroup owns 128 keys of one
-// (batch, KV head), 32 per wave, and walks every query head of that KV
-// head's group and every 64-query tile that can see its keys, so the GQA sum
-// happens in registers (deterministic, no atomics).  S = Q K^T and
-// dP = dO V^T use K and V from registers as the B operand: each lane then
-// owns one key (its l%32) and 16 queries per 32-query block; P and dS feed
-// dV^T += dO^T P and dK^T += Q^T dS straight from registers, with dO^T / Q^T
-// read transposed from the ring (the contraction over queries is permuted
-// identically on both operands).  Every wave keeps its own copy of the
-// tile's row statistics in the ring.  At D = 256 the output head dim is
-// split over two workgroups to keep the accumulators in the register file.
+// dK/dV kernel (bwd_dkv_kernel): a workgroup of 8 waves owns 128 keys of one
+// (batch, KV head) and walks every query head of that KV head's group and
+// every 32-query tile that can see its keys, so the GQA sum happens in
+// registers (deterministic, no atomics).  The two waves of a SIMD share a
+// 32-key group and split the work by role: one holds K and computes
+// S = Q K^T, P and dV^T += dO^T P; the other holds V and computes
+// dP = dO V^T, dS and dK^T += Q^T dS, reading P from LDS.  With K or V as
+// the B operand each lane owns one key (its l%32) and 16 queries per
+// 32-query block; dO^T / Q^T are read transposed from the ring (the
+// contraction over queries is permuted identically on both operands).  At
+// D = 256 the output head dim is split over two workgroups to keep the
+// accumulators in the register file.
 //
-// dQ kernel (bwd_dq_kernel): a workgroup owns 128 query rows, 32 per wave,
-// with Q and dO in registers; K/V tiles stream through the ring;
-// S^T = K Q^T and dP^T = V dO^T give one query per lane, and
-// dQ^T += K^T dS^T reads K^T transposed from the ring.
+// dQ kernel (bwd_dq_kernel): a workgroup of 4 waves owns 128 query rows, 32
+// per wave, with Q and dO in registers, two workgroups per CU (one at
+// D = 256); 32-key K/V tiles stream through the ring; S^T = K Q^T and
+// dP^T = V dO^T give one query per lane, and dQ^T += K^T dS^T reads K^T
+// transposed from the ring.
 #include "sk_common.h"
 #include "sk_kernels.h"
 
@@ -729,13 +725,14 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
 }
 
 // gfx950 tile table for the backward, by head dim (padded to 64, 128 or 256;
-// other dims run zero-padded in the next size up).  Four waves (one per
-// SIMD), 4 ring stages, one workgroup per CU:
-//   dK/dV: 128 keys per workgroup; query tiles of 64 rows (32 at D = 256,
-//          where the output head dim is also split over two workgroups);
-//          ring 4 x (Q + dO + stats) = 72 / 136 / 136 KiB.
-//   dQ:    128 query rows per workgroup; key tiles of 64 rows (32 at
-//          D = 256); ring 4 x (K + V) = 64 / 128 / 128 KiB.
+// other dims run zero-padded in the next size up), 4 ring stages:
+//   dK/dV: 8 waves, one workgroup per CU, 128 keys per workgroup, 32-query
+//          tiles (at D = 256 the output head dim is split over two
+//          workgroups); LDS ring 4 x (Q + dO + stats) + P exchange
+//          = 72 / 104 / 152 KiB.
+//   dQ:    4 waves, 128 query rows per workgroup, 32-key tiles; ring
+//          4 x (K + V) = 32 / 64 / 128 KiB, so two workgroups fit a CU at
+//          D <= 128.
 // dQ kernel table by padded head dim: key tile, workgroups per CU, and
 // whether a wave interleaves its own softmax with the next tile's MFMAs.
 template <int DP>

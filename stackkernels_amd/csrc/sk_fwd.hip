@@ -7,11 +7,18 @@
 // * A workgroup of NW waves owns BM = 32*NW query rows of one (batch, query
 //   head); each wave owns 32 of them, with its Q rows held in registers.
 //   At D <= 128 a workgroup is 8 waves (two per SIMD) and fills a CU alone.
-// * K/V tiles of BN keys stream through a STAGES-deep ring of LDS stages,
-//   written by buffer_load ... lds (direct to LDS, no register staging).
-//   Each wave issues whole 1 KiB segments; rows past S_k and head-dim
-//   padding come back as zeros from the buffer range check.  One barrier per
-//   tile; loads run STAGES-1 tiles ahead of the math.
+// * K/V tiles of BN keys stream through two 4-deep LDS rings (all K stages,
+//   then all V stages), written by buffer_load ... lds (direct to LDS, no
+//   register staging).  Each wave issues whole 1 KiB segments; rows past S_k
+//   and head-dim padding come back as zeros from the buffer range check.
+//   One barrier per tile; K runs three tiles and V two tiles ahead of the
+//   math.  The tile loop is unrolled by the ring depth, so every LDS
+//   address is a lane-constant register plus a compile-time offset.
+// * The two waves that share a SIMD (w, w + NW/2) sit at opposite points of
+//   the tile loop relative to the barrier, so one runs its VALU-heavy
+//   softmax while the other runs its MFMA-only O product.  Within a wave the
+//   softmax of tile t is interleaved, MFMA by MFMA, with the score MFMAs of
+//   tile t+1 in three pipelined steps (scale/exp, sum, pack).
 // * LDS tiles are unpadded with a 16-byte-chunk XOR swizzle: chunk c of row r
 //   sits at c ^ (r % 16) in K tiles (the 16-byte row reads of 16 consecutive
 //   rows hit disjoint bank quads) and at c ^ 4 (r % 4) in V tiles (the four
@@ -37,7 +44,10 @@
 // * XCD-aware order: each of the 8 XCDs walks a contiguous range of
 //   (head, query block) items, head-major, heaviest query block first, so
 //   the heads an XCD has in flight share its L2 and the causal triangle's
-//   long rows do not trail at the end of the grid.
+//   long rows do not trail at the end of the grid.  Under the causal mask a
+//   workgroup runs query blocks j and n-1-j back to back when the grid
+//   stays at two or more workgroups per CU, which evens out the work per
+//   workgroup and halves the per-item fixed cost.
 #include "sk_common.h"
 #include "sk_kernels.h"
 
