@@ -14,11 +14,12 @@
 //   One barrier per tile; K runs three tiles and V two tiles ahead of the
 //   math.  The tile loop is unrolled by the ring depth, so every LDS
 //   address is a lane-constant register plus a compile-time offset.
-// * The two waves that share a SIMD (w, w + NW/2) sit at opposite points of
-//   the tile loop relative to the barrier, so one runs its VALU-heavy
-//   softmax while the other runs its MFMA-only O product.  Within a wave the
-//   softmax of tile t is interleaved, MFMA by MFMA, with the score MFMAs of
-//   tile t+1 in three pipelined steps (scale/exp, sum, pack).
+// * One tile body per tile and wave: the score MFMAs of tile t+1, then the
+//   O MFMAs of tile t, with the softmax of tile t (scale/exp2, row sum,
+//   pack) and the row maximum of tile t+1 spread evenly between all of
+//   them.  A wave overlaps MFMA and VALU work only with its own
+//   instructions (an MFMA-bound wave starves the other wave of its SIMD),
+//   so every wave keeps both busy itself.
 // * LDS tiles are unpadded with a 16-byte-chunk XOR swizzle: chunk c of row r
 //   sits at c ^ (r % 16) in K tiles (the 16-byte row reads of 16 consecutive
 //   rows hit disjoint bank quads) and at c ^ 4 (r % 4) in V tiles (the four
@@ -77,6 +78,15 @@ __device__ __forceinline__ int swz_k(int r) {
 template <int DP>
 __device__ __forceinline__ int swz_v(int r) {
   return DP == 64 ? 4 * ((r >> 1) & 1) : 4 * (r & 3);
+}
+
+// Forward tile body schedule check: softmax pair g (FMA at slot g*fl/(ng-1),
+// pack two slots later) is packed at least one slot before the first O MFMA
+// that reads its k-step, O MFMA j sitting at slot ns + j with k-step j / db.
+constexpr bool softmax_pairs_fit(int ns, int db, int fl, int ng) {
+  for (int g = 0; g < ng; ++g)
+    if (g * fl / (ng - 1) + 2 > ns + (g / 4) * db - 2) return false;
+  return true;
 }
 
 template <class T, int DP, int BN, int NW, int STAGES, int OCC, bool CAUSAL>
@@ -265,7 +275,7 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[kb][r]);
+      for (int r = 0; r < 16; ++r) mt = __builtin_elementwise_maximum(mt, sc[kb][r]);
     return xhalf_max(mt);
   };
 
@@ -289,112 +299,108 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   // operand of the O^T product.
   u32x4 pk[KN];
 
-  // O^T += V^T P^T for the tile in stage stg: DB*KN MFMAs, each fed by two
-  // transposed 8-byte reads that the scheduling-group pattern issues OLEAD
-  // MFMAs ahead.
-  auto gemm1 = [&](int stg) {
-    constexpr int NM = DB * KN;
-    constexpr int OLEAD = NM < 5 ? NM : 5;
-    u32x4 vt[KN][DB];
-#pragma unroll
-    for (int s2 = 0; s2 < KN; ++s2)
-#pragma unroll
-      for (int c = 0; c < DB; ++c) {
-        const int a = v_lds[c] + stg * KT + 16 * s2 * RB;
-        const u32x2 lo = lds_read_tr((const uint16_t*)(smem + a));
-        const u32x2 hi = lds_read_tr((const uint16_t*)(smem + a + 8 * RB));
-        vt[s2][c] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
-      }
-#pragma unroll
-    for (int s2 = 0; s2 < KN; ++s2)
-#pragma unroll
-      for (int c = 0; c < DB; ++c) oacc[c] = mfma32<T>(vt[s2][c], pk[s2], oacc[c]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * OLEAD, 0);
-#pragma unroll
-    for (int i = 0; i < NM - OLEAD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, OLEAD, 0);
-  };
-
-  // Stage A: S(t+1) = K(t+1) Q^T interleaved, MFMA by MFMA, with the softmax
-  // of tile t (exp2, row sum, bf16/fp16 pack).  The order is written out
-  // explicitly and fenced with sched_barrier so the in-order issue keeps the
-  // K read of MFMA i + KLEAD ahead of MFMA i and puts softmax work between
-  // consecutive MFMAs, where it runs while the MFMA unit is busy.  The
-  // softmax is itself software-pipelined over groups of EPM elements: the
-  // slot after MFMA i holds the FMA of group i+2, the exp2 of group i+1 and
-  // the sum / pack of group i, so no instruction in a slot waits on another
-  // one in the same slot.
-  auto stage_a = [&](int stg_n, f32x16 (&nx)[KB], const f32x16 (&sc)[KB], float neg_m) {
-    constexpr int NM = KD * KB;
-    constexpr int KLEAD = NM < 3 ? NM : 3;
-    constexpr int NE = KN * 8;          // softmax elements per lane
-    constexpr int EPM = (NE + NM - 1) / NM;
-    constexpr int NG = (NE + EPM - 1) / EPM;  // element groups (<= NM)
-    static_assert(NG <= NM && NG >= 2, "softmax groups must fit the MFMA slots");
-    auto addr = [&](int i) { return k_lds[i / KB] + stg_n * KT + (i % KB) * 32 * RB; };
-    auto score = [&](int x) { return sc[x >> 4][x & 15]; };  // element x: block x/16, register x%16
-    u32x4 a[NM];
+  // Tile body for tile t, one MFMA per slot: S(t+1) = K(t+1) Q^T in slots
+  // 0..NS-1, then O^T += V(t)^T P(t)^T in slots NS..NM-1.  The softmax of
+  // tile t runs between the MFMAs, spread over all of them, so every slot
+  // carries about the same VALU work and the MFMA unit never waits for a
+  // long VALU stretch; a wave keeps MFMAs and VALU work overlapped by
+  // interleaving them itself.  Element pair g (elements 2g, 2g+1) takes its
+  // FMA at slot F(g), its exp2 at F(g)+1 and its row sum and 16-bit pack at
+  // F(g)+2; F spreads the pairs evenly so that P(t)'s k-step s2 is packed at
+  // least one slot before the first O MFMA that reads it.  The raw row maximum
+  // of S(t+1) is taken in the last slots, after its MFMAs have completed.
+  // The operand reads run KLEAD (K) and OLEAD (V^T) MFMAs ahead.  Each slot
+  // is fenced with sched_barrier so the in-order issue keeps this order.
+  auto body = [&](int stg_k, int stg_v, f32x16 (&nx)[KB], const f32x16 (&sc)[KB],
+                  float neg_m) {
+    constexpr int NS = KD * KB;
+    constexpr int NO = DB * KN;
+    constexpr int NM = NS + NO;
+    constexpr int KLEAD = NS < 3 ? NS : 3;
+    constexpr int OLEAD = NO < 5 ? NO : 5;
+    constexpr int NE = KN * 8;  // softmax elements per lane (pairs 4*s2 .. 4*s2+3 form pk[s2])
+    constexpr int NG = NE / 2;
+    constexpr int FL = NS + ((NG - 1) / 4) * DB - 4;  // F of the last pair
+    constexpr int MS = NS + 2;                         // first slot of the row maximum
+    constexpr int NX = 16 * KB;                        // S(t+1) elements per lane
+    static_assert(FL >= 0 && softmax_pairs_fit(NS, DB, FL, NG),
+                  "every pair is packed at least one slot before the first O MFMA that reads it");
+    static_assert(MS < NM, "row maximum slots");
+    auto fslot = [](int g) { return g * FL / (NG - 1); };
+    auto kaddr = [&](int i) { return k_lds[i / KB] + stg_k * KT + (i % KB) * 32 * RB; };
+    auto score = [&](int x) { return sc[x >> 4][x & 15]; };
+    auto read_vt = [&](int j) {
+      const int s2 = j / DB, c = j % DB;
+      const int ad = v_lds[c] + stg_v * KT + 16 * s2 * RB;
+      const u32x2 lo = lds_read_tr((const uint16_t*)(smem + ad));
+      const u32x2 hi = lds_read_tr((const uint16_t*)(smem + ad + 8 * RB));
+      return u32x4(__builtin_shufflevector(lo, hi, 0, 1, 2, 3));
+    };
+    // A result that nothing reads until the end of the body would otherwise
+    // be computed wherever the instruction selector puts it (at the end);
+    // an empty asm statement with side effects pins it into its slot.
+    u32x4 a[NS];
+    u32x4 vt[NO];
     float y[NE], e[NE];
     float psum[2] = {0.f, 0.f};
-    auto step1 = [&](int g) {
+    float mx = kNegInf;
 #pragma unroll
-      for (int k = 0; k < EPM; ++k)
-        if (g * EPM + k < NE) y[g * EPM + k] = fmaf(score(g * EPM + k), p.scale_log2, neg_m);
-    };
-    auto step2 = [&](int g) {
-#pragma unroll
-      for (int k = 0; k < EPM; ++k)
-        if (g * EPM + k < NE) e[g * EPM + k] = fast_exp2(y[g * EPM + k]);
-    };
-    auto step3 = [&](int g) {
-#pragma unroll
-      for (int k = 0; k < EPM; ++k) {
-        const int x = g * EPM + k;
-        if (x < NE) {
-          psum[x & 1] += e[x];
-          if (x & 1) pk[x >> 3][(x & 7) >> 1] = pack2<T>(e[x - 1], e[x]);
-        }
-      }
-    };
-#pragma unroll
-    for (int i = 0; i < KLEAD; ++i) a[i] = ld128(addr(i));
+    for (int i = 0; i < KLEAD; ++i) a[i] = ld128(kaddr(i));
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
-    step1(0);
-    step1(1);
-    step2(0);
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
-      if (i + KLEAD < NM) a[i + KLEAD] = ld128(addr(i + KLEAD));
-      nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
-      if (i + 2 < NG) step1(i + 2);
-      if (i + 1 < NG) step2(i + 1);
-      if (i < NG) step3(i);
+      if (i + KLEAD < NS) a[i + KLEAD] = ld128(kaddr(i + KLEAD));
+      if (i + OLEAD >= NS && i + OLEAD - NS < NO) vt[i + OLEAD - NS] = read_vt(i + OLEAD - NS);
+      if (i < NS) {
+        nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
+      } else {
+        const int j = i - NS;
+        oacc[j % DB] = mfma32<T>(vt[j], pk[j / DB], oacc[j % DB]);
+      }
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int f = fslot(g);
+        if (f == i) {
+          y[2 * g] = fmaf(score(2 * g), p.scale_log2, neg_m);
+          y[2 * g + 1] = fmaf(score(2 * g + 1), p.scale_log2, neg_m);
+        }
+        if (f + 1 == i) {
+          e[2 * g] = fast_exp2(y[2 * g]);
+          e[2 * g + 1] = fast_exp2(y[2 * g + 1]);
+        }
+        if (f + 2 == i) {
+          psum[0] += e[2 * g];
+          psum[1] += e[2 * g + 1];
+          pk[g >> 2][g & 3] = pack2<T>(e[2 * g], e[2 * g + 1]);
+          asm volatile("" : "+v"(psum[0]), "+v"(psum[1]));
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < NX / 2; ++q)
+        if (i == MS + q * (NM - MS) / (NX / 2))
+          mx = __builtin_elementwise_maximum(
+              mx, __builtin_elementwise_maximum(nx[q >> 3][(2 * q) & 15], nx[q >> 3][(2 * q + 1) & 15]));
+      if (i >= MS) asm volatile("" : "+v"(mx));
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += psum[0] + psum[1];
+    return xhalf_max(mx);
   };
 
-  // Pipeline.  Every wave runs, per tile t, stage A (S(t+1) MFMAs interleaved
-  // with the softmax of tile t) then O += V(t) P(t).  Barrier k -- after
-  // which group k (K(k+1), V(k)) is visible and group k + 2 is issued into
-  // the stages K(k-1) and V(k-2) used -- sits before stage A of tile k for
-  // waves 0-3 and between stage A and the O product of tile k-1 for waves
-  // 4-7.  So between two barriers waves 0-3 run stage A(k) then O(k) while
-  // waves 4-7 run O(k-1) then stage A(k): the two waves that share a SIMD
-  // (w, w+4) run their VALU-heavy and MFMA-only halves at opposite times.
-  // K tile x is read at stage A(x-1), V tile x at O(x), which for waves 4-7
-  // runs after barrier x+1; so each ring holds 4 tiles and every load has
-  // two tiles' time to land.  Stage indices are tile % 4; the loop is
-  // unrolled by 4 so they are compile-time constants.  Even tiles' scores
-  // live in s0, odd in s1.  A wave that sees tile t always runs stage A: on
-  // its last visible tile the S(t+1) it computes from a stale or empty stage
-  // is never read.
+  // Pipeline.  Barrier t makes group t (K(t+1), V(t)) visible to every wave
+  // and retires every wave's reads of tile t-1's body, which read K(t) and
+  // V(t-1); group t+2 (K(t+3), V(t+2)) is then issued into the stages K(t-1)
+  // and V(t-2) used, so each load has two tiles' time to land.  Stage indices
+  // are tile % 4 and the loop is unrolled by 4, so they are compile-time
+  // constants.  Even tiles' scores live in s0, odd in s1.  A wave that sees
+  // tile t always computes S(t+1) in its body; on its last visible tile that
+  // result (from a stale or empty stage) is never read.
   f32x16 s0[KB], s1[KB];
-  const bool late = wave >= NW / 2;  // waves 4-7 (wave-uniform)
+  auto masked = [&](int t) {
+    const int n0 = t * BN;
+    return n0 + BN > p.Sk || (CAUSAL && (n0 + BN - 1 > mw + diag));
+  };
   auto barrier_issue = [&](int k, int u_k) {  // barrier k; u_k = k % 4
     sync_group(k);
     if (k + 2 < n_tiles) {
@@ -402,6 +408,7 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
       issue_v((u_k + 2) % STAGES);
     }
   };
+  float neg_m = 0.f;
   if (n_tiles > 0) {
     issue_k(0);
     issue_k(1);
@@ -415,7 +422,7 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
     }
     __syncthreads();  // K(0)
     gemm0(0, s0);
-    if (late) barrier_issue(0, 0);
+    if (active(0)) neg_m = rescale(mask_max(0, s0));
   }
   for (int t0 = 0; t0 < n_tiles; t0 += STAGES) {
 #pragma unroll
@@ -424,14 +431,16 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
       if (t >= n_tiles) break;
       f32x16(&cur)[KB] = (u & 1) ? s1 : s0;
       f32x16(&nxt)[KB] = (u & 1) ? s0 : s1;
-      if (!late) barrier_issue(t, u);
-      const bool act = active(t);
-      if (act) stage_a((u + 1) % STAGES, nxt, cur, rescale(mask_max(t, cur)));
-      if (late) barrier_issue(t + 1, (u + 1) % STAGES);
-      if (act) gemm1(u);
+      barrier_issue(t, u);
+      if (active(t)) {
+        float mt = body((u + 1) % STAGES, u, nxt, cur, neg_m);
+        if (active(t + 1)) {
+          if (masked(t + 1)) mt = mask_max(t + 1, nxt);
+          neg_m = rescale(mt);
+        }
+      }
     }
   }
-  if (n_tiles > 0 && !late) __syncthreads();  // barrier n_tiles of waves 0-3
 
   const float l_tot = xhalf_sum(l_run);
   if (row < p.Sq) {
