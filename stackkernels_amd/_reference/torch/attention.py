@@ -13,7 +13,10 @@ build must keep so existing callers and tests behave identically:
 * out = (P v) cast back to q's dtype.
 
 The backward of this path is autograd through this function, as the
-reference's ``FlashAttentionFunction.backward`` does.
+reference's ``FlashAttentionFunction.backward`` does.  Where autograd is not
+available (inside a torch.library op implementation, which runs below the
+autograd dispatch key), ``attention_reference_backward`` gives the same
+gradients in closed form.
 """
 
 from __future__ import annotations
@@ -58,4 +61,44 @@ def attention_reference(
     return out, lse
 
 
-__all__ = ["attention_reference", "repeat_kv"]
+def attention_reference_backward(
+    do: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    is_causal: bool = False,
+    sm_scale: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients (dq, dk, dv) of ``attention_reference``'s output for upstream dO.
+
+    The closed form of that function's autograd graph: P = softmax(S) with
+    fully masked rows 0, dV = P^T dO, dP = dO V^T, dS = P * (dP - rowsum(dP * P)),
+    dQ = scale dS K, dK = scale dS^T Q, with the GQA group summed for dK, dV.
+    Computed in float32; results take the inputs' dtypes.
+    """
+    b, h_q, s_q, d = q.shape
+    _, h_kv, s_k, _ = k.shape
+    scale = 1.0 / math.sqrt(d) if sm_scale is None else sm_scale
+    group = h_q // h_kv
+    qf = q.float()
+    kf = repeat_kv(k, group).float()
+    vf = repeat_kv(v, group).float()
+    dof = do.float()
+    scores = (qf @ kf.transpose(-2, -1).contiguous()) * scale
+    if is_causal:
+        rows = torch.arange(s_q, device=q.device)[:, None]
+        cols = torch.arange(s_k, device=q.device)[None, :]
+        scores = scores.masked_fill(cols > rows + (s_k - s_q), float("-inf"))
+    probs = torch.nan_to_num(torch.softmax(scores, dim=-1), nan=0.0)
+    dvf = probs.transpose(-2, -1).contiguous() @ dof
+    dp = dof @ vf.transpose(-2, -1).contiguous()
+    ds = probs * (dp - (dp * probs).sum(dim=-1, keepdim=True))
+    dqf = (ds @ kf) * scale
+    dkf = (ds.transpose(-2, -1).contiguous() @ qf) * scale
+    if group > 1:
+        dkf = dkf.view(b, h_kv, group, s_k, d).sum(dim=2)
+        dvf = dvf.view(b, h_kv, group, s_k, d).sum(dim=2)
+    return dqf.to(q.dtype), dkf.to(k.dtype), dvf.to(v.dtype)
+
+
+__all__ = ["attention_reference", "attention_reference_backward", "repeat_kv"]

@@ -20,7 +20,10 @@ import torch.nn as nn
 from stackkernels_amd._core.attention.decode import flash_decode as core_flash_decode
 from stackkernels_amd._core.attention.flash_bwd import flash_attn_bwd
 from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
-from stackkernels_amd._reference.torch.attention import attention_reference
+from stackkernels_amd._reference.torch.attention import (
+    attention_reference,
+    attention_reference_backward,
+)
 from stackkernels_amd.torch._dispatch import should_use_hip
 from stackkernels_amd.torch._utils import ensure_contiguous
 
@@ -140,36 +143,97 @@ class FlashAttention(nn.Module):
         return flash_attention(q, k, v, is_causal=self.is_causal, sm_scale=self.sm_scale)
 
 
-# torch.library custom op under the reference's name
-# (src/stackkernels/torch/attention.py:200-223): ``torch.ops.stackkernels.flash_attn_op``,
-# forward only, fake impl returns empty_like(q).  If that name is already
-# registered in this process (the original package imported alongside), the
-# existing registration is kept.
-def _register_custom_op() -> bool:
+# torch.library ops.  ``torch.ops.stackkernels.flash_attn_op`` keeps the
+# reference's name and schema (src/stackkernels/torch/attention.py:200-223)
+# and becomes differentiable: it is a composite of two ops of this package,
+# ``stackkernels_amd::attn_fwd`` (output and LSE) and ``attn_bwd``, each with
+# a fake (meta) implementation, and attn_fwd carries register_autograd, so
+# torch.compile graphs run both the forward and the backward without a graph
+# break.  If flash_attn_op is already registered in this process (the
+# original package imported alongside), that registration is kept.
+def _attn_fwd_impl(q, k, v, is_causal, sm_scale):
+    qc, kc, vc = ensure_contiguous(q), ensure_contiguous(k), ensure_contiguous(v)
+    if should_use_hip(qc):
+        return flash_attn_fwd(qc, kc, vc, is_causal=is_causal, sm_scale=sm_scale)
+    return attention_reference(qc, kc, vc, is_causal=is_causal, sm_scale=sm_scale)
+
+
+def _attn_bwd_impl(do, q, k, v, out, lse, is_causal, sm_scale):
+    do = ensure_contiguous(do)
+    if should_use_hip(q):
+        return flash_attn_bwd(do, q, k, v, out, lse, is_causal=is_causal, sm_scale=sm_scale)
+    return attention_reference_backward(do, q, k, v, is_causal=is_causal, sm_scale=sm_scale)
+
+
+def _register_ops() -> bool:
+    @torch.library.custom_op("stackkernels_amd::attn_fwd", mutates_args=())
+    def _attn_fwd_op(
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        is_causal: bool,
+        sm_scale: float,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        out, lse = _attn_fwd_impl(q, k, v, is_causal, sm_scale)
+        return out, lse
+
+    @_attn_fwd_op.register_fake
+    def _attn_fwd_fake(q, k, v, is_causal, sm_scale):
+        B, Hq, Sq, _ = q.shape
+        return torch.empty_like(q), q.new_empty((B, Hq, Sq), dtype=torch.float32)
+
+    @torch.library.custom_op("stackkernels_amd::attn_bwd", mutates_args=())
+    def _attn_bwd_op(
+        do: torch.Tensor,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        out: torch.Tensor,
+        lse: torch.Tensor,
+        is_causal: bool,
+        sm_scale: float,
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        dq, dk, dv = _attn_bwd_impl(do, q, k, v, out, lse, is_causal, sm_scale)
+        return dq, dk, dv
+
+    @_attn_bwd_op.register_fake
+    def _attn_bwd_fake(do, q, k, v, out, lse, is_causal, sm_scale):
+        return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+    def _setup_context(ctx, inputs, output):
+        q, k, v, is_causal, sm_scale = inputs
+        out, lse = output
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.is_causal = is_causal
+        ctx.sm_scale = sm_scale
+
+    def _backward(ctx, dout, dlse):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = torch.ops.stackkernels_amd.attn_bwd(
+            dout, q, k, v, out, lse, ctx.is_causal, ctx.sm_scale)
+        return dq, dk, dv, None, None
+
+    _attn_fwd_op.register_autograd(_backward, setup_context=_setup_context)
+
     try:
         torch.ops.stackkernels.flash_attn_op  # noqa: B018
         return False
     except (AttributeError, RuntimeError):
         pass
+    lib = torch.library.Library("stackkernels", "FRAGMENT")
+    lib.define("flash_attn_op(Tensor q, Tensor k, Tensor v, bool is_causal, float? sm_scale) -> Tensor")
 
-    @torch.library.custom_op("stackkernels::flash_attn_op", mutates_args=())
-    def _flash_attn_op(
-        q: torch.Tensor,
-        k: torch.Tensor,
-        v: torch.Tensor,
-        is_causal: bool,
-        sm_scale: float | None,
-    ) -> torch.Tensor:
-        return flash_attention(q, k, v, is_causal=is_causal, sm_scale=sm_scale)
+    def _flash_attn_op(q, k, v, is_causal, sm_scale):
+        scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else sm_scale
+        return torch.ops.stackkernels_amd.attn_fwd(q, k, v, is_causal, scale)[0]
 
-    @_flash_attn_op.register_fake
-    def _flash_attn_op_fake(q, k, v, is_causal, sm_scale):
-        return torch.empty_like(q)
-
+    lib.impl("flash_attn_op", _flash_attn_op, "CompositeImplicitAutograd")
+    _LIBS.append(lib)  # a Library's registrations last as long as the object
     return True
 
 
-_CUSTOM_OP_REGISTERED = _register_custom_op()
+_LIBS: list = []
+_CUSTOM_OP_REGISTERED = _register_ops()
 
 
 __all__ = [

@@ -18,7 +18,7 @@ from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
 from stackkernels_amd._reference.torch.attention import attention_reference
 from stackkernels_amd.torch import flash_attention
 
-from _gpu_util import TOL, assert_close_maxabs, make_qkv, native_loaded, np64
+from _gpu_util import TOL, assert_close_maxabs, make_qkv, native_loaded, np64, oracle_fwd
 
 pytestmark = pytest.mark.gpu
 
@@ -149,6 +149,26 @@ def test_backward_gqa_equals_mha_on_repeated_kv(device):
     assert torch.equal(dq, dq2)
     assert_close_maxabs(dk, dk2.float().view(1, 2, 4, 192, 64).sum(2), 2e-2, "dK")
     assert_close_maxabs(dv, dv2.float().view(1, 2, 4, 192, 64).sum(2), 2e-2, "dV")
+
+
+@pytest.mark.parametrize("compiled", [False, True])
+def test_custom_op_backward(device, compiled):
+    """torch.ops.stackkernels.flash_attn_op forward + backward on the device (the HIP
+    kernels through stackkernels_amd::attn_fwd / attn_bwd), eager and compiled."""
+    dt = torch.bfloat16
+    q, k, v = make_qkv(2, 8, 2, 96, 160, 128, dt, seed=7)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    fn = lambda a, b, c: torch.ops.stackkernels.flash_attn_op(a, b, c, True, None)  # noqa: E731
+    if compiled:
+        fn = torch.compile(fn, backend="aot_eager", fullgraph=True)
+    out = fn(q, k, v)
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(8)).to(dt)
+    out.backward(g.to(out.device))
+    assert native_loaded()
+    o_ref = oracle_fwd(q, k, v, True)[0]
+    assert_close_maxabs(out, o_ref, TOL[dt], "O")
+    _check(q, k, v, g, True, dt)
 
 
 def test_config3_full_size_backward(device):
