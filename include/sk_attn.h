@@ -34,7 +34,7 @@ extern "C" {
 #define SK_API
 #endif
 
-#define SK_ABI_VERSION 1
+#define SK_ABI_VERSION 2
 
 /* Element type codes. */
 #define SK_F32 0
@@ -132,6 +132,40 @@ SK_API int sk_decode(int dtype, const void* q, const void* k, const void* v, voi
 /* Scratch bytes sk_decode needs for an explicit split count. */
 SK_API int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,
                         size_t* workspace_bytes);
+
+/*
+ * sk_decode with a cache length per batch row: row b attends to keys
+ * [0, clamp(cache_seqlens[b], 0, Sk)) of its cache; a row with no key gives
+ * O = 0.  cache_seqlens is a device array of B int32.  Sk is the cache
+ * capacity and sets the split plan (sk_decode_plan / sk_decode_workspace
+ * with the same Sk).  The reference has no counterpart yet: it realises the
+ * per-sequence cache lengths its decode roadmap names (stubs
+ * src/stackkernels/_core/attention/varlen.py, paged.py; reference decode
+ * src/stackkernels/_core/attention/decode.py:192-312 takes one S_k for all rows).
+ */
+SK_API int sk_decode_varlen(int dtype, const void* q, const void* k, const void* v, void* o,
+                     void* workspace, size_t workspace_bytes, int num_splits,
+                     int B, int Hq, int Hkv, int Sk, int D,
+                     const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides,
+                     const int32_t* cache_seqlens, float sm_scale, void* stream);
+
+/*
+ * KV-cache append: k_cache[b, h, slots[b*T + t], :] = k[b, h, t, :] and the
+ * same for v, for b < B, h < Hkv, t < T.  k, v (B, Hkv, T, D); k_cache,
+ * v_cache (B, Hkv, S_cache, D); element strides (b, h, s) with a contiguous
+ * head dim; slots is a device array of B*T int64.  A slot outside
+ * [0, S_cache) skips its token (pad value -1).  Slots must be distinct
+ * within a batch row (tokens that share one race).  Realises the planned
+ * kv_cache_update(k, v, k_cache, v_cache, slot_indices)
+ * (reference: docs/user_guide/dropout_cache_sampling.md:66-72; stubs
+ * src/stackkernels/torch/cache.py, src/stackkernels/_core/cache/kv_update.py).
+ */
+SK_API int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_cache,
+                       void* v_cache, const int64_t* slots, int B, int Hkv, int T,
+                       int S_cache, int D, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* kc_strides,
+                       const int64_t* vc_strides, void* stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,14 @@ What it restates (all arithmetic in float64 unless a caller asks otherwise):
                               ``:154`` calls the non-causal reference with S_q = 1).
 * ``split_partials`` / ``combine_partials`` -- the split-KV decomposition and the
                               LSE-weighted merge of ``_core/attention/decode.py:81-121,166-186``.
+* ``decode_varlen``        -- decode with a cache length per batch row: row b is the
+                              reference decode over its first ``min(L_b, S_k)`` keys
+                              (zeros when none); the per-sequence cache lengths of the
+                              reference's decode roadmap (stubs ``_core/attention/varlen.py``,
+                              ``paged.py``), which has no implementation to follow.
+* ``kv_cache_update``      -- ``k_cache[b, h, slot[b, t]] = k[b, h, t]`` (and v), slots outside
+                              the cache skipped: the planned ``kv_cache_update``
+                              (``docs/user_guide/dropout_cache_sampling.md:66-72``).
 
 How each function is pinned (see ``tests/test_oracle.py``):
 
@@ -37,7 +45,11 @@ How each function is pinned (see ``tests/test_oracle.py``):
   ``LSE = score``, ``q = 0`` gives the mean of the visible V rows and
   ``LSE = log(#visible)``, fully masked rows give ``O = 0`` and
   ``LSE = -inf`` and zero gradients, and the split-KV merge is invariant to
-  the number of splits.
+  the number of splits;
+* ``decode_varlen`` against ``decode`` (all rows full), against
+  ``attention_forward`` on each row's sliced cache, against a brute-force loop,
+  and with empty and over-long rows; ``kv_cache_update`` against a
+  per-element loop, including padded (-1) and out-of-range slots.
 """
 
 from __future__ import annotations
@@ -213,6 +225,42 @@ def combine_partials(outs, lses):
                      / np.where(den > 0, den, 1.0)[..., None], 0.0)
         lse = np.where(finite, m + np.log(np.where(den > 0, den, 1.0)), NEG_INF)[..., 0]
     return o, lse
+
+
+def decode_varlen(q, k, v, seqlens, sm_scale=None):
+    """Decode where batch row b attends to keys ``[0, clamp(seqlens[b], 0, S_k))``.
+
+    Each row is ``decode`` over its sliced cache; a row with no key gives zeros.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    assert q.shape[2] == 1, "flash_decode requires q_len == 1"
+    sk = k.shape[2]
+    out = np.zeros(q.shape)
+    for b, n in enumerate(np.asarray(seqlens).reshape(-1)):
+        n = int(min(max(int(n), 0), sk))
+        if n > 0:
+            out[b:b + 1] = decode(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], sm_scale)
+    return out
+
+
+def kv_cache_update(k, v, k_cache, v_cache, slots):
+    """Return copies of the caches with ``cache[b, h, slots[b, t]] = new[b, h, t]``.
+
+    A slot outside ``[0, S_cache)`` skips its token; slots are distinct per row.
+    """
+    kc = np.array(k_cache, copy=True)
+    vc = np.array(v_cache, copy=True)
+    k = np.asarray(k)
+    v = np.asarray(v)
+    slots = np.asarray(slots)
+    s = kc.shape[2]
+    for b in range(slots.shape[0]):
+        keep = (slots[b] >= 0) & (slots[b] < s)
+        kc[b][:, slots[b][keep]] = k[b][:, keep]
+        vc[b][:, slots[b][keep]] = v[b][:, keep]
+    return kc, vc
 
 
 def attention_forward_loops(q, k, v, is_causal=False, sm_scale=None):

@@ -6,6 +6,8 @@ k/v (B, H_kv, S_k, D) with any b/h/s strides (no copy when rows are
 16-byte aligned), returns (B, H_q, 1, D) in q's dtype.  ``S_q != 1`` raises
 ``AssertionError`` as the reference does (``:212``).  The split count comes
 from the library's gfx950 table (``plan``) unless ``num_splits`` is given.
+``cache_seqlens`` gives each batch row its own cache length (decode over a
+batch of sequences of different lengths sharing one cache capacity).
 """
 
 from __future__ import annotations
@@ -36,11 +38,28 @@ def plan(dtype: torch.dtype, b: int, hq: int, hkv: int, sk: int, d: int) -> tupl
     return ns.value, nb.value
 
 
-def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None = None):
-    """Launch split + combine; see module docstring."""
+def _seqlens_operand(cache_seqlens, b: int, dev) -> torch.Tensor:
+    """cache_seqlens as the kernels read it: int32 (B,) on q's device."""
+    if not isinstance(cache_seqlens, torch.Tensor):
+        cache_seqlens = torch.as_tensor(cache_seqlens)
+    if cache_seqlens.dim() != 1 or cache_seqlens.shape[0] != b:
+        raise ValueError(f"cache_seqlens must have shape ({b},), got {tuple(cache_seqlens.shape)}")
+    if cache_seqlens.dtype.is_floating_point or cache_seqlens.dtype == torch.bool:
+        raise ValueError(f"cache_seqlens must be an integer tensor, got {cache_seqlens.dtype}")
+    return cache_seqlens.to(device=dev, dtype=torch.int32).contiguous()
+
+
+def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None = None,
+                 cache_seqlens=None):
+    """Launch split + combine; see module docstring.
+
+    ``cache_seqlens`` (optional, integer (B,)): row b attends to keys
+    ``[0, min(cache_seqlens[b], S_k))`` of its cache (S_k is the capacity);
+    a row with no key gives O = 0."""
     b, hq, hkv, sq, sk, d = validate_attention_layout(q, k, v)
     assert sq == 1, f"flash_decode requires q_len == 1, got {sq}"
     dev = check_device(q, k, v)
+    lens = None if cache_seqlens is None else _seqlens_operand(cache_seqlens, b, dev)
     scale = default_scale(d, sm_scale)
     dk = kernel_head_dim(d)
     qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k, v))
@@ -57,12 +76,20 @@ def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None 
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        rc = lib.sk_decode(
-            code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
-            ws.numel(), ns, b, hq, hkv, sk, dk,
-            _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
-            scale, stream_of(dev),
-        )
+        if lens is None:
+            rc = lib.sk_decode(
+                code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                ws.numel(), ns, b, hq, hkv, sk, dk,
+                _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+                scale, stream_of(dev),
+            )
+        else:
+            rc = lib.sk_decode_varlen(
+                code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                ws.numel(), ns, b, hq, hkv, sk, dk,
+                _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+                lens.data_ptr(), scale, stream_of(dev),
+            )
     _lib.check(rc, "flash_decode")
     if dk != d:
         out = out[..., :d].contiguous()

@@ -259,10 +259,15 @@ int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int nu
   return SK_OK;
 }
 
-int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, void* workspace,
-              size_t workspace_bytes, int num_splits, int B, int Hq, int Hkv, int Sk, int D,
-              const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-              const int64_t* o_strides, float sm_scale, void* stream) {
+}  // extern "C"
+
+// sk_decode and sk_decode_varlen: seqlens is null (every row sees all Sk keys)
+// or a device array of B per-row key counts.
+static int decode_impl(int dtype, const void* q, const void* k, const void* v, void* o,
+                       void* workspace, size_t workspace_bytes, int num_splits, int B, int Hq,
+                       int Hkv, int Sk, int D, const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides,
+                       const int32_t* seqlens, float sm_scale, void* stream) {
   g_err[0] = 0;
   int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
   if (rc) return rc;
@@ -301,6 +306,7 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
     p.scale_log2 = p.scale * 1.4426950408889634f;
     p.q_sign = sm_scale < 0.f ? 1u : 0u;
     p.n_mblocks = 1;
+    p.seqlens = seqlens;
     hipError_t e = sk::launch_fwd_f32(p, false, s);
     if (e != hipSuccess) return hip_fail(e, "sk_decode launch");
     return SK_OK;
@@ -319,6 +325,7 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
   p.scale = std::fabs(sm_scale);
   p.scale_log2 = p.scale * 1.4426950408889634f;
   p.q_sign = sm_scale < 0.f ? 0x80008000u : 0u;
+  p.seqlens = seqlens;
   if (num_splits > 1) {
     p.part_o = (float*)workspace;
     p.part_lse = p.part_o + (size_t)B * Hq * num_splits * p.dpad;
@@ -330,6 +337,64 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
     if (e != hipSuccess) return hip_fail(e, "sk_decode combine launch");
   }
   return SK_OK;
+}
+
+extern "C" {
+
+int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, void* workspace,
+              size_t workspace_bytes, int num_splits, int B, int Hq, int Hkv, int Sk, int D,
+              const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+              const int64_t* o_strides, float sm_scale, void* stream) {
+  return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
+                     q_strides, k_strides, v_strides, o_strides, nullptr, sm_scale, stream);
+}
+
+int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_cache, void* v_cache,
+                       const int64_t* slots, int B, int Hkv, int T, int S_cache, int D,
+                       const int64_t* k_strides, const int64_t* v_strides,
+                       const int64_t* kc_strides, const int64_t* vc_strides, void* stream) {
+  g_err[0] = 0;
+  if (dtype != SK_F32 && dtype != SK_F16 && dtype != SK_BF16)
+    return fail(SK_EUNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (B < 0 || Hkv <= 0 || T < 0 || S_cache < 0 || D <= 0)
+    return fail(SK_EINVAL, "invalid sizes B=%d Hkv=%d T=%d S_cache=%d D=%d", B, Hkv, T, S_cache, D);
+  const int64_t* sts[4] = {k_strides, v_strides, kc_strides, vc_strides};
+  const char* names[4] = {"k", "v", "k_cache", "v_cache"};
+  for (int i = 0; i < 4; ++i) {
+    if (!sts[i]) return fail(SK_EINVAL, "%s strides pointer is NULL", names[i]);
+    for (int j = 0; j < 3; ++j)
+      if (sts[i][j] < 0)
+        return fail(SK_EINVAL, "%s stride[%d]=%lld must be non-negative", names[i], j,
+                    (long long)sts[i][j]);
+  }
+  if ((int64_t)B * T == 0) return SK_OK;
+  const void* ptrs[5] = {k, v, k_cache, v_cache, slots};
+  const char* pnames[5] = {"k", "v", "k_cache", "v_cache", "slot_indices"};
+  for (int i = 0; i < 5; ++i)
+    if (!ptrs[i]) return fail(SK_EINVAL, "%s pointer is NULL", pnames[i]);
+  sk::CacheParams p{};
+  p.k = k, p.v = v, p.kc = k_cache, p.vc = v_cache, p.slots = slots;
+  p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_ss = v_strides[2];
+  p.kc_sb = kc_strides[0], p.kc_sh = kc_strides[1], p.kc_ss = kc_strides[2];
+  p.vc_sb = vc_strides[0], p.vc_sh = vc_strides[1], p.vc_ss = vc_strides[2];
+  p.B = B, p.Hkv = Hkv, p.T = T, p.S = S_cache;
+  p.esize = elem_bytes(dtype);
+  p.row_bytes = D * p.esize;
+  hipError_t e = sk::launch_kv_cache_update(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sk_kv_cache_update launch");
+  return SK_OK;
+}
+
+int sk_decode_varlen(int dtype, const void* q, const void* k, const void* v, void* o,
+                     void* workspace, size_t workspace_bytes, int num_splits, int B, int Hq,
+                     int Hkv, int Sk, int D, const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides,
+                     const int32_t* cache_seqlens, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  if (B > 0 && !cache_seqlens) return fail(SK_EINVAL, "cache_seqlens is null");
+  return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
+                     q_strides, k_strides, v_strides, o_strides, cache_seqlens, sm_scale, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,96 @@
+// KV-cache append for decode: write T new key/value rows per (batch, KV head)
+// into cache positions given per token.
+//
+// Realises the reference's planned kv_cache_update(k, v, k_cache, v_cache,
+// slot_indices) (docs/user_guide/dropout_cache_sampling.md:66-72; stub
+// modules src/stackkernels/torch/cache.py, src/stackkernels/_core/cache/kv_update.py).
+//
+// One thread moves one UNIT-byte chunk of one row of K and the same chunk of
+// V: consecutive threads walk a row's chunks, so every wave's loads and
+// stores are contiguous runs.  The slot of a token is read once per chunk
+// (it is the same for every chunk of a row, so those reads hit the cache).
+// A slot outside [0, S) skips the token, which lets callers pad ragged
+// batches with -1.  Plain byte copies: the cache holds exactly the input's
+// bits.
+#include "sk_common.h"
+#include "sk_kernels.h"
+
+namespace sk {
+
+template <int UNIT>
+struct CopyUnit;
+template <>
+struct CopyUnit<16> {
+  using type = u32x4;
+};
+template <>
+struct CopyUnit<8> {
+  using type = u32x2;
+};
+template <>
+struct CopyUnit<4> {
+  using type = uint32_t;
+};
+template <>
+struct CopyUnit<2> {
+  using type = uint16_t;
+};
+
+template <int UNIT>
+__global__ void __launch_bounds__(256) kv_cache_update_kernel(CacheParams p) {
+  using U = typename CopyUnit<UNIT>::type;
+  const int chunks = p.row_bytes / UNIT;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t rows = (int64_t)p.B * p.Hkv * p.T;
+  if (i >= rows * chunks) return;
+  const int64_t r = i / chunks;
+  const int c = (int)(i - r * chunks);
+  const int t = (int)(r % p.T);
+  const int64_t bh = r / p.T;
+  const int h = (int)(bh % p.Hkv);
+  const int b = (int)(bh / p.Hkv);
+  const int64_t slot = p.slots[(int64_t)b * p.T + t];
+  if (slot < 0 || slot >= p.S) return;
+  const int64_t e = p.esize;
+  const char* ks = (const char*)p.k + (b * p.k_sb + h * p.k_sh + t * p.k_ss) * e + (int64_t)c * UNIT;
+  const char* vs = (const char*)p.v + (b * p.v_sb + h * p.v_sh + t * p.v_ss) * e + (int64_t)c * UNIT;
+  char* kd = (char*)p.kc + (b * p.kc_sb + h * p.kc_sh + slot * p.kc_ss) * e + (int64_t)c * UNIT;
+  char* vd = (char*)p.vc + (b * p.vc_sb + h * p.vc_sh + slot * p.vc_ss) * e + (int64_t)c * UNIT;
+  const U kx = *reinterpret_cast<const U*>(ks);
+  const U vx = *reinterpret_cast<const U*>(vs);
+  *reinterpret_cast<U*>(kd) = kx;
+  *reinterpret_cast<U*>(vd) = vx;
+}
+
+// Largest copy unit (16, 8, 4 or 2 bytes) that divides the row and every
+// byte address and stride involved.
+static int copy_unit(const CacheParams& p) {
+  uint64_t bits = (uint64_t)p.row_bytes;
+  const void* ptrs[4] = {p.k, p.v, p.kc, p.vc};
+  for (const void* q : ptrs) bits |= (uint64_t)(uintptr_t)q;
+  const int64_t strides[12] = {p.k_sb, p.k_sh, p.k_ss, p.v_sb, p.v_sh, p.v_ss,
+                               p.kc_sb, p.kc_sh, p.kc_ss, p.vc_sb, p.vc_sh, p.vc_ss};
+  for (int64_t st : strides) bits |= (uint64_t)(st * p.esize);
+  for (int u = 16; u >= 2; u /= 2)
+    if ((bits & (uint64_t)(u - 1)) == 0) return u;
+  return 1;
+}
+
+hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s) {
+  const int unit = copy_unit(p);
+  if (unit < 2) return hipErrorInvalidValue;
+  const int64_t threads = (int64_t)p.B * p.Hkv * p.T * (p.row_bytes / unit);
+  if (threads == 0) return hipSuccess;
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)blocks);
+  switch (unit) {
+    case 16: hipLaunchKernelGGL(kv_cache_update_kernel<16>, grid, dim3(256), 0, s, p); break;
+    case 8: hipLaunchKernelGGL(kv_cache_update_kernel<8>, grid, dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL(kv_cache_update_kernel<4>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(kv_cache_update_kernel<2>, grid, dim3(256), 0, s, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sk

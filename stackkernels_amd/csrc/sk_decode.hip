@@ -57,7 +57,8 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   const int b = bk / p.Hkv;
   const int hkv = bk % p.Hkv;
   const int k_lo = split * p.keys_per_split;
-  const int k_hi = min(p.Sk, k_lo + p.keys_per_split);
+  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;  // this row's keys
+  const int k_hi = min(sk_b, k_lo + p.keys_per_split);
   const int n_tiles = k_hi > k_lo ? (k_hi - k_lo + BN - 1) / BN : 0;
 
   const int hd = 16 * wave + c16;  // head within the group for this lane's column
@@ -242,7 +243,8 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
   const int b = bk / p.Hkv;
   const int hkv = bk % p.Hkv;
   const int k_lo = split * p.keys_per_split;
-  const int k_hi = min(p.Sk, k_lo + p.keys_per_split);
+  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;  // this row's keys
+  const int k_hi = min(sk_b, k_lo + p.keys_per_split);
   const int n_tiles = k_hi > k_lo ? (k_hi - k_lo + BN - 1) / BN : 0;
 
   const int hd = 16 * wave + c16;  // head within the group for this lane's column

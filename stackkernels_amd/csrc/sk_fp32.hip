@@ -53,15 +53,17 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
     acc[i] = 0.f;
   }
   float m_run = kNegInf, l_run = 0.f;
-  int n_end = p.Sk;
-  if (CAUSAL) n_end = min(p.Sk, m0 + kF32Rows + diag);
-  const int lim = CAUSAL ? min(p.Sk - 1, row + diag) : p.Sk - 1;
+  // Keys this batch row sees: all S_k, or its cache length (decode).
+  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
+  int n_end = sk_b;
+  if (CAUSAL) n_end = min(sk_b, m0 + kF32Rows + diag);
+  const int lim = CAUSAL ? min(sk_b - 1, row + diag) : sk_b - 1;
 
   for (int n0 = 0; n0 < n_end; n0 += kF32Tile) {
     __syncthreads();
     for (int e = tid; e < kF32Tile * DP; e += 256) {
       const int r = e / DP, d = e % DP, n = n0 + r;
-      const bool ok = n < p.Sk && d < p.D;
+      const bool ok = n < sk_b && d < p.D;
       ks[r][d] = ok ? kbase[(int64_t)n * p.k_ss + d] : 0.f;
       vs[r][d] = ok ? vbase[(int64_t)n * p.v_ss + d] : 0.f;
     }

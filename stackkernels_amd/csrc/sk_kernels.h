@@ -26,6 +26,9 @@ struct FwdParams {
   float scale;       // |sm_scale|
   float scale_log2;  // |sm_scale| * log2(e)
   uint32_t q_sign;   // 0, or the sign-bit mask that negates q when sm_scale < 0
+  // Decode only (fp32 path, non-causal): null, or per-batch-row key counts;
+  // row b sees keys [0, clamp(seqlens[b], 0, Sk)).
+  const int* seqlens;
 };
 
 // Split-KV decode (Sq == 1).
@@ -44,6 +47,8 @@ struct DecParams {
   int num_splits, keys_per_split, dpad;
   float scale, scale_log2;
   uint32_t q_sign;
+  // Null, or per-batch-row key counts: row b sees keys [0, clamp(seqlens[b], 0, Sk)).
+  const int* seqlens;
 };
 
 // Backward attention; every tensor contiguous BHSD.
@@ -70,6 +75,23 @@ struct BwdParams {
   int n_mblocks, n_nblocks;
 };
 
+// KV-cache append: k_cache[b, h, slots[b*T + t], :] = k[b, h, t, :], same for v.
+// Strides are element strides (b, h, s); the head dim is contiguous.
+struct CacheParams {
+  const void* k;
+  const void* v;
+  void* kc;
+  void* vc;
+  const int64_t* slots;  // [B*T]; a slot outside [0, S) skips that token
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t kc_sb, kc_sh, kc_ss;
+  int64_t vc_sb, vc_sh, vc_ss;
+  int B, Hkv, T, S;
+  int esize;      // bytes per element
+  int row_bytes;  // D * esize
+};
+
 // Launchers: return hipSuccess or the launch error.  dtype is SK_F32/F16/BF16.
 hipError_t launch_fwd_mfma(int dtype, const FwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_fwd_f32(const FwdParams& p, bool causal, hipStream_t s);
@@ -78,6 +100,7 @@ hipError_t launch_decode_combine(int dtype, const DecParams& p, hipStream_t s);
 hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s);
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s);
+hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s);
 
 // Rows of queries one forward workgroup covers for (dtype, head dim).
 int fwd_rows_per_block(int dtype, int d);

@@ -7,4 +7,7 @@ from stackkernels_amd.torch.attention import (
     flash_decode,
 )
 
-__all__ = ["flash_attention", "flash_decode", "FlashAttention", "FlashAttentionFunction"]
+from stackkernels_amd.torch.cache import kv_cache_update
+
+__all__ = ["flash_attention", "flash_decode", "FlashAttention", "FlashAttentionFunction",
+           "kv_cache_update"]

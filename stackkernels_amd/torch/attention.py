@@ -105,19 +105,44 @@ def flash_decode(
     k: torch.Tensor,
     v: torch.Tensor,
     sm_scale: float | None = None,
+    cache_seqlens: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Split-KV decode for one query token (S_q = 1) over the whole cache.
 
     Args:
         q: (B, H_q, 1, D).  k, v: (B, H_kv, S_k, D); any b/h/s strides.
         sm_scale: score scale, default 1/sqrt(D).
+        cache_seqlens: optional integer (B,): row b attends to the first
+            ``min(cache_seqlens[b], S_k)`` keys of its cache; a row with no
+            key gives zeros.  Not in the reference, which decodes every row
+            over all S_k keys (``None``, the default, does the same).
 
     Returns:
         (B, H_q, 1, D) in q's dtype.
     """
     if should_use_hip(q):
-        return core_flash_decode(q, k, v, sm_scale=sm_scale)
-    out, _ = attention_reference(q, k, v, is_causal=False, sm_scale=sm_scale)
+        return core_flash_decode(q, k, v, sm_scale=sm_scale, cache_seqlens=cache_seqlens)
+    if cache_seqlens is None:
+        out, _ = attention_reference(q, k, v, is_causal=False, sm_scale=sm_scale)
+        return out
+    return _decode_varlen_reference(q, k, v, sm_scale, cache_seqlens)
+
+
+def _decode_varlen_reference(q, k, v, sm_scale, cache_seqlens):
+    """CPU path of flash_decode with per-row cache lengths: the reference
+    attention of each row over its first keys (zeros for an empty row)."""
+    b, _, sq, _ = q.shape
+    assert sq == 1, f"flash_decode requires q_len == 1, got {sq}"
+    lens = torch.as_tensor(cache_seqlens).to("cpu", torch.int64)
+    if lens.dim() != 1 or lens.shape[0] != b:
+        raise ValueError(f"cache_seqlens must have shape ({b},), got {tuple(lens.shape)}")
+    out = torch.zeros_like(q)
+    sk = k.shape[2]
+    for i in range(b):
+        n = int(min(max(int(lens[i]), 0), sk))
+        if n > 0:
+            out[i:i + 1], _ = attention_reference(q[i:i + 1], k[i:i + 1, :, :n], v[i:i + 1, :, :n],
+                                                  is_causal=False, sm_scale=sm_scale)
     return out
 
 

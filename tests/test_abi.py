@@ -30,7 +30,8 @@ def header_functions():
 def test_header_declares_expected_api():
     names = set(header_functions())
     assert {"sk_abi_version", "sk_last_error", "sk_attn_fwd", "sk_attn_bwd",
-            "sk_attn_bwd_workspace", "sk_decode_plan", "sk_decode", "sk_decode_workspace"} <= names
+            "sk_attn_bwd_workspace", "sk_decode_plan", "sk_decode", "sk_decode_workspace",
+            "sk_decode_varlen", "sk_kv_cache_update"} <= names
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -108,3 +109,26 @@ def test_bwd_workspace(lib):
     nb = ctypes.c_size_t()
     assert lib.sk_attn_bwd_workspace(2, 2, 32, 8, 2048, 8192, 128, 1, ctypes.byref(nb)) == 0
     assert nb.value >= 2 * 2 * 32 * 2048 * 4
+
+
+def test_varlen_and_cache_argument_errors(lib):
+    from stackkernels_amd._core.attention import _lib
+
+    st = _st(1024, 512, 64)
+    # sk_decode_varlen without the lengths array
+    rc = lib.sk_decode_varlen(2, 16, 16, 16, 16, 16, 1 << 20, 1, 1, 4, 2, 8, 64,
+                              st, st, st, st, None, 0.125, None)
+    assert rc == _lib.SK_EINVAL and "cache_seqlens" in _lib.last_error()
+
+    def upd(dtype=2, k=16, v=16, kc=16, vc=16, slots=16, B=1, H=2, T=3, S=8, D=64, sts=None):
+        s4 = sts or [st, st, st, st]
+        return lib.sk_kv_cache_update(dtype, k, v, kc, vc, slots, B, H, T, S, D, *s4, None)
+
+    assert upd(dtype=9) == _lib.SK_EUNSUPPORTED
+    assert upd(H=0) == _lib.SK_EINVAL and "invalid sizes" in _lib.last_error()
+    assert upd(D=0) == _lib.SK_EINVAL
+    assert upd(sts=[st, None, st, st]) == _lib.SK_EINVAL and "strides" in _lib.last_error()
+    assert upd(sts=[st, st, _st(-1, 0, 0), st]) == _lib.SK_EINVAL
+    assert upd(slots=None) == _lib.SK_EINVAL and "slot_indices" in _lib.last_error()
+    assert upd(T=0) == _lib.SK_OK  # nothing to write: no launch
+    assert upd(B=0, k=None) == _lib.SK_OK

@@ -204,3 +204,66 @@ def test_decode_is_noncausal_forward_and_causal_with_one_query():
     o = orc.decode(q, k, v)
     np.testing.assert_allclose(o, orc.attention_forward(q, k, v, False)[0], atol=1e-12)
     np.testing.assert_allclose(o, orc.attention_forward(q, k, v, True)[0], atol=1e-12)
+
+
+# ---- per-row cache lengths and the KV-cache append -------------------------
+
+def _dec_inputs(seed, b=3, hq=4, hkv=2, sk=19, d=8):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((b, hq, 1, d)), rng.standard_normal((b, hkv, sk, d)),
+            rng.standard_normal((b, hkv, sk, d)))
+
+
+def test_decode_varlen_full_rows_equal_decode():
+    q, k, v = _dec_inputs(0)
+    np.testing.assert_allclose(orc.decode_varlen(q, k, v, [19, 19, 19]), orc.decode(q, k, v),
+                               rtol=0, atol=1e-15)
+
+
+def test_decode_varlen_rows_equal_forward_on_sliced_cache():
+    # attention_forward is pinned by the golden vectors; each row must be it on its own slice
+    q, k, v = _dec_inputs(1)
+    lens = [5, 1, 19]
+    out = orc.decode_varlen(q, k, v, lens, 0.3)
+    for b, n in enumerate(lens):
+        ref, _ = orc.attention_forward(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], False, 0.3)
+        np.testing.assert_allclose(out[b:b + 1], ref, rtol=0, atol=1e-15)
+
+
+def test_decode_varlen_matches_loops():
+    q, k, v = _dec_inputs(2, b=2, hq=2, hkv=1, sk=6, d=4)
+    out = orc.decode_varlen(q, k, v, [4, 6])
+    for b, n in enumerate([4, 6]):
+        ref, _ = orc.attention_forward_loops(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n])
+        np.testing.assert_allclose(out[b:b + 1], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_varlen_empty_and_overlong_rows():
+    q, k, v = _dec_inputs(3)
+    out = orc.decode_varlen(q, k, v, [0, -3, 1000])
+    assert np.all(out[0] == 0) and np.all(out[1] == 0)
+    np.testing.assert_allclose(out[2:], orc.decode(q[2:], k[2:], v[2:]), rtol=0, atol=1e-15)
+    # a single visible key gives O = V of that key (softmax over one element)
+    one = orc.decode_varlen(q, k, v, [1, 1, 1])
+    np.testing.assert_allclose(one[:, :, 0], np.repeat(v[:, :, 0], 2, axis=1), rtol=0, atol=1e-15)
+
+
+def test_kv_cache_update_matches_loops():
+    rng = np.random.default_rng(4)
+    b, h, t, s, d = 2, 3, 5, 9, 4
+    k, v = rng.standard_normal((b, h, t, d)), rng.standard_normal((b, h, t, d))
+    kc, vc = rng.standard_normal((b, h, s, d)), rng.standard_normal((b, h, s, d))
+    slots = np.array([[3, 0, -1, 8, 5], [9, 2, 4, 100, 1]])
+    nk, nv = orc.kv_cache_update(k, v, kc, vc, slots)
+    ek, ev = kc.copy(), vc.copy()
+    for bi in range(b):
+        for ti in range(t):
+            sl = slots[bi, ti]
+            if 0 <= sl < s:
+                for hi in range(h):
+                    for di in range(d):
+                        ek[bi, hi, sl, di] = k[bi, hi, ti, di]
+                        ev[bi, hi, sl, di] = v[bi, hi, ti, di]
+    assert np.array_equal(nk, ek) and np.array_equal(nv, ev)
+    # untouched rows keep their contents; the inputs are not modified
+    assert np.array_equal(nk[0, :, 1], kc[0, :, 1]) and not np.array_equal(nk, kc)

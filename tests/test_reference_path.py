@@ -103,3 +103,28 @@ def test_launcher_rejects_bad_layouts(shapes, msg):
     q, k, v = (torch.zeros(s) for s in shapes)
     with pytest.raises(ValueError, match=msg):
         flash_attn_fwd(q, k, v)
+
+
+def test_decode_varlen_reference_path():
+    torch.manual_seed(3)
+    q, k, v = torch.randn(4, 8, 1, 32), torch.randn(4, 2, 40, 32), torch.randn(4, 2, 40, 32)
+    lens = torch.tensor([0, 1, 17, 99])
+    out = flash_decode(q, k, v, cache_seqlens=lens)
+    np.testing.assert_allclose(_np(out), orc.decode_varlen(_np(q), _np(k), _np(v), lens.numpy()),
+                               atol=1e-5)
+    with pytest.raises(ValueError, match="cache_seqlens"):
+        flash_decode(q, k, v, cache_seqlens=torch.tensor([1, 2]))
+
+
+def test_kv_cache_update_reference_path():
+    from stackkernels_amd.torch import kv_cache_update
+
+    torch.manual_seed(4)
+    k, v = torch.randn(2, 3, 4, 16), torch.randn(2, 3, 4, 16)
+    kc, vc = torch.randn(2, 3, 10, 16), torch.randn(2, 3, 10, 16)
+    slots = torch.tensor([[2, -1, 9, 0], [5, 6, 30, 1]])
+    ek, ev = orc.kv_cache_update(_np(k), _np(v), _np(kc), _np(vc), slots.numpy())
+    kv_cache_update(k, v, kc, vc, slots)
+    assert np.array_equal(_np(kc), ek) and np.array_equal(_np(vc), ev)
+    with pytest.raises(ValueError, match="slot_indices"):
+        kv_cache_update(k, v, kc, vc, slots[:1])
