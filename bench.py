@@ -14,8 +14,15 @@ Workloads (inputs synthetic, seeded, generated on the device):
                     D=128 (two KV buffer sets alternate so the 256 MB
                     Infinity Cache cannot hold the working set).
 
+* ``decode_varlen`` -- decode on the C4 cache with a seeded cache length per
+                    batch row, uniform in [1, S_k] (``cache_seqlens``).  GB/s over
+                    the keys each row sees + q read + O written.
+* ``kv_update``  -- in-place append of 128 new key/value tokens per row into the
+                    C4 cache at seeded distinct slots (``kv_cache_update``).  GB/s
+                    over the new K/V read + the cache rows written + the slots.
+
 ``python bench.py`` runs ``fwd`` as the headline (``value``) and, unless
-``--no-extra``, the other three as entries of ``extra``.  Each line carries a
+``--no-extra``, the others as entries of ``extra``.  Each line carries a
 ``roofline`` object for the dominant kernel (algorithmic work per launch over
 the average launch time measured with HIP events on the launch stream) and a
 ``cpu_baseline`` measured on this host with the PyTorch reference path
@@ -51,6 +58,8 @@ HBM_TRAFFIC_BYTES = {
     "fwdbwd": 788_786_752,
     "decode": 8_612_428_279,
     "decode_mqa": 572_983_785,
+    "decode_varlen": 4_305_177_417,
+    "kv_update": 67_274_953,
 }
 
 
@@ -71,7 +80,30 @@ WORKLOADS = {
                    causal=False, dtype="bf16", kind="decode"),
     "decode_mqa": dict(name="C5 flash_decode fp16 MQA start_pos=Sk-1", B=8, Hq=64, Hkv=1, Sq=1,
                        Sk=131072, D=128, causal=False, dtype="fp16", kind="decode"),
+    # Next-row workloads (per-row cache lengths, in-place cache append) on the C4 cache.
+    "decode_varlen": dict(name="flash_decode bf16 GQA, C4 cache, per-row lengths U[1, Sk]", B=64,
+                          Hq=32, Hkv=8, Sq=1, Sk=32768, D=128, causal=False, dtype="bf16",
+                          kind="decode_varlen"),
+    "kv_update": dict(name="kv_cache_update bf16, C4 cache, 128 new tokens per row", B=64, Hq=32,
+                      Hkv=8, Sq=128, Sk=32768, D=128, causal=False, dtype="bf16",
+                      kind="kv_update"),
 }
+
+
+def varlen_lengths(w: dict):
+    """Seeded per-row cache lengths of the decode_varlen workload, uniform in [1, Sk]."""
+    import torch
+
+    g = torch.Generator().manual_seed(3)
+    return torch.randint(1, w["Sk"] + 1, (w["B"],), generator=g, dtype=torch.int32)
+
+
+def update_slots(w: dict):
+    """Seeded distinct cache slots of the kv_update workload: (B, T) int64."""
+    import torch
+
+    g = torch.Generator().manual_seed(4)
+    return torch.stack([torch.randperm(w["Sk"], generator=g)[:w["Sq"]] for _ in range(w["B"])])
 
 
 def work_units(w: dict) -> tuple[float, str]:
@@ -81,6 +113,14 @@ def work_units(w: dict) -> tuple[float, str]:
         kv = 2 * w["B"] * w["Hkv"] * w["Sk"] * w["D"] * esz
         qo = 2 * w["B"] * w["Hq"] * w["D"] * esz
         return float(kv + qo), "GB/s"
+    if w["kind"] == "decode_varlen":
+        esz = 2
+        kv = 2 * int(varlen_lengths(w).sum()) * w["Hkv"] * w["D"] * esz  # the keys each row sees
+        qo = 2 * w["B"] * w["Hq"] * w["D"] * esz
+        return float(kv + qo), "GB/s"
+    if w["kind"] == "kv_update":
+        rows = w["B"] * w["Hkv"] * w["Sq"]
+        return float(4 * rows * w["D"] * 2 + w["B"] * w["Sq"] * 8), "GB/s"  # K, V read + written
     pairs = causal_pairs(w["Sq"], w["Sk"], w["causal"])
     per = 4 if w["kind"] == "fwd" else 14
     return float(per * w["D"] * pairs * w["B"] * w["Hq"]), "TFLOP/s"
@@ -94,6 +134,13 @@ def _make_inputs(w: dict, torch, dev, sets: int = 1):
     dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float16
     g = torch.Generator(device=dev).manual_seed(0)
     out = []
+    if w["kind"] == "kv_update":  # (new k, new v, k_cache, v_cache)
+        shp_new = (w["B"], w["Hkv"], w["Sq"], w["D"])
+        shp_cache = (w["B"], w["Hkv"], w["Sk"], w["D"])
+        return [(torch.randn(shp_new, generator=g, device=dev, dtype=dt),
+                 torch.randn(shp_new, generator=g, device=dev, dtype=dt),
+                 torch.randn(shp_cache, generator=g, device=dev, dtype=dt),
+                 torch.randn(shp_cache, generator=g, device=dev, dtype=dt))]
     for _ in range(sets):
         q = torch.randn(w["B"], w["Hq"], w["Sq"], w["D"], generator=g, device=dev, dtype=dt)
         k = torch.randn(w["B"], w["Hkv"], w["Sk"], w["D"], generator=g, device=dev, dtype=dt)
@@ -119,6 +166,34 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
     B, Hq, Hkv, Sq, Sk, D = (w[k_] for k_ in ("B", "Hq", "Hkv", "Sq", "Sk", "D"))
     scale = 1.0 / math.sqrt(D)
     q0 = inputs[0][0]
+    if w["kind"] == "kv_update":
+        kn, vn, kc, vc = inputs[0]
+        slots = update_slots(w).to(dev)
+        sts = [_lib.strides3(t) for t in (kn, vn, kc, vc)]
+
+        def launch(i):
+            rc = lib.sk_kv_cache_update(code, kn.data_ptr(), vn.data_ptr(), kc.data_ptr(),
+                                        vc.data_ptr(), slots.data_ptr(), B, Hkv, Sq, Sk, D,
+                                        *sts, stream)
+            _lib.check(rc, "sk_kv_cache_update")
+        return launch
+    if w["kind"] == "decode_varlen":
+        ns = ctypes.c_int(0)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+                   "plan")
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+        q, k, v = inputs[0]
+        o = torch.empty_like(q)
+        lens = varlen_lengths(w).to(dev)
+        sts = [_lib.strides3(t) for t in (q, k, v, o)]
+
+        def launch(i):
+            rc = lib.sk_decode_varlen(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), ns.value, B, Hq, Hkv, Sk, D,
+                                      *sts, lens.data_ptr(), scale, stream)
+            _lib.check(rc, "sk_decode_varlen")
+        return launch
     if w["kind"] == "decode":
         ns = ctypes.c_int(0)
         nb = ctypes.c_size_t(0)
@@ -236,6 +311,23 @@ def run_gpu(w: dict, steps: int, warmup: int):
         def step(i):
             q, k, v = inputs[i % sets]
             flash_decode(q, k, v)
+    elif w["kind"] == "decode_varlen":
+        q0 = inputs[0][0]
+        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        lens_dev = varlen_lengths(w).to(dev)
+        details["mean_length"] = round(float(lens_dev.float().mean()), 1)
+
+        def step(i):
+            q, k, v = inputs[0]
+            flash_decode(q, k, v, cache_seqlens=lens_dev)
+    elif w["kind"] == "kv_update":
+        from stackkernels_amd.torch.cache import kv_cache_update
+
+        slots_dev = update_slots(w).to(dev)
+
+        def step(i):
+            kn, vn, kc, vc = inputs[0]
+            kv_cache_update(kn, vn, kc, vc, slots_dev)
     elif w["kind"] == "fwd":
         def step(i):
             q, k, v = inputs[0]
@@ -259,6 +351,53 @@ def run_gpu(w: dict, steps: int, warmup: int):
     return ms_step, mean, details
 
 
+def _cpu_baseline_next_rows(w: dict, budget_s: float):
+    """CPU baseline of the next-row workloads: this build's own CPU path on one batch
+    row (decode over row 0's cache length; the cache append of row 0's tokens)."""
+    import torch
+
+    from stackkernels_amd.torch.attention import flash_decode
+    from stackkernels_amd.torch.cache import kv_cache_update
+
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(0)
+    D, Hq, Hkv = w["D"], w["Hq"], w["Hkv"]
+    if w["kind"] == "decode_varlen":
+        n = int(varlen_lengths(w)[0])
+        q = torch.randn(1, Hq, 1, D, generator=g).bfloat16()
+        k = torch.randn(1, Hkv, n, D, generator=g).bfloat16()
+        v = torch.randn(1, Hkv, n, D, generator=g).bfloat16()
+        units_one = 2 * n * Hkv * D * 2 + 2 * Hq * D * 2
+        fn = lambda: flash_decode(q, k, v, cache_seqlens=torch.tensor([n]))  # noqa: E731
+        what = f"flash_decode reference path on batch row 0 (length {n}, {Hq} query heads)"
+    else:
+        T = w["Sq"]
+        kn = torch.randn(1, Hkv, T, D, generator=g).bfloat16()
+        vn = torch.randn(1, Hkv, T, D, generator=g).bfloat16()
+        kc = torch.zeros(1, Hkv, w["Sk"], D, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        sl = update_slots(w)[:1]
+        units_one = 4 * Hkv * T * D * 2 + T * 8
+        fn = lambda: kv_cache_update(kn, vn, kc, vc, sl)  # noqa: E731
+        what = f"kv_cache_update reference path (torch indexing) on batch row 0 ({T} tokens)"
+    done = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {
+        "value": round(_rate(units_one * done, "GB/s", el), 6),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{what} of {w['name']}, {done} repetition(s) in {el:.1f} s; "
+                   f"host {os.cpu_count()} CPUs, torch threads {threads}"),
+    }
+
+
 def run_cpu_baseline(w: dict, budget_s: float):
     """The reference's CPU algorithm (fp32 torch, ``attention_reference``) on a bounded
     sample of the workload: one batch row, KV-head groups in turn, repeated until
@@ -267,6 +406,8 @@ def run_cpu_baseline(w: dict, budget_s: float):
 
     from stackkernels_amd._reference.torch.attention import attention_reference
 
+    if w["kind"] in ("decode_varlen", "kv_update"):
+        return _cpu_baseline_next_rows(w, budget_s)
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
     grp = w["Hq"] // w["Hkv"]
@@ -313,10 +454,12 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
     ms_step, ms_kernel, details = run_gpu(w, steps, warmup)
     value = _rate(units, unit, ms_step / 1e3)
     achieved = _rate(units, unit, ms_kernel / 1e3)
-    bound = "hbm" if w["kind"] == "decode" else "mfma"
+    bound = "hbm" if unit == "GB/s" else "mfma"
     peak = PEAK_HBM_GBPS if bound == "hbm" else PEAK_BF16_TFLOPS
     kernel = {"fwd": "fwd_mfma_kernel", "fwdbwd": "fwd + bwd kernels",
-              "decode": "decode_split_kernel + decode_combine_kernel"}[w["kind"]]
+              "decode": "decode_split_kernel + decode_combine_kernel",
+              "decode_varlen": "decode_split_kernel + decode_combine_kernel",
+              "kv_update": "kv_cache_update_kernel"}[w["kind"]]
     if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
         kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
     res = {

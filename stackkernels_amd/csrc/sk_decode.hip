@@ -56,9 +56,14 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   const int bk = blockIdx.y;
   const int b = bk / p.Hkv;
   const int hkv = bk % p.Hkv;
-  const int k_lo = split * p.keys_per_split;
-  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;  // this row's keys
-  const int k_hi = min(sk_b, k_lo + p.keys_per_split);
+  // Keys this row sees: all S_k, or its cache length.  With per-row lengths
+  // the row's keys are spread over all its splits (32-key multiples), so a
+  // short row does not leave most of its workgroups empty.
+  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
+  const int kps = p.seqlens ? max(32, ((sk_b + p.num_splits - 1) / p.num_splits + 31) / 32 * 32)
+                            : p.keys_per_split;
+  const int k_lo = split * kps;
+  const int k_hi = min(sk_b, k_lo + kps);
   const int n_tiles = k_hi > k_lo ? (k_hi - k_lo + BN - 1) / BN : 0;
 
   const int hd = 16 * wave + c16;  // head within the group for this lane's column
@@ -242,9 +247,14 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
   const int bk = blockIdx.y;
   const int b = bk / p.Hkv;
   const int hkv = bk % p.Hkv;
-  const int k_lo = split * p.keys_per_split;
-  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;  // this row's keys
-  const int k_hi = min(sk_b, k_lo + p.keys_per_split);
+  // Keys this row sees: all S_k, or its cache length.  With per-row lengths
+  // the row's keys are spread over all its splits (32-key multiples), so a
+  // short row does not leave most of its workgroups empty.
+  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
+  const int kps = p.seqlens ? max(32, ((sk_b + p.num_splits - 1) / p.num_splits + 31) / 32 * 32)
+                            : p.keys_per_split;
+  const int k_lo = split * kps;
+  const int k_hi = min(sk_b, k_lo + kps);
   const int n_tiles = k_hi > k_lo ? (k_hi - k_lo + BN - 1) / BN : 0;
 
   const int hd = 16 * wave + c16;  // head within the group for this lane's column
