@@ -34,7 +34,7 @@ extern "C" {
 #define SK_API
 #endif
 
-#define SK_ABI_VERSION 2
+#define SK_ABI_VERSION 3
 
 /* Element type codes. */
 #define SK_F32 0
@@ -151,6 +151,26 @@ SK_API int sk_decode_varlen(int dtype, const void* q, const void* k, const void*
                      const int32_t* cache_seqlens, float sm_scale, void* stream);
 
 /*
+ * sk_decode_varlen over a paged cache.  k_pool, v_pool hold num_pages pages of
+ * page_size keys (element strides: page, head, in-page row; contiguous head
+ * dim); key j of batch row b is in-page row j % page_size of page
+ * block_table[b * max_pages + j / page_size], for j < cache_seqlens[b]
+ * (clamped to max_pages * page_size).  page_size is a positive multiple of 32;
+ * a page index outside [0, num_pages) masks its keys.  block_table (B x
+ * max_pages int32) and cache_seqlens (B int32) live on the device.  Plan the
+ * splits with Sk = max_pages * page_size.  The reference has no counterpart
+ * yet: it realises the paged KV decode of its roadmap (stub
+ * src/stackkernels/_core/attention/paged.py).
+ */
+SK_API int sk_decode_paged(int dtype, const void* q, const void* k_pool, const void* v_pool,
+                    void* o, void* workspace, size_t workspace_bytes, int num_splits,
+                    int B, int Hq, int Hkv, int num_pages, int page_size, int max_pages, int D,
+                    const int64_t* q_strides, const int64_t* kp_strides,
+                    const int64_t* vp_strides, const int64_t* o_strides,
+                    const int32_t* block_table, const int32_t* cache_seqlens,
+                    float sm_scale, void* stream);
+
+/*
  * KV-cache append: k_cache[b, h, slots[b*T + t], :] = k[b, h, t, :] and the
  * same for v, for b < B, h < Hkv, t < T.  k, v (B, Hkv, T, D); k_cache,
  * v_cache (B, Hkv, S_cache, D); element strides (b, h, s) with a contiguous
@@ -166,6 +186,22 @@ SK_API int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_c
                        int S_cache, int D, const int64_t* k_strides,
                        const int64_t* v_strides, const int64_t* kc_strides,
                        const int64_t* vc_strides, void* stream);
+
+/*
+ * KV-cache append into a paged pool: token t of batch row b goes to in-page
+ * row s % page_size of page s / page_size, s = slot_mapping[b*T + t], for
+ * s in [0, num_pages * page_size) (other values skip the token).  Pool
+ * element strides: page, head, in-page row.  Realises the planned
+ * kv_cache_update for paged caches (reference:
+ * docs/user_guide/dropout_cache_sampling.md:66-72, stub
+ * src/stackkernels/_core/cache/kv_update.py).
+ */
+SK_API int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, void* k_pool,
+                             void* v_pool, const int64_t* slot_mapping, int B, int Hkv,
+                             int T, int num_pages, int page_size, int D,
+                             const int64_t* k_strides, const int64_t* v_strides,
+                             const int64_t* kp_strides, const int64_t* vp_strides,
+                             void* stream);
 
 #ifdef __cplusplus
 }

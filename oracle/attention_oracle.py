@@ -30,6 +30,11 @@ What it restates (all arithmetic in float64 unless a caller asks otherwise):
 * ``kv_cache_update``      -- ``k_cache[b, h, slot[b, t]] = k[b, h, t]`` (and v), slots outside
                               the cache skipped: the planned ``kv_cache_update``
                               (``docs/user_guide/dropout_cache_sampling.md:66-72``).
+* ``gather_pages`` / ``decode_paged`` / ``kv_cache_update_paged`` -- the same two
+                              operations on a paged pool (key j of row b in page
+                              ``table[b, j // page_size]``, row ``j % page_size``; a page
+                              outside the pool masks its keys): the paged KV decode of
+                              the roadmap (stub ``_core/attention/paged.py``).
 
 How each function is pinned (see ``tests/test_oracle.py``):
 
@@ -49,7 +54,10 @@ How each function is pinned (see ``tests/test_oracle.py``):
 * ``decode_varlen`` against ``decode`` (all rows full), against
   ``attention_forward`` on each row's sliced cache, against a brute-force loop,
   and with empty and over-long rows; ``kv_cache_update`` against a
-  per-element loop, including padded (-1) and out-of-range slots.
+  per-element loop, including padded (-1) and out-of-range slots;
+  ``decode_paged`` against ``decode_varlen`` on caches assembled page by page
+  with a loop, and with a page index outside the pool against the same row
+  cut at that page; ``kv_cache_update_paged`` against a per-element loop.
 """
 
 from __future__ import annotations
@@ -261,6 +269,54 @@ def kv_cache_update(k, v, k_cache, v_cache, slots):
         kc[b][:, slots[b][keep]] = k[b][:, keep]
         vc[b][:, slots[b][keep]] = v[b][:, keep]
     return kc, vc
+
+
+def gather_pages(pool, table):
+    """(num_pages, H_kv, page_size, D) pool and (B, max_pages) table ->
+    (B, H_kv, max_pages * page_size, D) caches, and a (B, max_pages * page_size)
+    mask that is False for keys whose page lies outside the pool."""
+    pool = np.asarray(pool, dtype=np.float64)
+    table = np.asarray(table)
+    n_pages, hkv, ps, d = pool.shape
+    b, mp = table.shape
+    valid = (table >= 0) & (table < n_pages)
+    rows = pool[np.where(valid, table, 0)]  # (B, max_pages, H_kv, page_size, D)
+    cache = rows.transpose(0, 2, 1, 3, 4).reshape(b, hkv, mp * ps, d)
+    return cache, np.repeat(valid, ps, axis=1)
+
+
+def decode_paged(q, k_pool, v_pool, table, seqlens, sm_scale=None):
+    """Decode over a paged pool: row b sees keys j < clamp(seqlens[b], 0,
+    max_pages * page_size) whose page is inside the pool."""
+    q = np.asarray(q, dtype=np.float64)
+    k, kv_ok = gather_pages(k_pool, table)
+    v, _ = gather_pages(v_pool, table)
+    sk = k.shape[2]
+    out = np.zeros(q.shape)
+    for b, n in enumerate(np.asarray(seqlens).reshape(-1)):
+        n = int(min(max(int(n), 0), sk))
+        keep = np.nonzero(kv_ok[b, :n])[0]
+        if keep.size:
+            out[b:b + 1] = decode(q[b:b + 1], k[b:b + 1][:, :, keep], v[b:b + 1][:, :, keep], sm_scale)
+    return out
+
+
+def kv_cache_update_paged(k, v, k_pool, v_pool, slots):
+    """Return copies of the pools with ``pool[s // ps, h, s % ps] = new[b, h, t]``,
+    s = slots[b, t]; a slot outside the pool skips its token."""
+    kp = np.array(k_pool, copy=True)
+    vp = np.array(v_pool, copy=True)
+    k = np.asarray(k)
+    v = np.asarray(v)
+    slots = np.asarray(slots)
+    n_pages, _, ps, _ = kp.shape
+    for b in range(slots.shape[0]):
+        for t in range(slots.shape[1]):
+            s = int(slots[b, t])
+            if 0 <= s < n_pages * ps:
+                kp[s // ps, :, s % ps] = k[b, :, t]
+                vp[s // ps, :, s % ps] = v[b, :, t]
+    return kp, vp
 
 
 def attention_forward_loops(q, k, v, is_causal=False, sm_scale=None):

@@ -96,4 +96,73 @@ def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None 
     return out
 
 
-__all__ = ["flash_decode", "plan"]
+def _table_operand(block_table, b: int, dev) -> torch.Tensor:
+    if not isinstance(block_table, torch.Tensor):
+        block_table = torch.as_tensor(block_table)
+    if block_table.dim() != 2 or block_table.shape[0] != b:
+        raise ValueError(f"block_table must have shape ({b}, max_pages), got "
+                         f"{tuple(block_table.shape)}")
+    if block_table.dtype.is_floating_point or block_table.dtype == torch.bool:
+        raise ValueError(f"block_table must be an integer tensor, got {block_table.dtype}")
+    return block_table.to(device=dev, dtype=torch.int32).contiguous()
+
+
+def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
+                       sm_scale: float | None = None, num_splits: int | None = None):
+    """Decode over a paged KV cache.
+
+    q (B, H_q, 1, D); k_pool, v_pool (num_pages, H_kv, page_size, D) with any
+    page/head/row strides; block_table integer (B, max_pages): page of each
+    page_size-key block of a row; cache_seqlens integer (B,): keys per row.
+    Key j of row b is row ``j % page_size`` of page ``block_table[b, j // page_size]``.
+    page_size must be a multiple of 32.  A page index outside the pool masks
+    its keys; a row with no key gives zeros.  Returns (B, H_q, 1, D)."""
+    if q.dim() != 4 or k_pool.dim() != 4 or v_pool.dim() != 4:
+        raise ValueError("Expected 4D q (B, H, 1, D) and 4D page pools (pages, H_kv, page_size, D)")
+    if k_pool.shape != v_pool.shape:
+        raise ValueError(f"k_pool and v_pool shapes differ: {tuple(k_pool.shape)} vs "
+                         f"{tuple(v_pool.shape)}")
+    b, hq, sq, d = q.shape
+    num_pages, hkv, page_size, dk_ = k_pool.shape
+    assert sq == 1, f"flash_decode requires q_len == 1, got {sq}"
+    if dk_ != d:
+        raise ValueError(f"Head dimension mismatch: q has {d}, k has {dk_}")
+    if hq % hkv != 0:
+        raise ValueError(f"Query heads ({hq}) must be divisible by KV heads ({hkv}) for GQA/MQA")
+    if page_size <= 0 or page_size % 32 != 0:
+        raise ValueError(f"page_size (k_pool.shape[2]) must be a positive multiple of 32, "
+                         f"got {page_size}")
+    dev = check_device(q, k_pool, v_pool)
+    table = _table_operand(block_table, b, dev)
+    lens = _seqlens_operand(cache_seqlens, b, dev)
+    max_pages = table.shape[1]
+    scale = default_scale(d, sm_scale)
+    dk = kernel_head_dim(d)
+    qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k_pool, v_pool))
+    lib = _lib.load()
+    code = _lib.dtype_code(q.dtype)
+    sk = max_pages * page_size
+    if num_splits is None:
+        ns, nbytes = plan(q.dtype, b, hq, hkv, sk, d)
+    else:
+        ns = int(num_splits)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_workspace(code, b, hq, hkv, sk, dk, ns, ctypes.byref(nb)),
+                   "flash_decode")
+        nbytes = nb.value
+    out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.sk_decode_paged(
+            code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
+            ws.numel(), ns, b, hq, hkv, num_pages, page_size, max_pages, dk,
+            _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+            table.data_ptr(), lens.data_ptr(), scale, stream_of(dev),
+        )
+    _lib.check(rc, "flash_decode")
+    if dk != d:
+        out = out[..., :d].contiguous()
+    return out
+
+
+__all__ = ["flash_decode", "flash_decode_paged", "plan"]

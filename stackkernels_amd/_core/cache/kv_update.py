@@ -16,8 +16,10 @@ from stackkernels_amd._core.attention import _lib
 from stackkernels_amd._core.attention._common import check_device, stream_of
 
 
-def validate_cache_update(k, v, k_cache, v_cache, slot_indices) -> tuple[int, int, int, int, int]:
-    """Shapes (B, Hkv, T, S_cache, D); raises ValueError on a mismatch."""
+def validate_cache_update(k, v, k_cache, v_cache, slot_indices,
+                          paged: bool = False) -> tuple[int, int, int, int, int]:
+    """Shapes (B, Hkv, T, S_cache, D) -- for a paged pool S_cache is the pool's
+    num_pages * page_size slots; raises ValueError on a mismatch."""
     for name, t in (("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache)):
         if t.dim() != 4:
             raise ValueError(f"Expected 4D tensor for {name} (B, H, S, D), got {t.dim()}D")
@@ -28,7 +30,11 @@ def validate_cache_update(k, v, k_cache, v_cache, slot_indices) -> tuple[int, in
                          f"{tuple(v_cache.shape)}")
     b, h, t, d = k.shape
     bc, hc, s, dc = k_cache.shape
-    if (bc, hc, dc) != (b, h, d):
+    if paged:
+        if (hc, dc) != (h, d):
+            raise ValueError(f"pool (H, D) = {(hc, dc)} does not match new keys' {(h, d)}")
+        s = bc * s  # pool slots: num_pages * page_size
+    elif (bc, hc, dc) != (b, h, d):
         raise ValueError(f"cache (B, H, D) = {(bc, hc, dc)} does not match new keys' {(b, h, d)}")
     if tuple(slot_indices.shape) != (b, t):
         raise ValueError(f"slot_indices must have shape ({b}, {t}), got {tuple(slot_indices.shape)}")
@@ -40,20 +46,26 @@ def validate_cache_update(k, v, k_cache, v_cache, slot_indices) -> tuple[int, in
     return b, h, t, s, d
 
 
-def kv_cache_update(k, v, k_cache, v_cache, slot_indices) -> None:
+def kv_cache_update(k, v, k_cache, v_cache, slot_indices, paged: bool = False) -> None:
     """Write k, v (B, Hkv, T, D) into k_cache, v_cache (B, Hkv, S_cache, D) at
-    slot_indices (B, T); in place, on the caches' stream."""
-    b, h, t, s, d = validate_cache_update(k, v, k_cache, v_cache, slot_indices)
+    slot_indices (B, T); in place, on the caches' stream.  With ``paged`` the
+    caches are page pools (num_pages, Hkv, page_size, D) and a slot s is row
+    ``s % page_size`` of page ``s // page_size``."""
+    b, h, t, s, d = validate_cache_update(k, v, k_cache, v_cache, slot_indices, paged)
     dev = check_device(k, v, k_cache, v_cache)
     slots = slot_indices.to(device=dev, dtype=torch.int64).contiguous()
     lib = _lib.load()
+    sts = (_lib.strides3(k), _lib.strides3(v), _lib.strides3(k_cache), _lib.strides3(v_cache))
     with torch.cuda.device(dev):
-        rc = lib.sk_kv_cache_update(
-            _lib.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
-            v_cache.data_ptr(), slots.data_ptr(), b, h, t, s, d,
-            _lib.strides3(k), _lib.strides3(v), _lib.strides3(k_cache), _lib.strides3(v_cache),
-            stream_of(dev),
-        )
+        if paged:
+            rc = lib.sk_kv_cache_update_paged(
+                _lib.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
+                v_cache.data_ptr(), slots.data_ptr(), b, h, t, k_cache.shape[0],
+                k_cache.shape[2], d, *sts, stream_of(dev))
+        else:
+            rc = lib.sk_kv_cache_update(
+                _lib.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
+                v_cache.data_ptr(), slots.data_ptr(), b, h, t, s, d, *sts, stream_of(dev))
     _lib.check(rc, "kv_cache_update")
 
 

@@ -261,13 +261,21 @@ int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int nu
 
 }  // extern "C"
 
-// sk_decode and sk_decode_varlen: seqlens is null (every row sees all Sk keys)
-// or a device array of B per-row key counts.
+// Paged cache of the decode entry points (block_table null: contiguous).
+struct PagedCache {
+  const int32_t* block_table = nullptr;
+  int page_size = 0, max_pages = 0, num_pages = 0;
+};
+
+// sk_decode, sk_decode_varlen and sk_decode_paged: seqlens is null (every row
+// sees all Sk keys) or a device array of B per-row key counts; pc describes a
+// paged cache (then Sk = max_pages * page_size).
 static int decode_impl(int dtype, const void* q, const void* k, const void* v, void* o,
                        void* workspace, size_t workspace_bytes, int num_splits, int B, int Hq,
                        int Hkv, int Sk, int D, const int64_t* q_strides, const int64_t* k_strides,
                        const int64_t* v_strides, const int64_t* o_strides,
-                       const int32_t* seqlens, float sm_scale, void* stream) {
+                       const int32_t* seqlens, const PagedCache& pc, float sm_scale,
+                       void* stream) {
   g_err[0] = 0;
   int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
   if (rc) return rc;
@@ -307,6 +315,8 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
     p.q_sign = sm_scale < 0.f ? 1u : 0u;
     p.n_mblocks = 1;
     p.seqlens = seqlens;
+    p.block_table = pc.block_table;
+    p.page_size = pc.page_size, p.max_pages = pc.max_pages, p.num_pages = pc.num_pages;
     hipError_t e = sk::launch_fwd_f32(p, false, s);
     if (e != hipSuccess) return hip_fail(e, "sk_decode launch");
     return SK_OK;
@@ -326,6 +336,8 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
   p.scale_log2 = p.scale * 1.4426950408889634f;
   p.q_sign = sm_scale < 0.f ? 0x80008000u : 0u;
   p.seqlens = seqlens;
+  p.block_table = pc.block_table;
+  p.page_size = pc.page_size, p.max_pages = pc.max_pages, p.num_pages = pc.num_pages;
   if (num_splits > 1) {
     p.part_o = (float*)workspace;
     p.part_lse = p.part_o + (size_t)B * Hq * num_splits * p.dpad;
@@ -346,18 +358,24 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
               const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
               const int64_t* o_strides, float sm_scale, void* stream) {
   return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
-                     q_strides, k_strides, v_strides, o_strides, nullptr, sm_scale, stream);
+                     q_strides, k_strides, v_strides, o_strides, nullptr, PagedCache{}, sm_scale,
+                     stream);
 }
 
-int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_cache, void* v_cache,
-                       const int64_t* slots, int B, int Hkv, int T, int S_cache, int D,
-                       const int64_t* k_strides, const int64_t* v_strides,
-                       const int64_t* kc_strides, const int64_t* vc_strides, void* stream) {
-  g_err[0] = 0;
+}  // extern "C"
+
+// sk_kv_cache_update (page_size 0: S_cache rows per batch row) and
+// sk_kv_cache_update_paged (S_cache = num_pages * page_size pool slots).
+static int cache_update_impl(int dtype, const void* k, const void* v, void* k_cache,
+                             void* v_cache, const int64_t* slots, int B, int Hkv, int T,
+                             int64_t S_cache, int page_size, int D, const int64_t* k_strides,
+                             const int64_t* v_strides, const int64_t* kc_strides,
+                             const int64_t* vc_strides, void* stream) {
   if (dtype != SK_F32 && dtype != SK_F16 && dtype != SK_BF16)
     return fail(SK_EUNSUPPORTED, "unsupported dtype code %d", dtype);
   if (B < 0 || Hkv <= 0 || T < 0 || S_cache < 0 || D <= 0)
-    return fail(SK_EINVAL, "invalid sizes B=%d Hkv=%d T=%d S_cache=%d D=%d", B, Hkv, T, S_cache, D);
+    return fail(SK_EINVAL, "invalid sizes B=%d Hkv=%d T=%d S_cache=%lld D=%d", B, Hkv, T,
+                (long long)S_cache, D);
   const int64_t* sts[4] = {k_strides, v_strides, kc_strides, vc_strides};
   const char* names[4] = {"k", "v", "k_cache", "v_cache"};
   for (int i = 0; i < 4; ++i) {
@@ -379,11 +397,36 @@ int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_cache, v
   p.kc_sb = kc_strides[0], p.kc_sh = kc_strides[1], p.kc_ss = kc_strides[2];
   p.vc_sb = vc_strides[0], p.vc_sh = vc_strides[1], p.vc_ss = vc_strides[2];
   p.B = B, p.Hkv = Hkv, p.T = T, p.S = S_cache;
+  p.page_size = page_size;
   p.esize = elem_bytes(dtype);
   p.row_bytes = D * p.esize;
   hipError_t e = sk::launch_kv_cache_update(p, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sk_kv_cache_update launch");
   return SK_OK;
+}
+
+extern "C" {
+
+int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_cache, void* v_cache,
+                       const int64_t* slots, int B, int Hkv, int T, int S_cache, int D,
+                       const int64_t* k_strides, const int64_t* v_strides,
+                       const int64_t* kc_strides, const int64_t* vc_strides, void* stream) {
+  g_err[0] = 0;
+  return cache_update_impl(dtype, k, v, k_cache, v_cache, slots, B, Hkv, T, S_cache, 0, D,
+                           k_strides, v_strides, kc_strides, vc_strides, stream);
+}
+
+int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, void* k_pool,
+                             void* v_pool, const int64_t* slot_mapping, int B, int Hkv, int T,
+                             int num_pages, int page_size, int D, const int64_t* k_strides,
+                             const int64_t* v_strides, const int64_t* kp_strides,
+                             const int64_t* vp_strides, void* stream) {
+  g_err[0] = 0;
+  if (page_size <= 0 || num_pages < 0)
+    return fail(SK_EINVAL, "invalid page_size=%d num_pages=%d", page_size, num_pages);
+  return cache_update_impl(dtype, k, v, k_pool, v_pool, slot_mapping, B, Hkv, T,
+                           (int64_t)num_pages * page_size, page_size, D, k_strides, v_strides,
+                           kp_strides, vp_strides, stream);
 }
 
 int sk_decode_varlen(int dtype, const void* q, const void* k, const void* v, void* o,
@@ -394,7 +437,34 @@ int sk_decode_varlen(int dtype, const void* q, const void* k, const void* v, voi
   g_err[0] = 0;
   if (B > 0 && !cache_seqlens) return fail(SK_EINVAL, "cache_seqlens is null");
   return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
-                     q_strides, k_strides, v_strides, o_strides, cache_seqlens, sm_scale, stream);
+                     q_strides, k_strides, v_strides, o_strides, cache_seqlens, PagedCache{},
+                     sm_scale, stream);
+}
+
+int sk_decode_paged(int dtype, const void* q, const void* k_pool, const void* v_pool, void* o,
+                    void* workspace, size_t workspace_bytes, int num_splits, int B, int Hq,
+                    int Hkv, int num_pages, int page_size, int max_pages, int D,
+                    const int64_t* q_strides, const int64_t* kp_strides,
+                    const int64_t* vp_strides, const int64_t* o_strides,
+                    const int32_t* block_table, const int32_t* cache_seqlens, float sm_scale,
+                    void* stream) {
+  g_err[0] = 0;
+  if (page_size <= 0 || page_size % 32 != 0)
+    return fail(SK_EINVAL, "page_size=%d must be a positive multiple of 32", page_size);
+  if (num_pages < 0 || max_pages < 0)
+    return fail(SK_EINVAL, "invalid num_pages=%d max_pages=%d", num_pages, max_pages);
+  if ((int64_t)max_pages * page_size > 0x7fffffffLL)
+    return fail(SK_EINVAL, "max_pages * page_size overflows int");
+  if (B > 0 && max_pages > 0 && (!block_table || !cache_seqlens))
+    return fail(SK_EINVAL, "block_table and cache_seqlens are required");
+  PagedCache pc;
+  pc.block_table = block_table;
+  pc.page_size = page_size, pc.max_pages = max_pages, pc.num_pages = num_pages;
+  const int sk = max_pages * page_size;
+  if (sk > 0 && num_pages == 0) return fail(SK_EINVAL, "empty page pool");
+  return decode_impl(dtype, q, k_pool, v_pool, o, workspace, workspace_bytes, num_splits, B, Hq,
+                     Hkv, sk, D, q_strides, kp_strides, vp_strides, o_strides, cache_seqlens, pc,
+                     sm_scale, stream);
 }
 
 }  // extern "C"

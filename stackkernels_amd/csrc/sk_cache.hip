@@ -51,11 +51,14 @@ __global__ void __launch_bounds__(256) kv_cache_update_kernel(CacheParams p) {
   const int b = (int)(bh / p.Hkv);
   const int64_t slot = p.slots[(int64_t)b * p.T + t];
   if (slot < 0 || slot >= p.S) return;
+  // Contiguous: row slot of batch row b's cache.  Paged: in-page row of a page.
+  const int64_t unit = p.page_size > 0 ? slot / p.page_size : b;
+  const int64_t row = p.page_size > 0 ? slot % p.page_size : slot;
   const int64_t e = p.esize;
   const char* ks = (const char*)p.k + (b * p.k_sb + h * p.k_sh + t * p.k_ss) * e + (int64_t)c * UNIT;
   const char* vs = (const char*)p.v + (b * p.v_sb + h * p.v_sh + t * p.v_ss) * e + (int64_t)c * UNIT;
-  char* kd = (char*)p.kc + (b * p.kc_sb + h * p.kc_sh + slot * p.kc_ss) * e + (int64_t)c * UNIT;
-  char* vd = (char*)p.vc + (b * p.vc_sb + h * p.vc_sh + slot * p.vc_ss) * e + (int64_t)c * UNIT;
+  char* kd = (char*)p.kc + (unit * p.kc_sb + h * p.kc_sh + row * p.kc_ss) * e + (int64_t)c * UNIT;
+  char* vd = (char*)p.vc + (unit * p.vc_sb + h * p.vc_sh + row * p.vc_ss) * e + (int64_t)c * UNIT;
   const U kx = *reinterpret_cast<const U*>(ks);
   const U vx = *reinterpret_cast<const U*>(vs);
   *reinterpret_cast<U*>(kd) = kx;

@@ -171,6 +171,13 @@ __device__ __forceinline__ i32x4 make_rsrc_words(const void* base, int num_bytes
   return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), num_bytes, 0x00020000};
 }
 
+// The four words with each read from the first active lane: for values that
+// are wave-uniform but that the compiler cannot prove so.
+__device__ __forceinline__ i32x4 uniform_words(i32x4 r) {
+  return i32x4{__builtin_amdgcn_readfirstlane(r[0]), __builtin_amdgcn_readfirstlane(r[1]),
+               __builtin_amdgcn_readfirstlane(r[2]), __builtin_amdgcn_readfirstlane(r[3])};
+}
+
 // LDS byte address of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;

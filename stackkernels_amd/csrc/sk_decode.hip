@@ -33,7 +33,31 @@ struct DecTile {
   static constexpr int kChunks = kBN * kChunksPerRow;
 };
 
-template <class T, int DP, int NWH>
+// Rows of the 32-key tile that starts at key n0 of batch row b (a tile never
+// straddles a page): contiguous caches, or the tile's page of a paged cache.
+// ok is false when the page index lies outside the pool; such a tile reads as
+// zeros and its keys are masked.
+struct TileRows {
+  const uint16_t* k;
+  const uint16_t* v;
+  bool ok;
+};
+template <bool PAGED>
+__device__ __forceinline__ TileRows tile_rows(const DecParams& p, const uint16_t* kbase,
+                                              const uint16_t* vbase, int b, int hkv, int n0) {
+  if (!PAGED) return {kbase + (int64_t)n0 * p.k_ss, vbase + (int64_t)n0 * p.v_ss, true};
+  // (readfirstlane: the table entry is the same for every lane, and the
+  // DMA resource built from it must sit in scalar registers.)
+  const int page =
+      __builtin_amdgcn_readfirstlane(p.block_table[(int64_t)b * p.max_pages + n0 / p.page_size]);
+  const bool ok = page >= 0 && page < p.num_pages;
+  const int64_t pg = ok ? page : 0;
+  const int64_t off = n0 % p.page_size;
+  return {(const uint16_t*)p.k + pg * p.k_sb + (int64_t)hkv * p.k_sh + off * p.k_ss,
+          (const uint16_t*)p.v + pg * p.v_sb + (int64_t)hkv * p.v_sh + off * p.v_ss, ok};
+}
+
+template <class T, int DP, int NWH, bool PAGED>
 __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   using Tile = DecTile<DP>;
   constexpr int BN = Tile::kBN;
@@ -59,7 +83,8 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   // Keys this row sees: all S_k, or its cache length.  With per-row lengths
   // the row's keys are spread over all its splits (32-key multiples), so a
   // short row does not leave most of its workgroups empty.
-  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
+  const int sk_b =
+      p.seqlens ? min(max(__builtin_amdgcn_readfirstlane(p.seqlens[b]), 0), p.Sk) : p.Sk;
   const int kps = p.seqlens ? max(32, ((sk_b + p.num_splits - 1) / p.num_splits + 31) / 32 * 32)
                             : p.keys_per_split;
   const int k_lo = split * kps;
@@ -89,6 +114,7 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   u32x4 kreg[LOADS], vreg[LOADS];
   auto load_tile = [&](int t) {
     const int n0 = k_lo + t * BN;
+    const TileRows tr = tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int c = tid + i * NT;
@@ -96,9 +122,9 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
       const int d = (c % Tile::kChunksPerRow) * 8;
       const int n = n0 + r;
       u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
-      if (n < k_hi && d < p.D && (!kRagged || c < Tile::kChunks)) {
-        kx = ldg_b128(kbase + (int64_t)n * p.k_ss + d);
-        vx = ldg_b128(vbase + (int64_t)n * p.v_ss + d);
+      if (tr.ok && n < k_hi && d < p.D && (!kRagged || c < Tile::kChunks)) {
+        kx = ldg_b128(tr.k + (int64_t)r * p.k_ss + d);
+        vx = ldg_b128(tr.v + (int64_t)r * p.v_ss + d);
       }
       kreg[i] = kx;
       vreg[i] = vx;
@@ -142,12 +168,13 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
         sacc[kb] = mfma16<T>(a, qreg[s], sacc[kb]);
       }
     }
-    if (n0 + BN > k_hi) {
+    const bool tile_ok = !PAGED || tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0).ok;
+    if (!tile_ok || n0 + BN > k_hi) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (n0 + 16 * kb + 4 * g + r >= k_hi) sacc[kb][r] = kNegInf;
+          if (!tile_ok || n0 + 16 * kb + 4 * g + r >= k_hi) sacc[kb][r] = kNegInf;
     }
     float mt = fmaxf(fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3])),
                      fmaxf(fmaxf(sacc[1][0], sacc[1][1]), fmaxf(sacc[1][2], sacc[1][3])));
@@ -222,7 +249,7 @@ __device__ __forceinline__ int dec_swz_v(int r) {
   return DP == 64 ? 2 * ((r >> 1) & 3) : 2 * (r & 7);
 }
 
-template <class T, int DP, int NWH, int STAGES>
+template <class T, int DP, int NWH, int STAGES, bool PAGED>
 __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
   constexpr int BN = 32;                  // keys per tile
   constexpr int CPR = DP / 8;             // 16-byte chunks per row
@@ -250,7 +277,8 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
   // Keys this row sees: all S_k, or its cache length.  With per-row lengths
   // the row's keys are spread over all its splits (32-key multiples), so a
   // short row does not leave most of its workgroups empty.
-  const int sk_b = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
+  const int sk_b =
+      p.seqlens ? min(max(__builtin_amdgcn_readfirstlane(p.seqlens[b]), 0), p.Sk) : p.Sk;
   const int kps = p.seqlens ? max(32, ((sk_b + p.num_splits - 1) / p.num_splits + 31) / 32 * 32)
                             : p.keys_per_split;
   const int k_lo = split * kps;
@@ -291,9 +319,13 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
   }
   auto issue_tile = [&](int t) {
     const int n0 = k_lo + t * BN;
-    const int rows = min(BN, k_hi - n0);
-    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.k_ss, tile_bytes(rows, p.k_ss, p.D));
-    const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.v_ss, tile_bytes(rows, p.v_ss, p.D));
+    const TileRows tr = tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0);
+    const int rows = tr.ok ? min(BN, k_hi - n0) : 0;
+    // (The paged row pointers come from a table load; readfirstlane states
+    // what is true -- they are wave-uniform -- so the DMA resources stay
+    // scalar.)
+    const i32x4 kr = uniform_words(make_rsrc_words(tr.k, tile_bytes(rows, p.k_ss, p.D)));
+    const i32x4 vr = uniform_words(make_rsrc_words(tr.v, tile_bytes(rows, p.v_ss, p.D)));
     const uint32_t st = lds_addr(smem) + (t % STAGES) * STAGEB;
 #pragma unroll
     for (int j = 0; j < LW; ++j) {
@@ -347,12 +379,13 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
         sacc[kb] = mfma16<T>(a, qreg[s], sacc[kb]);
       }
     }
-    if (n0 + BN > k_hi) {
+    const bool tile_ok = !PAGED || tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0).ok;
+    if (!tile_ok || n0 + BN > k_hi) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (n0 + 16 * kb + 4 * g + r >= k_hi) sacc[kb][r] = kNegInf;
+          if (!tile_ok || n0 + 16 * kb + 4 * g + r >= k_hi) sacc[kb][r] = kNegInf;
     }
     float mt = fmaxf(fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3])),
                      fmaxf(fmaxf(sacc[1][0], sacc[1][1]), fmaxf(sacc[1][2], sacc[1][3])));
@@ -485,43 +518,48 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecParams p) {
 // 128 KB in flight); 32- and 64-head groups use the 2- and 4-wave LDS-ring
 // kernel with 5 stages of 16 KB (2 workgroups per CU at D = 128, so 128 KB
 // of loads in flight per CU: HBM streaming is latency-bound below that).
-template <class T, int DP>
+template <class T, int DP, bool PAGED>
 static hipError_t launch_decode_dp(const DecParams& p, hipStream_t s) {
   const dim3 grid((unsigned)p.num_splits, (unsigned)(p.B * p.Hkv));
   constexpr bool kRing = DP == 64 || DP == 128 || DP == 256;
   constexpr int kStages = DP == 256 ? 2 : 5;
   if (p.group <= 16)
-    hipLaunchKernelGGL((decode_split_kernel<T, DP, 1>), grid, dim3(64), 0, s, p);
+    hipLaunchKernelGGL((decode_split_kernel<T, DP, 1, PAGED>), grid, dim3(64), 0, s, p);
   else if (p.group <= 32) {
     if constexpr (kRing)
-      hipLaunchKernelGGL((decode_ring_kernel<T, DP, 2, kStages>), grid, dim3(128), 0, s, p);
+      hipLaunchKernelGGL((decode_ring_kernel<T, DP, 2, kStages, PAGED>), grid, dim3(128), 0, s, p);
     else
-      hipLaunchKernelGGL((decode_split_kernel<T, DP, 2>), grid, dim3(128), 0, s, p);
+      hipLaunchKernelGGL((decode_split_kernel<T, DP, 2, PAGED>), grid, dim3(128), 0, s, p);
   } else if (p.group <= 64) {
     if constexpr (kRing)
-      hipLaunchKernelGGL((decode_ring_kernel<T, DP, 4, kStages>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((decode_ring_kernel<T, DP, 4, kStages, PAGED>), grid, dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((decode_split_kernel<T, DP, 4>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((decode_split_kernel<T, DP, 4, PAGED>), grid, dim3(256), 0, s, p);
   } else {
     return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-template <class T>
-static hipError_t launch_decode_t(const DecParams& p, hipStream_t s) {
+template <class T, bool PAGED>
+static hipError_t launch_decode_tp(const DecParams& p, hipStream_t s) {
   switch (padded_head_dim(p.D)) {
     case 64:
-      return launch_decode_dp<T, 64>(p, s);
+      return launch_decode_dp<T, 64, PAGED>(p, s);
     case 96:
-      return launch_decode_dp<T, 96>(p, s);
+      return launch_decode_dp<T, 96, PAGED>(p, s);
     case 128:
-      return launch_decode_dp<T, 128>(p, s);
+      return launch_decode_dp<T, 128, PAGED>(p, s);
     case 256:
-      return launch_decode_dp<T, 256>(p, s);
+      return launch_decode_dp<T, 256, PAGED>(p, s);
     default:
       return hipErrorInvalidValue;
   }
+}
+
+template <class T>
+static hipError_t launch_decode_t(const DecParams& p, hipStream_t s) {
+  return p.block_table ? launch_decode_tp<T, true>(p, s) : launch_decode_tp<T, false>(p, s);
 }
 
 hipError_t launch_decode_mfma(int dtype, const DecParams& p, hipStream_t s) {

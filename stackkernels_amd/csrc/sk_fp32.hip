@@ -27,6 +27,7 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
   constexpr int DC = DP / 4;  // head-dim slice per lane
   __shared__ float ks[kF32Tile][DP];
   __shared__ float vs[kF32Tile][DP];
+  __shared__ int kok[kF32Tile];  // paged decode: the key's page lies in the pool
 
   const int tid = threadIdx.x;
   const int part = tid & 3;
@@ -59,13 +60,33 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
   if (CAUSAL) n_end = min(sk_b, m0 + kF32Rows + diag);
   const int lim = CAUSAL ? min(sk_b - 1, row + diag) : sk_b - 1;
 
+  // Key n's K and V rows: contiguous, or in-page row n % page_size of page
+  // block_table[b][n / page_size] of a paged pool (decode only).
+  auto key_rows = [&](int n, const float*& kr, const float*& vr) {
+    if (!p.block_table) {
+      kr = kbase + (int64_t)n * p.k_ss;
+      vr = vbase + (int64_t)n * p.v_ss;
+      return true;
+    }
+    const int page = p.block_table[(int64_t)b * p.max_pages + n / p.page_size];
+    const bool ok = page >= 0 && page < p.num_pages;
+    const int64_t pg = ok ? page : 0, off = n % p.page_size;
+    kr = (const float*)p.k + pg * p.k_sb + (int64_t)hkv * p.k_sh + off * p.k_ss;
+    vr = (const float*)p.v + pg * p.v_sb + (int64_t)hkv * p.v_sh + off * p.v_ss;
+    return ok;
+  };
+
   for (int n0 = 0; n0 < n_end; n0 += kF32Tile) {
     __syncthreads();
     for (int e = tid; e < kF32Tile * DP; e += 256) {
       const int r = e / DP, d = e % DP, n = n0 + r;
-      const bool ok = n < sk_b && d < p.D;
-      ks[r][d] = ok ? kbase[(int64_t)n * p.k_ss + d] : 0.f;
-      vs[r][d] = ok ? vbase[(int64_t)n * p.v_ss + d] : 0.f;
+      const float* kr = nullptr;
+      const float* vr = nullptr;
+      const bool page_ok = n < sk_b && key_rows(n, kr, vr);
+      const bool ok = page_ok && d < p.D;
+      ks[r][d] = ok ? kr[d] : 0.f;
+      vs[r][d] = ok ? vr[d] : 0.f;
+      if (d == 0) kok[r] = page_ok;
     }
     __syncthreads();
     float s[kF32Tile];
@@ -76,7 +97,7 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
 #pragma unroll
       for (int i = 0; i < DC; ++i) x = fmaf(q[i], ks[j][part * DC + i], x);
       x = quad_sum(x) * p.scale;
-      if (n0 + j > lim) x = kNegInf;
+      if (n0 + j > lim || !kok[j]) x = kNegInf;
       s[j] = x;
       mt = fmaxf(mt, x);
     }

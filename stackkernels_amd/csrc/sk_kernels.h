@@ -29,6 +29,9 @@ struct FwdParams {
   // Decode only (fp32 path, non-causal): null, or per-batch-row key counts;
   // row b sees keys [0, clamp(seqlens[b], 0, Sk)).
   const int* seqlens;
+  // Decode only: null, or a paged cache (see DecParams).
+  const int* block_table;
+  int page_size, max_pages, num_pages;
 };
 
 // Split-KV decode (Sq == 1).
@@ -49,6 +52,13 @@ struct DecParams {
   uint32_t q_sign;
   // Null, or per-batch-row key counts: row b sees keys [0, clamp(seqlens[b], 0, Sk)).
   const int* seqlens;
+  // Null (k/v are (B, Hkv, Sk, D)), or a paged cache: k/v are pools of
+  // num_pages pages (k_sb / v_sb is the page stride) of page_size keys, and
+  // key n of row b is in-page row n % page_size of page
+  // block_table[b * max_pages + n / page_size] (Sk = max_pages * page_size).
+  // page_size is a multiple of 32; a page index outside the pool masks its keys.
+  const int* block_table;
+  int page_size, max_pages, num_pages;
 };
 
 // Backward attention; every tensor contiguous BHSD.
@@ -83,11 +93,16 @@ struct CacheParams {
   void* kc;
   void* vc;
   const int64_t* slots;  // [B*T]; a slot outside [0, S) skips that token
+  // 0: the caches are (B, Hkv, S, D) and a slot is a row of batch row b's cache.
+  // > 0: the caches are pools of S / page_size pages (kc_sb / vc_sb is the page
+  // stride) and slot s is in-page row s % page_size of page s / page_size.
+  int page_size;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
   int64_t kc_sb, kc_sh, kc_ss;
   int64_t vc_sb, vc_sh, vc_ss;
-  int B, Hkv, T, S;
+  int B, Hkv, T;
+  int64_t S;      // slots: rows per batch row's cache, or num_pages * page_size
   int esize;      // bytes per element
   int row_bytes;  // D * esize
 };

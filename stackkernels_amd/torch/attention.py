@@ -18,6 +18,7 @@ import torch
 import torch.nn as nn
 
 from stackkernels_amd._core.attention.decode import flash_decode as core_flash_decode
+from stackkernels_amd._core.attention.decode import flash_decode_paged as core_flash_decode_paged
 from stackkernels_amd._core.attention.flash_bwd import flash_attn_bwd
 from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
 from stackkernels_amd._reference.torch.attention import (
@@ -106,6 +107,7 @@ def flash_decode(
     v: torch.Tensor,
     sm_scale: float | None = None,
     cache_seqlens: torch.Tensor | None = None,
+    block_table: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Split-KV decode for one query token (S_q = 1) over the whole cache.
 
@@ -116,16 +118,51 @@ def flash_decode(
             ``min(cache_seqlens[b], S_k)`` keys of its cache; a row with no
             key gives zeros.  Not in the reference, which decodes every row
             over all S_k keys (``None``, the default, does the same).
+        block_table: optional integer (B, max_pages) for a paged cache: then
+            k, v are page pools (num_pages, H_kv, page_size, D), page_size a
+            multiple of 32, key j of row b is row ``j % page_size`` of page
+            ``block_table[b, j // page_size]``, and cache_seqlens is required.
 
     Returns:
         (B, H_q, 1, D) in q's dtype.
     """
-    if should_use_hip(q):
+    if block_table is not None:
+        if cache_seqlens is None:
+            raise ValueError("a paged decode (block_table) needs cache_seqlens")
+        if should_use_hip(q):
+            return core_flash_decode_paged(q, k, v, block_table, cache_seqlens, sm_scale=sm_scale)
+        return _decode_paged_reference(q, k, v, sm_scale, cache_seqlens, block_table)
+    elif should_use_hip(q):
         return core_flash_decode(q, k, v, sm_scale=sm_scale, cache_seqlens=cache_seqlens)
     if cache_seqlens is None:
         out, _ = attention_reference(q, k, v, is_causal=False, sm_scale=sm_scale)
         return out
     return _decode_varlen_reference(q, k, v, sm_scale, cache_seqlens)
+
+
+def _decode_paged_reference(q, k_pool, v_pool, sm_scale, cache_seqlens, block_table):
+    """CPU path of the paged decode: each row's visible keys gathered from its
+    pages (keys past the row's length, or in a page outside the pool, are
+    left out), then the reference attention; zeros for a row with no key."""
+    table = torch.as_tensor(block_table).to("cpu", torch.int64)
+    lens = torch.as_tensor(cache_seqlens).to("cpu", torch.int64)
+    num_pages, _, page_size, _ = k_pool.shape
+    b, max_pages = table.shape
+    if lens.dim() != 1 or lens.shape[0] != b or q.shape[0] != b:
+        raise ValueError(f"cache_seqlens must have shape ({b},), got {tuple(lens.shape)}")
+    out = torch.zeros_like(q)
+    for i in range(b):
+        n = int(min(max(int(lens[i]), 0), max_pages * page_size))
+        keys = [j for j in range(n) if 0 <= int(table[i, j // page_size]) < num_pages]
+        if not keys:
+            continue
+        idx = torch.tensor(keys)
+        pg = table[i, idx // page_size].to(k_pool.device)
+        off = (idx % page_size).to(k_pool.device)
+        k = k_pool[pg, :, off].permute(1, 0, 2).unsqueeze(0)  # (1, H_kv, n_keys, D)
+        v = v_pool[pg, :, off].permute(1, 0, 2).unsqueeze(0)
+        out[i:i + 1], _ = attention_reference(q[i:i + 1], k, v, is_causal=False, sm_scale=sm_scale)
+    return out
 
 
 def _decode_varlen_reference(q, k, v, sm_scale, cache_seqlens):

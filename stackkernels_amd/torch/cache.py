@@ -21,6 +21,7 @@ def kv_cache_update(
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
     slot_indices: torch.Tensor,
+    paged: bool = False,
 ) -> None:
     """Insert new key/value rows into the caches in place.
 
@@ -33,13 +34,25 @@ def kv_cache_update(
             updated in place.
         slot_indices: integer (B, T) cache positions.  A position outside
             ``[0, S_cache)`` skips its token (pad ragged batches with -1).  Positions
-            must be distinct within a batch row.
+            must be distinct within a batch row (within the pool when paged).
+        paged: the caches are page pools (num_pages, H_kv, page_size, D) shared by
+            all rows, and a position s is row ``s % page_size`` of page
+            ``s // page_size`` (S_cache = num_pages * page_size).
     """
     if should_use_hip(k_cache):
-        _core_kv_cache_update(k, v, k_cache, v_cache, slot_indices)
+        _core_kv_cache_update(k, v, k_cache, v_cache, slot_indices, paged)
         return
-    b, _, t, s, _ = validate_cache_update(k, v, k_cache, v_cache, slot_indices)
+    b, _, t, s, _ = validate_cache_update(k, v, k_cache, v_cache, slot_indices, paged)
     slots = slot_indices.to("cpu", torch.int64)
+    if paged:
+        ps = k_cache.shape[2]
+        for i in range(b):
+            for j in range(t):
+                pos = int(slots[i, j])
+                if 0 <= pos < s:
+                    k_cache[pos // ps, :, pos % ps] = k[i, :, j].to(k_cache.dtype)
+                    v_cache[pos // ps, :, pos % ps] = v[i, :, j].to(v_cache.dtype)
+        return
     for i in range(b):
         pos = slots[i]
         keep = (pos >= 0) & (pos < s)

@@ -31,7 +31,8 @@ def test_header_declares_expected_api():
     names = set(header_functions())
     assert {"sk_abi_version", "sk_last_error", "sk_attn_fwd", "sk_attn_bwd",
             "sk_attn_bwd_workspace", "sk_decode_plan", "sk_decode", "sk_decode_workspace",
-            "sk_decode_varlen", "sk_kv_cache_update"} <= names
+            "sk_decode_varlen", "sk_kv_cache_update", "sk_decode_paged",
+            "sk_kv_cache_update_paged"} <= names
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -132,3 +133,30 @@ def test_varlen_and_cache_argument_errors(lib):
     assert upd(slots=None) == _lib.SK_EINVAL and "slot_indices" in _lib.last_error()
     assert upd(T=0) == _lib.SK_OK  # nothing to write: no launch
     assert upd(B=0, k=None) == _lib.SK_OK
+
+
+def test_paged_argument_errors(lib):
+    from stackkernels_amd._core.attention import _lib
+
+    st = _st(1024, 512, 64)
+
+    def dec(page_size=64, num_pages=4, max_pages=2, table=16, lens=16, B=1):
+        return lib.sk_decode_paged(2, 16, 16, 16, 16, 16, 1 << 20, 1, B, 4, 2, num_pages,
+                                   page_size, max_pages, 64, st, st, st, st, table, lens,
+                                   0.125, None)
+
+    assert dec(page_size=48) == _lib.SK_EINVAL and "multiple of 32" in _lib.last_error()
+    assert dec(page_size=0) == _lib.SK_EINVAL
+    assert dec(max_pages=-1) == _lib.SK_EINVAL
+    assert dec(table=None) == _lib.SK_EINVAL and "block_table" in _lib.last_error()
+    assert dec(lens=None) == _lib.SK_EINVAL
+    assert dec(num_pages=0) == _lib.SK_EINVAL and "pool" in _lib.last_error()
+    assert dec(B=0) == _lib.SK_OK
+
+    def upd(page_size=32, num_pages=4, T=3):
+        return lib.sk_kv_cache_update_paged(2, 16, 16, 16, 16, 16, 1, 2, T, num_pages, page_size,
+                                            64, st, st, st, st, None)
+
+    assert upd(page_size=0) == _lib.SK_EINVAL
+    assert upd(num_pages=-1) == _lib.SK_EINVAL
+    assert upd(T=0) == _lib.SK_OK

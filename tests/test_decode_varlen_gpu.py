@@ -223,3 +223,107 @@ def test_config4_cache_append_one_token(device):
         ref = orc.decode_varlen(np64(q[r:r + 1]), np64(kc[r:r + 1]), np64(vc[r:r + 1]),
                                 (lens[r:r + 1] + 1).numpy())
         assert_close_maxabs(out[r:r + 1], ref, TOL[dt], f"O row {r}")
+
+
+# ---- paged pools ----------------------------------------------------------------
+
+def _pool(pages, hkv, ps, d, dtype, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    kp = torch.randn(pages, hkv, ps, d, generator=g).to(dtype).to(device)
+    vp = torch.randn(pages, hkv, ps, d, generator=g).to(dtype).to(device)
+    return kp, vp
+
+
+def _table(b, pages, max_pages, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.stack([torch.randperm(pages, generator=g)[:max_pages] for _ in range(b)]).to(torch.int32)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("group", [1, 4, 16, 32, 64])
+@pytest.mark.parametrize("ps", [32, 64, 256])
+def test_decode_paged(device, dtype, group, ps):
+    b, hkv, d, max_pages = 5, 2, 128, 6
+    pages = b * max_pages + 3
+    kp, vp = _pool(pages, hkv, ps, d, dtype, seed=ps + group, device=device)
+    q = torch.randn(b, hkv * group, 1, d, generator=torch.Generator().manual_seed(group)).to(dtype).to(device)
+    table = _table(b, pages, max_pages, seed=ps)
+    table[2, 1] = -1          # outside the pool: those keys are masked
+    table[3, 0] = pages + 4
+    lens = torch.tensor([0, max_pages * ps, max_pages * ps - 5, 3 * ps + 7, max_pages * ps + 50])
+    out = flash_decode(q, kp, vp, cache_seqlens=lens.to(device), block_table=table.to(device))
+    assert native_loaded()
+    ref = orc.decode_paged(np64(q), np64(kp), np64(vp), table.numpy(), lens.numpy())
+    assert out.shape == q.shape and out.dtype == dtype
+    assert_close_maxabs(out, ref, TOL[dtype], "O")
+    assert torch.all(out[0] == 0)
+
+
+def test_decode_paged_bshd_pool_and_split_counts(device):
+    """A pool allocated (pages, page_size, H_kv, D) and viewed as (pages, H_kv, page_size, D)."""
+    dt = torch.bfloat16
+    b, hkv, ps, d, max_pages = 4, 4, 64, 128, 8
+    pages = 40
+    g = torch.Generator().manual_seed(9)
+    kp = torch.randn(pages, ps, hkv, d, generator=g).to(dt).to(device).transpose(1, 2)
+    vp = torch.randn(pages, ps, hkv, d, generator=g).to(dt).to(device).transpose(1, 2)
+    q = torch.randn(b, 16, 1, d, generator=g).to(dt).to(device)
+    table = _table(b, pages, max_pages, seed=10)
+    lens = torch.tensor([512, 100, 1, 300], dtype=torch.int32)
+    ref = orc.decode_paged(np64(q), np64(kp), np64(vp), table.numpy(), lens.numpy())
+    from stackkernels_amd._core.attention.decode import flash_decode_paged
+
+    for ns in (None, 1, 3, 16):
+        out = flash_decode_paged(q, kp, vp, table.to(device), lens.to(device), num_splits=ns)
+        assert_close_maxabs(out, ref, TOL[dt], f"O splits={ns}")
+
+
+def test_decode_paged_errors(device):
+    dt = torch.float16
+    kp, vp = _pool(4, 2, 48, 64, dt, seed=1, device=device)  # page_size 48: not a multiple of 32
+    q = torch.zeros(1, 2, 1, 64, dtype=dt, device=device)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        flash_decode(q, kp, vp, cache_seqlens=torch.tensor([10]), block_table=torch.tensor([[0]]))
+    kp, vp = _pool(4, 2, 64, 64, dt, seed=1, device=device)
+    with pytest.raises(ValueError, match="cache_seqlens"):
+        flash_decode(q, kp, vp, block_table=torch.tensor([[0]], device=device))
+
+
+def test_config4_paged_pool(device):
+    """The C4 decode shape (B=64, Hq=32, Hkv=8, D=128, bf16) over a paged pool of 64-key
+    pages (512 pages per row, shuffled), random lengths; four rows against the oracle."""
+    dt = torch.bfloat16
+    b, hkv, ps, d, max_pages = 64, 8, 64, 128, 512
+    pages = b * max_pages
+    gd = torch.Generator(device=device).manual_seed(3)
+    kp = torch.randn(pages, hkv, ps, d, generator=gd, device=device).to(dt)
+    vp = torch.randn(pages, hkv, ps, d, generator=gd, device=device).to(dt)
+    q = torch.randn(b, 32, 1, d, generator=gd, device=device).to(dt)
+    table = torch.randperm(pages, generator=torch.Generator().manual_seed(4)).view(b, max_pages).to(torch.int32)
+    lens = _lens(b, max_pages * ps, seed=5)
+    out = flash_decode(q, kp, vp, cache_seqlens=lens.to(device), block_table=table.to(device))
+    torch.cuda.synchronize()
+    for r in (0, 1, 2, 33):
+        pages_r = table[r].long().to(device)
+        ref = orc.decode_paged(np64(q[r:r + 1]), np64(kp[pages_r]), np64(vp[pages_r]),
+                               np.arange(max_pages)[None], lens[r:r + 1].numpy())
+        assert_close_maxabs(out[r:r + 1], ref, TOL[dt], f"O row {r}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("d", [4, 64, 128])
+def test_kv_cache_update_paged_exact(device, dtype, d):
+    b, h, t, pages, ps = 3, 2, 5, 7, 32
+    g = torch.Generator().manual_seed(d + 1)
+    k = torch.randn(b, h, t, d, generator=g).to(dtype)
+    v = torch.randn(b, h, t, d, generator=g).to(dtype)
+    kp = torch.randn(pages, h, ps, d, generator=g).to(dtype)
+    vp = torch.randn(pages, h, ps, d, generator=g).to(dtype)
+    sl = torch.randperm(pages * ps, generator=g)[:b * t].view(b, t)
+    sl[0, 0] = -1
+    sl[2, 4] = pages * ps + 3
+    ek, ev = orc.kv_cache_update_paged(_bits(k).numpy(), _bits(v).numpy(), _bits(kp).numpy(),
+                                       _bits(vp).numpy(), sl.numpy())
+    kd, vd, kpd, vpd = (x.to(device) for x in (k, v, kp, vp))
+    kv_cache_update(kd, vd, kpd, vpd, sl.to(device), paged=True)
+    assert np.array_equal(_bits(kpd).numpy(), ek) and np.array_equal(_bits(vpd).numpy(), ev)

@@ -267,3 +267,58 @@ def test_kv_cache_update_matches_loops():
     assert np.array_equal(nk, ek) and np.array_equal(nv, ev)
     # untouched rows keep their contents; the inputs are not modified
     assert np.array_equal(nk[0, :, 1], kc[0, :, 1]) and not np.array_equal(nk, kc)
+
+
+# ---- paged pools ---------------------------------------------------------------
+
+def _pool_inputs(seed, b=3, hq=4, hkv=2, pages=6, ps=4, d=8, mp=3):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((b, hq, 1, d))
+    kp, vp = rng.standard_normal((pages, hkv, ps, d)), rng.standard_normal((pages, hkv, ps, d))
+    table = np.stack([rng.permutation(pages)[:mp] for _ in range(b)])
+    return q, kp, vp, table
+
+
+def test_decode_paged_equals_varlen_on_assembled_caches():
+    q, kp, vp, table = _pool_inputs(5)
+    lens = np.array([5, 12, 0])
+    ps = kp.shape[2]
+    # assemble each row's cache page by page with explicit loops
+    k = np.zeros((3, 2, 12, 8))
+    v = np.zeros((3, 2, 12, 8))
+    for b in range(3):
+        for j in range(12):
+            page = table[b, j // ps]
+            k[b, :, j] = kp[page, :, j % ps]
+            v[b, :, j] = vp[page, :, j % ps]
+    np.testing.assert_allclose(orc.decode_paged(q, kp, vp, table, lens, 0.5),
+                               orc.decode_varlen(q, k, v, lens, 0.5), rtol=0, atol=1e-15)
+
+
+def test_decode_paged_out_of_pool_page_masks_its_keys():
+    q, kp, vp, table = _pool_inputs(6)
+    table[1, 1] = 99  # outside the 6-page pool
+    lens = np.array([12, 12, 12])
+    out = orc.decode_paged(q, kp, vp, table, lens)
+    # row 1 sees its pages 0 and 2 only
+    k = np.concatenate([kp[table[1, 0]], kp[table[1, 2]]], axis=1)[None]
+    v = np.concatenate([vp[table[1, 0]], vp[table[1, 2]]], axis=1)[None]
+    np.testing.assert_allclose(out[1:2], orc.decode(q[1:2], k, v), rtol=0, atol=1e-15)
+
+
+def test_kv_cache_update_paged_matches_loops():
+    rng = np.random.default_rng(7)
+    k, v = rng.standard_normal((2, 3, 4, 5)), rng.standard_normal((2, 3, 4, 5))
+    kp, vp = rng.standard_normal((4, 3, 8, 5)), rng.standard_normal((4, 3, 8, 5))
+    slots = np.array([[0, 9, -1, 31], [17, 40, 2, 8]])
+    nk, nv = orc.kv_cache_update_paged(k, v, kp, vp, slots)
+    ek, ev = kp.copy(), vp.copy()
+    for b in range(2):
+        for t in range(4):
+            s = slots[b, t]
+            if 0 <= s < 32:
+                for h in range(3):
+                    for d in range(5):
+                        ek[s // 8, h, s % 8, d] = k[b, h, t, d]
+                        ev[s // 8, h, s % 8, d] = v[b, h, t, d]
+    assert np.array_equal(nk, ek) and np.array_equal(nv, ev)

@@ -128,3 +128,21 @@ def test_kv_cache_update_reference_path():
     assert np.array_equal(_np(kc), ek) and np.array_equal(_np(vc), ev)
     with pytest.raises(ValueError, match="slot_indices"):
         kv_cache_update(k, v, kc, vc, slots[:1])
+
+
+def test_decode_paged_and_cache_update_paged_reference_path():
+    from stackkernels_amd.torch import kv_cache_update
+
+    torch.manual_seed(5)
+    q = torch.randn(2, 4, 1, 16)
+    kp, vp = torch.randn(6, 2, 32, 16), torch.randn(6, 2, 32, 16)
+    table = torch.tensor([[5, 0, 2], [1, -1, 4]])
+    lens = torch.tensor([70, 96])
+    out = flash_decode(q, kp, vp, cache_seqlens=lens, block_table=table)
+    ref = orc.decode_paged(_np(q), _np(kp), _np(vp), table.numpy(), lens.numpy())
+    np.testing.assert_allclose(_np(out), ref, atol=1e-5)
+    k, v = torch.randn(2, 2, 3, 16), torch.randn(2, 2, 3, 16)
+    slots = torch.tensor([[0, 33, -1], [191, 64, 500]])
+    ek, ev = orc.kv_cache_update_paged(_np(k), _np(v), _np(kp), _np(vp), slots.numpy())
+    kv_cache_update(k, v, kp, vp, slots, paged=True)
+    assert np.array_equal(_np(kp), ek) and np.array_equal(_np(vp), ev)
