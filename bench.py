@@ -17,6 +17,9 @@ Workloads (inputs synthetic, seeded, generated on the device):
 * ``decode_varlen`` -- decode on the C4 cache with a seeded cache length per
                     batch row, uniform in [1, S_k] (``cache_seqlens``).  GB/s over
                     the keys each row sees + q read + O written.
+* ``decode_paged`` -- ``decode_varlen`` over a paged pool: 64-key pages, each row's
+                    pages drawn from one shuffled pool (``block_table``).  Same
+                    bytes as ``decode_varlen``.
 * ``kv_update``  -- in-place append of 128 new key/value tokens per row into the
                     C4 cache at seeded distinct slots (``kv_cache_update``).  GB/s
                     over the new K/V read + the cache rows written + the slots.
@@ -60,6 +63,7 @@ HBM_TRAFFIC_BYTES = {
     "decode_mqa": 572_983_785,
     "decode_varlen": 4_305_177_417,
     "kv_update": 67_274_953,
+    "decode_paged": 4_305_404_288,
 }
 
 
@@ -87,6 +91,10 @@ WORKLOADS = {
     "kv_update": dict(name="kv_cache_update bf16, C4 cache, 128 new tokens per row", B=64, Hq=32,
                       Hkv=8, Sq=128, Sk=32768, D=128, causal=False, dtype="bf16",
                       kind="kv_update"),
+    "decode_paged": dict(name="flash_decode bf16 GQA over a paged pool: 64-key pages, shuffled "
+                              "block table, C4 capacity, per-row lengths U[1, Sk]", B=64, Hq=32,
+                         Hkv=8, Sq=1, Sk=32768, D=128, causal=False, dtype="bf16",
+                         kind="decode_paged", page_size=64),
 }
 
 
@@ -96,6 +104,16 @@ def varlen_lengths(w: dict):
 
     g = torch.Generator().manual_seed(3)
     return torch.randint(1, w["Sk"] + 1, (w["B"],), generator=g, dtype=torch.int32)
+
+
+def paged_table(w: dict):
+    """Seeded block table of the decode_paged workload: every row's pages drawn
+    without repetition from one shuffled pool of B * Sk / page_size pages."""
+    import torch
+
+    per_row = w["Sk"] // w["page_size"]
+    g = torch.Generator().manual_seed(5)
+    return torch.randperm(w["B"] * per_row, generator=g).view(w["B"], per_row).to(torch.int32)
 
 
 def update_slots(w: dict):
@@ -113,7 +131,7 @@ def work_units(w: dict) -> tuple[float, str]:
         kv = 2 * w["B"] * w["Hkv"] * w["Sk"] * w["D"] * esz
         qo = 2 * w["B"] * w["Hq"] * w["D"] * esz
         return float(kv + qo), "GB/s"
-    if w["kind"] == "decode_varlen":
+    if w["kind"] in ("decode_varlen", "decode_paged"):
         esz = 2
         kv = 2 * int(varlen_lengths(w).sum()) * w["Hkv"] * w["D"] * esz  # the keys each row sees
         qo = 2 * w["B"] * w["Hq"] * w["D"] * esz
@@ -134,6 +152,12 @@ def _make_inputs(w: dict, torch, dev, sets: int = 1):
     dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float16
     g = torch.Generator(device=dev).manual_seed(0)
     out = []
+    if w["kind"] == "decode_paged":  # (q, k_pool, v_pool)
+        pages = w["B"] * w["Sk"] // w["page_size"]
+        shp = (pages, w["Hkv"], w["page_size"], w["D"])
+        return [(torch.randn(w["B"], w["Hq"], 1, w["D"], generator=g, device=dev, dtype=dt),
+                 torch.randn(shp, generator=g, device=dev, dtype=dt),
+                 torch.randn(shp, generator=g, device=dev, dtype=dt))]
     if w["kind"] == "kv_update":  # (new k, new v, k_cache, v_cache)
         shp_new = (w["B"], w["Hkv"], w["Sq"], w["D"])
         shp_cache = (w["B"], w["Hkv"], w["Sk"], w["D"])
@@ -176,6 +200,26 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
                                         vc.data_ptr(), slots.data_ptr(), B, Hkv, Sq, Sk, D,
                                         *sts, stream)
             _lib.check(rc, "sk_kv_cache_update")
+        return launch
+    if w["kind"] == "decode_paged":
+        ns = ctypes.c_int(0)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+                   "plan")
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+        q, kp, vp = inputs[0]
+        o = torch.empty_like(q)
+        lens = varlen_lengths(w).to(dev)
+        table = paged_table(w).to(dev)
+        sts = [_lib.strides3(t) for t in (q, kp, vp, o)]
+        ps = w["page_size"]
+
+        def launch(i):
+            rc = lib.sk_decode_paged(code, q.data_ptr(), kp.data_ptr(), vp.data_ptr(), o.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), ns.value, B, Hq, Hkv, kp.shape[0],
+                                     ps, table.shape[1], D, *sts, table.data_ptr(),
+                                     lens.data_ptr(), scale, stream)
+            _lib.check(rc, "sk_decode_paged")
         return launch
     if w["kind"] == "decode_varlen":
         ns = ctypes.c_int(0)
@@ -320,6 +364,19 @@ def run_gpu(w: dict, steps: int, warmup: int):
         def step(i):
             q, k, v = inputs[0]
             flash_decode(q, k, v, cache_seqlens=lens_dev)
+    elif w["kind"] == "decode_paged":
+        from stackkernels_amd._core.attention.decode import flash_decode_paged
+
+        q0 = inputs[0][0]
+        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        lens_dev = varlen_lengths(w).to(dev)
+        table_dev = paged_table(w).to(dev)
+        details["mean_length"] = round(float(lens_dev.float().mean()), 1)
+        details["page_size"] = w["page_size"]
+
+        def step(i):
+            q, kp, vp = inputs[0]
+            flash_decode_paged(q, kp, vp, table_dev, lens_dev)
     elif w["kind"] == "kv_update":
         from stackkernels_amd.torch.cache import kv_cache_update
 
@@ -362,7 +419,20 @@ def _cpu_baseline_next_rows(w: dict, budget_s: float):
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
     D, Hq, Hkv = w["D"], w["Hq"], w["Hkv"]
-    if w["kind"] == "decode_varlen":
+    if w["kind"] == "decode_paged":
+        n = int(varlen_lengths(w)[0])
+        ps = w["page_size"]
+        n_pages = (n + ps - 1) // ps
+        q = torch.randn(1, Hq, 1, D, generator=g).bfloat16()
+        kp = torch.randn(n_pages, Hkv, ps, D, generator=g).bfloat16()
+        vp = torch.randn(n_pages, Hkv, ps, D, generator=g).bfloat16()
+        table = torch.randperm(n_pages, generator=g).view(1, n_pages)
+        units_one = 2 * n * Hkv * D * 2 + 2 * Hq * D * 2
+        fn = lambda: flash_decode(q, kp, vp, cache_seqlens=torch.tensor([n]),  # noqa: E731
+                                  block_table=table)
+        what = (f"paged flash_decode reference path on batch row 0 (length {n}, {n_pages} "
+                f"pages of {ps} keys, {Hq} query heads)")
+    elif w["kind"] == "decode_varlen":
         n = int(varlen_lengths(w)[0])
         q = torch.randn(1, Hq, 1, D, generator=g).bfloat16()
         k = torch.randn(1, Hkv, n, D, generator=g).bfloat16()
@@ -406,7 +476,7 @@ def run_cpu_baseline(w: dict, budget_s: float):
 
     from stackkernels_amd._reference.torch.attention import attention_reference
 
-    if w["kind"] in ("decode_varlen", "kv_update"):
+    if w["kind"] in ("decode_varlen", "kv_update", "decode_paged"):
         return _cpu_baseline_next_rows(w, budget_s)
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
@@ -459,6 +529,7 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
     kernel = {"fwd": "fwd_mfma_kernel", "fwdbwd": "fwd + bwd kernels",
               "decode": "decode_split_kernel + decode_combine_kernel",
               "decode_varlen": "decode_split_kernel + decode_combine_kernel",
+              "decode_paged": "decode_split_kernel (paged) + decode_combine_kernel",
               "kv_update": "kv_cache_update_kernel"}[w["kind"]]
     if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
         kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
