@@ -23,6 +23,13 @@ Workloads (inputs synthetic, seeded, generated on the device):
 * ``kv_update``  -- in-place append of 128 new key/value tokens per row into the
                     C4 cache at seeded distinct slots (``kv_cache_update``).  GB/s
                     over the new K/V read + the cache rows written + the slots.
+* ``decode_rope`` -- C4 decode with the RoPE rotation of q fused into the decode
+                    kernel (fp32 (Sk, D) tables, every row's query at position
+                    Sk - 1).  Bytes of ``decode`` + the table rows read.
+* ``kv_update_rope`` -- the cache append with the new keys rotated on the way in:
+                    128 tokens per row appended at seeded per-row positions
+                    p_b .. p_b + 127 (slots = positions), fp32 tables.  Bytes of
+                    ``kv_update`` + the distinct table rows read.
 
 ``python bench.py`` runs ``fwd`` as the headline (``value``) and, unless
 ``--no-extra``, the others as entries of ``extra``.  Each line carries a
@@ -95,6 +102,14 @@ WORKLOADS = {
                               "block table, C4 capacity, per-row lengths U[1, Sk]", B=64, Hq=32,
                          Hkv=8, Sq=1, Sk=32768, D=128, causal=False, dtype="bf16",
                          kind="decode_paged", page_size=64),
+    # RoPE fused into the decode prologue and into the cache append.
+    "decode_rope": dict(name="C4 flash_decode bf16 GQA, RoPE of q fused (fp32 tables, position "
+                             "Sk-1)", B=64, Hq=32, Hkv=8, Sq=1, Sk=32768, D=128, causal=False,
+                        dtype="bf16", kind="decode_rope"),
+    "kv_update_rope": dict(name="kv_cache_update bf16, RoPE of the new keys fused, C4 cache, 128 "
+                                "new tokens per row at seeded per-row positions", B=64, Hq=32,
+                           Hkv=8, Sq=128, Sk=32768, D=128, causal=False, dtype="bf16",
+                           kind="kv_update_rope"),
 }
 
 
@@ -124,8 +139,33 @@ def update_slots(w: dict):
     return torch.stack([torch.randperm(w["Sk"], generator=g)[:w["Sq"]] for _ in range(w["B"])])
 
 
+def rope_starts(w: dict):
+    """Seeded per-row positions of the first appended token (kv_update_rope),
+    uniform in [0, Sk - T]: int32 (B,)."""
+    import torch
+
+    g = torch.Generator().manual_seed(6)
+    return torch.randint(0, w["Sk"] - w["Sq"] + 1, (w["B"],), generator=g, dtype=torch.int32)
+
+
+def rope_tables(w: dict, dev):
+    """fp32 (Sk, D) cos / sin tables (the reference's precompute_freqs)."""
+    from stackkernels_amd._reference.torch.rope import precompute_freqs
+
+    return precompute_freqs(w["D"], w["Sk"], device=dev)
+
+
 def work_units(w: dict) -> tuple[float, str]:
     """Algorithmic work of one step: (FLOP or bytes, unit of the rate)."""
+    if w["kind"] == "decode_rope":
+        base, unit = work_units(dict(w, kind="decode"))
+        return base + 2 * w["D"] * 4, unit  # one (cos, sin) row pair: every query at Sk - 1
+    if w["kind"] == "kv_update_rope":
+        import torch
+
+        base, unit = work_units(dict(w, kind="kv_update"))
+        pos = rope_starts(w)[:, None].long() + torch.arange(w["Sq"])
+        return base + int(pos.unique().numel()) * 2 * w["D"] * 4, unit
     if w["kind"] == "decode":
         esz = 2
         kv = 2 * w["B"] * w["Hkv"] * w["Sk"] * w["D"] * esz
@@ -158,7 +198,7 @@ def _make_inputs(w: dict, torch, dev, sets: int = 1):
         return [(torch.randn(w["B"], w["Hq"], 1, w["D"], generator=g, device=dev, dtype=dt),
                  torch.randn(shp, generator=g, device=dev, dtype=dt),
                  torch.randn(shp, generator=g, device=dev, dtype=dt))]
-    if w["kind"] == "kv_update":  # (new k, new v, k_cache, v_cache)
+    if w["kind"] in ("kv_update", "kv_update_rope"):  # (new k, new v, k_cache, v_cache)
         shp_new = (w["B"], w["Hkv"], w["Sq"], w["D"])
         shp_cache = (w["B"], w["Hkv"], w["Sk"], w["D"])
         return [(torch.randn(shp_new, generator=g, device=dev, dtype=dt),
@@ -190,6 +230,39 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
     B, Hq, Hkv, Sq, Sk, D = (w[k_] for k_ in ("B", "Hq", "Hkv", "Sq", "Sk", "D"))
     scale = 1.0 / math.sqrt(D)
     q0 = inputs[0][0]
+    if w["kind"] == "kv_update_rope":
+        kn, vn, kc, vc = inputs[0]
+        starts = rope_starts(w)
+        slots = (starts[:, None].long() + torch.arange(Sq)).to(dev)
+        cos, sin = rope_tables(w, dev)
+        sts = [_lib.strides3(t) for t in (kn, vn, kc, vc)]
+        starts_dev = starts.to(dev)
+
+        def launch(i):
+            rc = lib.sk_kv_cache_update_rope(code, kn.data_ptr(), vn.data_ptr(), kc.data_ptr(),
+                                             vc.data_ptr(), slots.data_ptr(), B, Hkv, Sq, Sk, D,
+                                             *sts, cos.data_ptr(), sin.data_ptr(), _lib.SK_F32,
+                                             Sk, D, starts_dev.data_ptr(), 0, stream)
+            _lib.check(rc, "sk_kv_cache_update_rope")
+        return launch
+    if w["kind"] == "decode_rope":
+        ns = ctypes.c_int(0)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+                   "plan")
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+        q, k, v = inputs[0]
+        o = torch.empty_like(q)
+        cos, sin = rope_tables(w, dev)
+        sts = [_lib.strides3(t) for t in (q, k, v, o)]
+
+        def launch(i):
+            rc = lib.sk_decode_rope(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), ns.value, B, Hq, Hkv, Sk, D, *sts,
+                                    None, cos.data_ptr(), sin.data_ptr(), _lib.SK_F32, Sk, D,
+                                    None, Sk - 1, scale, stream)
+            _lib.check(rc, "sk_decode_rope")
+        return launch
     if w["kind"] == "kv_update":
         kn, vn, kc, vc = inputs[0]
         slots = update_slots(w).to(dev)
@@ -377,6 +450,26 @@ def run_gpu(w: dict, steps: int, warmup: int):
         def step(i):
             q, kp, vp = inputs[0]
             flash_decode_paged(q, kp, vp, table_dev, lens_dev)
+    elif w["kind"] == "decode_rope":
+        q0 = inputs[0][0]
+        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        cos, sin = rope_tables(w, dev)
+
+        def step(i):
+            q, k, v = inputs[0]
+            flash_decode(q, k, v, rope_cos=cos, rope_sin=sin, start_pos=w["Sk"] - 1)
+    elif w["kind"] == "kv_update_rope":
+        from stackkernels_amd.torch.cache import kv_cache_update
+
+        starts = rope_starts(w)
+        slots_dev = (starts[:, None].long() + torch.arange(w["Sq"])).to(dev)
+        starts_dev = starts.to(dev)
+        cos, sin = rope_tables(w, dev)
+
+        def step(i):
+            kn, vn, kc, vc = inputs[0]
+            kv_cache_update(kn, vn, kc, vc, slots_dev, rope_cos=cos, rope_sin=sin,
+                            start_pos=starts_dev)
     elif w["kind"] == "kv_update":
         from stackkernels_amd.torch.cache import kv_cache_update
 
@@ -440,6 +533,29 @@ def _cpu_baseline_next_rows(w: dict, budget_s: float):
         units_one = 2 * n * Hkv * D * 2 + 2 * Hq * D * 2
         fn = lambda: flash_decode(q, k, v, cache_seqlens=torch.tensor([n]))  # noqa: E731
         what = f"flash_decode reference path on batch row 0 (length {n}, {Hq} query heads)"
+    elif w["kind"] == "decode_rope":
+        n = w["Sk"]
+        q = torch.randn(1, Hq, 1, D, generator=g).bfloat16()
+        k = torch.randn(1, Hkv, n, D, generator=g).bfloat16()
+        v = torch.randn(1, Hkv, n, D, generator=g).bfloat16()
+        cos, sin = rope_tables(w, "cpu")
+        units_one = 2 * n * Hkv * D * 2 + 2 * Hq * D * 2 + 2 * D * 4
+        fn = lambda: flash_decode(q, k, v, rope_cos=cos, rope_sin=sin,  # noqa: E731
+                                  start_pos=n - 1)
+        what = f"flash_decode reference path with RoPE of q on batch row 0 ({n} keys)"
+    elif w["kind"] == "kv_update_rope":
+        T = w["Sq"]
+        kn = torch.randn(1, Hkv, T, D, generator=g).bfloat16()
+        vn = torch.randn(1, Hkv, T, D, generator=g).bfloat16()
+        kc = torch.zeros(1, Hkv, w["Sk"], D, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        st = rope_starts(w)[:1]
+        sl = st[:, None].long() + torch.arange(T)
+        cos, sin = rope_tables(w, "cpu")
+        units_one = 4 * Hkv * T * D * 2 + T * 8 + T * 2 * D * 4
+        fn = lambda: kv_cache_update(kn, vn, kc, vc, sl, rope_cos=cos, rope_sin=sin,  # noqa: E731
+                                     start_pos=st)
+        what = f"kv_cache_update reference path with RoPE of k on batch row 0 ({T} tokens)"
     else:
         T = w["Sq"]
         kn = torch.randn(1, Hkv, T, D, generator=g).bfloat16()
@@ -476,7 +592,8 @@ def run_cpu_baseline(w: dict, budget_s: float):
 
     from stackkernels_amd._reference.torch.attention import attention_reference
 
-    if w["kind"] in ("decode_varlen", "kv_update", "decode_paged"):
+    if w["kind"] in ("decode_varlen", "kv_update", "decode_paged", "decode_rope",
+                     "kv_update_rope"):
         return _cpu_baseline_next_rows(w, budget_s)
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
@@ -530,7 +647,9 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
               "decode": "decode_split_kernel + decode_combine_kernel",
               "decode_varlen": "decode_split_kernel + decode_combine_kernel",
               "decode_paged": "decode_split_kernel (paged) + decode_combine_kernel",
-              "kv_update": "kv_cache_update_kernel"}[w["kind"]]
+              "kv_update": "kv_cache_update_kernel",
+              "decode_rope": "decode_split_kernel (q rotated on load) + decode_combine_kernel",
+              "kv_update_rope": "kv_cache_update_rope_kernel"}[w["kind"]]
     if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
         kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
     res = {

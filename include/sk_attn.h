@@ -34,7 +34,7 @@ extern "C" {
 #define SK_API
 #endif
 
-#define SK_ABI_VERSION 3
+#define SK_ABI_VERSION 4
 
 /* Element type codes. */
 #define SK_F32 0
@@ -202,6 +202,92 @@ SK_API int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, voi
                              const int64_t* k_strides, const int64_t* v_strides,
                              const int64_t* kp_strides, const int64_t* vp_strides,
                              void* stream);
+
+/*
+ * RoPE fused into the attention prologue.  The *_rope entry points below take
+ * the arguments of the call they extend plus a rotary position embedding that
+ * the kernels apply to q (attention, decode) or to the new keys (cache
+ * append) as they load them, so the rotated vectors never make a separate
+ * trip through HBM.  The rotation is the reference's apply_rope
+ * (src/stackkernels/torch/embedding.py:67-100; math in
+ * src/stackkernels/_reference/torch/rope.py:32-58):
+ *
+ *   out[d] = x[d] cos[p][d] - x[d + D/2] sin[p][d]   (d <  D/2)
+ *   out[d] = x[d] cos[p][d] + x[d - D/2] sin[p][d]   (d >= D/2)
+ *
+ * in fp32 (two products and a sum, each rounded; no fused multiply-add),
+ * rounded to the tensor's type.  Arguments:
+ *
+ *   rope_cos, rope_sin  device tables of rope_rows rows (element stride
+ *                       rope_stride >= D between rows; the first D columns are
+ *                       read), element type rope_dtype (SK_F32/F16/BF16) --
+ *                       the (max_seq_len, D) tables of precompute_freqs
+ *                       (src/stackkernels/_reference/torch/rope.py:6-29);
+ *   rope_pos            NULL, or a device array of B int32 per-row base positions;
+ *   rope_start          added to every position (the reference's start_pos).
+ *
+ * Token t of batch row b sits at p = (rope_pos ? rope_pos[b] : 0) + rope_start + t:
+ * query row t for attention, t = 0 for the decode query, new token t for the
+ * cache append.  With rope_pos NULL, [rope_start, rope_start + tokens) must lie
+ * in the table (SK_EINVAL otherwise, as the reference's table slice fails);
+ * with rope_pos given, a position outside [0, rope_rows) leaves that vector
+ * unrotated.  D must be a multiple of 16 (SK_EUNSUPPORTED otherwise).  The
+ * reference has no fused counterpart: it rotates q and k in a separate pass
+ * (src/stackkernels/_core/positional/rope.py:12-222) before attention.
+ */
+
+/* sk_attn_fwd with q rotated on load (query row i is token i).  Forward only:
+ * sk_attn_bwd takes the rotated q, which this call does not write out. */
+SK_API int sk_attn_fwd_rope(int dtype, const void* q, const void* k, const void* v, void* o,
+                     float* lse, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                     const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides, int is_causal,
+                     const void* rope_cos, const void* rope_sin, int rope_dtype, int rope_rows,
+                     int64_t rope_stride, const int32_t* rope_pos, int rope_start,
+                     float sm_scale, void* stream);
+
+/* sk_decode (cache_seqlens NULL) or sk_decode_varlen with q rotated on load. */
+SK_API int sk_decode_rope(int dtype, const void* q, const void* k, const void* v, void* o,
+                   void* workspace, size_t workspace_bytes, int num_splits,
+                   int B, int Hq, int Hkv, int Sk, int D,
+                   const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* o_strides,
+                   const int32_t* cache_seqlens, const void* rope_cos, const void* rope_sin,
+                   int rope_dtype, int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                   int rope_start, float sm_scale, void* stream);
+
+/* sk_decode_paged with q rotated on load. */
+SK_API int sk_decode_paged_rope(int dtype, const void* q, const void* k_pool, const void* v_pool,
+                         void* o, void* workspace, size_t workspace_bytes, int num_splits,
+                         int B, int Hq, int Hkv, int num_pages, int page_size, int max_pages,
+                         int D, const int64_t* q_strides, const int64_t* kp_strides,
+                         const int64_t* vp_strides, const int64_t* o_strides,
+                         const int32_t* block_table, const int32_t* cache_seqlens,
+                         const void* rope_cos, const void* rope_sin, int rope_dtype,
+                         int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                         int rope_start, float sm_scale, void* stream);
+
+/* sk_kv_cache_update with the new keys rotated before they are written (new
+ * token t is token t); values are copied unchanged.  k, v, the caches and all
+ * their strides must be 16-byte aligned. */
+SK_API int sk_kv_cache_update_rope(int dtype, const void* k, const void* v, void* k_cache,
+                            void* v_cache, const int64_t* slots, int B, int Hkv, int T,
+                            int S_cache, int D, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* kc_strides,
+                            const int64_t* vc_strides, const void* rope_cos,
+                            const void* rope_sin, int rope_dtype, int rope_rows,
+                            int64_t rope_stride, const int32_t* rope_pos, int rope_start,
+                            void* stream);
+
+/* sk_kv_cache_update_paged with the new keys rotated (as above). */
+SK_API int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v, void* k_pool,
+                                  void* v_pool, const int64_t* slot_mapping, int B, int Hkv,
+                                  int T, int num_pages, int page_size, int D,
+                                  const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* kp_strides, const int64_t* vp_strides,
+                                  const void* rope_cos, const void* rope_sin, int rope_dtype,
+                                  int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                                  int rope_start, void* stream);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,13 @@ What it restates (all arithmetic in float64 unless a caller asks otherwise):
                               ``table[b, j // page_size]``, row ``j % page_size``; a page
                               outside the pool masks its keys): the paged KV decode of
                               the roadmap (stub ``_core/attention/paged.py``).
+* ``rope_tables`` / ``rope_positions`` / ``rope_rotate`` / ``round_to`` -- RoPE:
+                              ``precompute_freqs``, ``rotate_half`` and
+                              ``apply_rope_single`` of ``_reference/torch/rope.py:6-58``
+                              (fp32 products and sum, each rounded, then rounded
+                              to the tensor type), with one position per (row,
+                              token); the fused paths are these composed with
+                              ``attention_forward`` / ``decode*`` / ``kv_cache_update*``.
 
 How each function is pinned (see ``tests/test_oracle.py``):
 
@@ -58,6 +65,17 @@ How each function is pinned (see ``tests/test_oracle.py``):
   ``decode_paged`` against ``decode_varlen`` on caches assembled page by page
   with a loop, and with a page index outside the pool against the same row
   cut at that page; ``kv_cache_update_paged`` against a per-element loop.
+* RoPE: ``rope_tables`` against cos/sin of the angle written out per entry,
+  with row 0 all (1, 0) and the two halves equal; ``rope_rotate`` against the
+  rotation written as a complex product (x_d + i x_{d+D/2}) e^{i angle} in
+  float64, which fixes the sign and the half that is negated, against a
+  per-element loop, through the invariants it must keep (the norm of each
+  (d, d + D/2) pair, identity at position 0, rotation by p1 then p2 equals
+  rotation by p1 + p2), and with out-of-table positions; ``round_to`` against
+  torch's own bfloat16 / float16 casts, ties included.  The reference's RoPE
+  tests (``tests/ops/test_rope.py``) hold no fixed vectors: they compare its
+  kernel with its torch restatement at start_pos 0, 15, 23, 31, 64, and the
+  same start positions are used here.
 """
 
 from __future__ import annotations
@@ -319,6 +337,67 @@ def kv_cache_update_paged(k, v, k_pool, v_pool, slots):
     return kp, vp
 
 
+def round_to(x, dtype: str) -> np.ndarray:
+    """float32 values rounded to the element type ``dtype`` ("bf16", "f16",
+    "f32"; round to nearest even), returned as float32.  bf16 is the upper
+    half of the fp32 bit pattern after adding 0x7fff plus the lowest kept bit
+    (finite inputs)."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "f32":
+        return x.copy()
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype != "bf16":
+        raise ValueError(dtype)
+    u = x.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def rope_tables(dim: int, max_seq_len: int, base: float = 10000.0):
+    """(cos, sin), each (max_seq_len, dim) float64: angle t * base^(-i / (dim/2))
+    for column i < dim/2, the same angles again for the second half
+    (``src/stackkernels/_reference/torch/rope.py:6-29``)."""
+    half = dim // 2
+    inv_freq = 1.0 / (base ** (np.arange(half, dtype=np.float64) / half))
+    ang = np.outer(np.arange(max_seq_len, dtype=np.float64), inv_freq)
+    ang = np.concatenate([ang, ang], axis=1)
+    return np.cos(ang), np.sin(ang)
+
+
+def rope_positions(start_pos, b: int, tokens: int) -> np.ndarray:
+    """(B, tokens) positions: start_pos + t, or start_pos[b] + t per row
+    (``start_pos`` of ``src/stackkernels/_reference/torch/rope.py:40-58``, per row)."""
+    t = np.arange(tokens, dtype=np.int64)
+    base = np.asarray(start_pos, dtype=np.int64).reshape(-1, 1)
+    return np.broadcast_to(base + t, (b, tokens)).copy()
+
+
+def rope_rotate(x, cos, sin, positions) -> np.ndarray:
+    """RoPE of x (B, H, S, D) with token (b, s) at ``positions[b, s]``.
+
+    ``apply_rope_single`` (``src/stackkernels/_reference/torch/rope.py:40-58``,
+    ``rotate_half`` ``:32-37``): out = x * cos + rotate_half(x) * sin with
+    rotate_half(x) = (-x2, x1), in float32 with each product and the sum
+    rounded (numpy float32 arithmetic is IEEE round-to-nearest-even).  The
+    caller rounds the float32 result to the tensor's type (``round_to``).  A
+    position outside the table leaves its token as it is.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    c = np.asarray(cos, dtype=np.float32)
+    s = np.asarray(sin, dtype=np.float32)
+    pos = np.asarray(positions, dtype=np.int64)
+    d = x.shape[-1]
+    half = d // 2
+    ok = (pos >= 0) & (pos < c.shape[0])
+    idx = np.where(ok, pos, 0)
+    cc = c[idx][:, None, :, :d]  # (B, 1, S, D)
+    ss = s[idx][:, None, :, :d]
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    out = (x * cc) + (rot * ss)
+    return np.where(ok[:, None, :, None], out, x).astype(np.float32)
+
+
 def attention_forward_loops(q, k, v, is_causal=False, sm_scale=None):
     """Brute-force per-element restatement for tiny shapes (pins ``attention_forward``)."""
     q = np.asarray(q, dtype=np.float64)
@@ -356,5 +435,14 @@ __all__ = [
     "decode",
     "split_partials",
     "combine_partials",
+    "decode_varlen",
+    "kv_cache_update",
+    "gather_pages",
+    "decode_paged",
+    "kv_cache_update_paged",
+    "round_to",
+    "rope_tables",
+    "rope_positions",
+    "rope_rotate",
     "attention_forward_loops",
 ]

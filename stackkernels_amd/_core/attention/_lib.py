@@ -15,7 +15,7 @@ import threading
 
 SK_F32, SK_F16, SK_BF16 = 0, 1, 2
 SK_OK, SK_EINVAL, SK_EUNSUPPORTED, SK_EWORKSPACE = 0, -1, -2, -3
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "csrc")
 LIB_PATH = os.environ.get("SK_ATTN_LIB", os.path.join(_LIB_DIR, "libsk_attn.so"))
@@ -31,6 +31,9 @@ _sizep = ctypes.POINTER(ctypes.c_size_t)
 _intp = ctypes.POINTER(ctypes.c_int)
 
 # name -> (restype, argtypes); mirrors include/sk_attn.h.
+# RoPE arguments: cos, sin, table dtype, rows, row stride, positions, start.
+_ROPE = (_vp, _vp, _c_int, _c_int, ctypes.c_int64, _vp, _c_int)
+
 SIGNATURES: dict[str, tuple] = {
     "sk_abi_version": (_c_int, []),
     "sk_last_error": (ctypes.c_char_p, []),
@@ -60,6 +63,24 @@ SIGNATURES: dict[str, tuple] = {
     "sk_kv_cache_update_paged": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,
                                           _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                           _i64p, _i64p, _i64p, _i64p, _vp]),
+    # *_rope: the call they extend with (cos, sin, table dtype, rows, row
+    # stride, per-row positions, start) inserted before sm_scale / stream.
+    "sk_attn_fwd_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,
+                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                  _i64p, _i64p, _i64p, _i64p, _c_int, *_ROPE, _c_float, _vp]),
+    "sk_decode_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _c_int,
+                                _c_int, _c_int, _c_int, _c_int, _c_int,
+                                _i64p, _i64p, _i64p, _i64p, _vp, *_ROPE, _c_float, _vp]),
+    "sk_decode_paged_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _c_int,
+                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _i64p, _i64p, _i64p, _i64p, _vp, _vp, *_ROPE, _c_float,
+                                      _vp]),
+    "sk_kv_cache_update_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,
+                                         _c_int, _c_int, _c_int, _c_int, _c_int,
+                                         _i64p, _i64p, _i64p, _i64p, *_ROPE, _vp]),
+    "sk_kv_cache_update_paged_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,
+                                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                               _i64p, _i64p, _i64p, _i64p, *_ROPE, _vp]),
 }
 
 

@@ -1,0 +1,69 @@
+"""RoPE arguments of the fused ``*_rope`` library calls.
+
+The rotation is the reference's ``apply_rope`` (``src/stackkernels/torch/embedding.py:67-100``;
+math in ``src/stackkernels/_reference/torch/rope.py:32-58``), applied by the
+kernels to q or to the new keys as they load them.  Tables are the
+``(max_seq_len, D)`` ``cos`` / ``sin`` of ``precompute_freqs``
+(``_reference/torch/rope.py:6-29``); ``start_pos`` is the reference's
+``start_pos`` (an int for the whole batch) or, for a batch of sequences at
+different lengths, an integer ``(B,)`` tensor of per-row positions.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from stackkernels_amd._core.attention import _lib
+
+_TABLE_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+class RopeArgs:
+    """Validated tables and positions; ``args`` is the ctypes tail
+    (cos, sin, dtype code, rows, row stride, positions or None, start)."""
+
+    def __init__(self, cos, sin, start_pos, b: int, d: int, dev: torch.device):
+        if cos is None or sin is None:
+            raise ValueError("RoPE needs both cos and sin tables")
+        for name, t in (("cos", cos), ("sin", sin)):
+            if not isinstance(t, torch.Tensor) or t.dim() != 2:
+                raise ValueError(f"{name} must be a 2-D (max_seq_len, D) tensor")
+            if t.device != dev:
+                raise ValueError(f"{name} is on {t.device}, the attention tensors on {dev}")
+            if t.dtype not in _TABLE_DTYPES:
+                raise NotImplementedError(f"{name} dtype {t.dtype} unsupported "
+                                          f"(float32, float16, bfloat16)")
+        if cos.shape != sin.shape or cos.dtype != sin.dtype:
+            raise ValueError(f"cos {tuple(cos.shape)} {cos.dtype} and sin {tuple(sin.shape)} "
+                             f"{sin.dtype} differ")
+        if cos.shape[1] != d:
+            raise ValueError(f"RoPE tables have {cos.shape[1]} columns, head dim is {d}")
+        if d % 16 != 0:
+            raise NotImplementedError(f"fused RoPE needs a head dim that is a multiple of 16, "
+                                      f"got {d}")
+        if cos.stride(1) != 1 or sin.stride(1) != 1 or cos.stride(0) != sin.stride(0):
+            cos, sin = cos.contiguous(), sin.contiguous()
+        self.cos, self.sin = cos, sin
+        self.pos = None
+        start = 0
+        if isinstance(start_pos, torch.Tensor):
+            if start_pos.dim() != 1 or start_pos.shape[0] != b:
+                raise ValueError(f"start_pos tensor must have shape ({b},), got "
+                                 f"{tuple(start_pos.shape)}")
+            if start_pos.dtype.is_floating_point or start_pos.dtype == torch.bool:
+                raise ValueError(f"start_pos must be an integer tensor, got {start_pos.dtype}")
+            self.pos = start_pos.to(device=dev, dtype=torch.int32).contiguous()
+        else:
+            start = int(start_pos)
+        self.args = (cos.data_ptr(), sin.data_ptr(), _lib.dtype_code(cos.dtype), cos.shape[0],
+                     cos.stride(0), None if self.pos is None else self.pos.data_ptr(), start)
+
+
+def rope_args(cos, sin, start_pos, b: int, d: int, dev: torch.device) -> RopeArgs | None:
+    """None when no table is given (no rotation), else the validated arguments."""
+    if cos is None and sin is None:
+        return None
+    return RopeArgs(cos, sin, start_pos, b, d, dev)
+
+
+__all__ = ["RopeArgs", "rope_args"]

@@ -8,6 +8,8 @@ k/v (B, H_kv, S_k, D) with any b/h/s strides (no copy when rows are
 from the library's gfx950 table (``plan``) unless ``num_splits`` is given.
 ``cache_seqlens`` gives each batch row its own cache length (decode over a
 batch of sequences of different lengths sharing one cache capacity).
+``rope_cos`` / ``rope_sin`` / ``start_pos`` rotate q in the kernel's
+prologue (the reference's ``apply_rope`` on q, fused; see ``_rope``).
 """
 
 from __future__ import annotations
@@ -17,6 +19,7 @@ import ctypes
 import torch
 
 from stackkernels_amd._core.attention import _lib
+from stackkernels_amd._core.attention._rope import rope_args
 from stackkernels_amd._core.attention._common import (
     check_device,
     default_scale,
@@ -50,16 +53,19 @@ def _seqlens_operand(cache_seqlens, b: int, dev) -> torch.Tensor:
 
 
 def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None = None,
-                 cache_seqlens=None):
+                 cache_seqlens=None, rope_cos=None, rope_sin=None, start_pos=0):
     """Launch split + combine; see module docstring.
 
     ``cache_seqlens`` (optional, integer (B,)): row b attends to keys
     ``[0, min(cache_seqlens[b], S_k))`` of its cache (S_k is the capacity);
-    a row with no key gives O = 0."""
+    a row with no key gives O = 0.  With ``rope_cos`` / ``rope_sin``
+    ((max_seq_len, D) tables) q is rotated to position ``start_pos`` (int, or
+    integer (B,) per row) before the scores."""
     b, hq, hkv, sq, sk, d = validate_attention_layout(q, k, v)
     assert sq == 1, f"flash_decode requires q_len == 1, got {sq}"
     dev = check_device(q, k, v)
     lens = None if cache_seqlens is None else _seqlens_operand(cache_seqlens, b, dev)
+    rope = rope_args(rope_cos, rope_sin, start_pos, b, d, dev)
     scale = default_scale(d, sm_scale)
     dk = kernel_head_dim(d)
     qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k, v))
@@ -76,7 +82,14 @@ def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None 
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        if lens is None:
+        if rope is not None:
+            rc = lib.sk_decode_rope(
+                code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                ws.numel(), ns, b, hq, hkv, sk, dk,
+                _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+                None if lens is None else lens.data_ptr(), *rope.args, scale, stream_of(dev),
+            )
+        elif lens is None:
             rc = lib.sk_decode(
                 code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
                 ws.numel(), ns, b, hq, hkv, sk, dk,
@@ -108,7 +121,8 @@ def _table_operand(block_table, b: int, dev) -> torch.Tensor:
 
 
 def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
-                       sm_scale: float | None = None, num_splits: int | None = None):
+                       sm_scale: float | None = None, num_splits: int | None = None,
+                       rope_cos=None, rope_sin=None, start_pos=0):
     """Decode over a paged KV cache.
 
     q (B, H_q, 1, D); k_pool, v_pool (num_pages, H_kv, page_size, D) with any
@@ -116,7 +130,8 @@ def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
     page_size-key block of a row; cache_seqlens integer (B,): keys per row.
     Key j of row b is row ``j % page_size`` of page ``block_table[b, j // page_size]``.
     page_size must be a multiple of 32.  A page index outside the pool masks
-    its keys; a row with no key gives zeros.  Returns (B, H_q, 1, D)."""
+    its keys; a row with no key gives zeros.  Returns (B, H_q, 1, D).  RoPE
+    arguments as for ``flash_decode``."""
     if q.dim() != 4 or k_pool.dim() != 4 or v_pool.dim() != 4:
         raise ValueError("Expected 4D q (B, H, 1, D) and 4D page pools (pages, H_kv, page_size, D)")
     if k_pool.shape != v_pool.shape:
@@ -135,6 +150,7 @@ def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
     dev = check_device(q, k_pool, v_pool)
     table = _table_operand(block_table, b, dev)
     lens = _seqlens_operand(cache_seqlens, b, dev)
+    rope = rope_args(rope_cos, rope_sin, start_pos, b, d, dev)
     max_pages = table.shape[1]
     scale = default_scale(d, sm_scale)
     dk = kernel_head_dim(d)
@@ -152,13 +168,15 @@ def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
         nbytes = nb.value
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    paged_args = (code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(),
+                  ws.data_ptr(), ws.numel(), ns, b, hq, hkv, num_pages, page_size, max_pages, dk,
+                  _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
+                  table.data_ptr(), lens.data_ptr())
     with torch.cuda.device(dev):
-        rc = lib.sk_decode_paged(
-            code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), ws.data_ptr(),
-            ws.numel(), ns, b, hq, hkv, num_pages, page_size, max_pages, dk,
-            _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),
-            table.data_ptr(), lens.data_ptr(), scale, stream_of(dev),
-        )
+        if rope is None:
+            rc = lib.sk_decode_paged(*paged_args, scale, stream_of(dev))
+        else:
+            rc = lib.sk_decode_paged_rope(*paged_args, *rope.args, scale, stream_of(dev))
     _lib.check(rc, "flash_decode")
     if dk != d:
         out = out[..., :d].contiguous()

@@ -5,7 +5,9 @@ slot_indices)`` (``docs/user_guide/dropout_cache_sampling.md:66-72``; the
 reference's ``src/stackkernels/_core/cache/kv_update.py`` is a stub):
 ``k_cache[b, h, slot_indices[b, t], :] = k[b, h, t, :]`` and the same for v,
 in place, with no reallocation.  A slot outside ``[0, S_cache)`` skips its
-token (pad ragged batches with -1).
+token (pad ragged batches with -1).  With RoPE tables the new keys are
+rotated on their way into the cache (the reference's ``apply_rope`` on k,
+fused into the append; values are copied unchanged).
 """
 
 from __future__ import annotations
@@ -14,6 +16,7 @@ import torch
 
 from stackkernels_amd._core.attention import _lib
 from stackkernels_amd._core.attention._common import check_device, stream_of
+from stackkernels_amd._core.attention._rope import rope_args
 
 
 def validate_cache_update(k, v, k_cache, v_cache, slot_indices,
@@ -46,18 +49,33 @@ def validate_cache_update(k, v, k_cache, v_cache, slot_indices,
     return b, h, t, s, d
 
 
-def kv_cache_update(k, v, k_cache, v_cache, slot_indices, paged: bool = False) -> None:
+def kv_cache_update(k, v, k_cache, v_cache, slot_indices, paged: bool = False,
+                    rope_cos=None, rope_sin=None, start_pos=0) -> None:
     """Write k, v (B, Hkv, T, D) into k_cache, v_cache (B, Hkv, S_cache, D) at
     slot_indices (B, T); in place, on the caches' stream.  With ``paged`` the
     caches are page pools (num_pages, Hkv, page_size, D) and a slot s is row
-    ``s % page_size`` of page ``s // page_size``."""
+    ``s % page_size`` of page ``s // page_size``.  With ``rope_cos`` /
+    ``rope_sin`` ((max_seq_len, D) tables) new token t of row b is rotated to
+    position ``start_pos + t`` (``start_pos``: int, or integer (B,) per row)
+    before it is written."""
     b, h, t, s, d = validate_cache_update(k, v, k_cache, v_cache, slot_indices, paged)
     dev = check_device(k, v, k_cache, v_cache)
     slots = slot_indices.to(device=dev, dtype=torch.int64).contiguous()
+    rope = rope_args(rope_cos, rope_sin, start_pos, b, d, dev)
     lib = _lib.load()
     sts = (_lib.strides3(k), _lib.strides3(v), _lib.strides3(k_cache), _lib.strides3(v_cache))
     with torch.cuda.device(dev):
-        if paged:
+        if rope is not None and paged:
+            rc = lib.sk_kv_cache_update_paged_rope(
+                _lib.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
+                v_cache.data_ptr(), slots.data_ptr(), b, h, t, k_cache.shape[0],
+                k_cache.shape[2], d, *sts, *rope.args, stream_of(dev))
+        elif rope is not None:
+            rc = lib.sk_kv_cache_update_rope(
+                _lib.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
+                v_cache.data_ptr(), slots.data_ptr(), b, h, t, s, d, *sts, *rope.args,
+                stream_of(dev))
+        elif paged:
             rc = lib.sk_kv_cache_update_paged(
                 _lib.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
                 v_cache.data_ptr(), slots.data_ptr(), b, h, t, k_cache.shape[0],

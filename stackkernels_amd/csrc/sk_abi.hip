@@ -112,6 +112,40 @@ size_t decode_ws_bytes(int dtype, int B, int Hq, int D, int splits) {
   return (size_t)B * Hq * splits * (dpad + 1) * sizeof(float);
 }
 
+// RoPE arguments of the *_rope entry points -> r.  `tokens` is the number of
+// consecutive positions each batch row uses from its base (1 for decode, T
+// for the cache append, Sq for the forward).  With one base for the whole
+// batch (rope_pos NULL) the positions [rope_start, rope_start + tokens) must
+// lie in the table, as the reference's table slice
+// cos[start_pos : start_pos + seq_len] requires
+// (src/stackkernels/_reference/torch/rope.py:49-50).
+int make_rope(const void* cos, const void* sin, int rope_dtype, int rope_rows,
+              int64_t rope_stride, const int32_t* rope_pos, int rope_start, int D, int tokens,
+              sk::RopeParams* r) {
+  if (!cos || !sin) return fail(SK_EINVAL, "rope cos/sin pointer is NULL");
+  if (rope_dtype != SK_F32 && rope_dtype != SK_F16 && rope_dtype != SK_BF16)
+    return fail(SK_EUNSUPPORTED, "unsupported rope table dtype code %d", rope_dtype);
+  if (D % 16 != 0)
+    return fail(SK_EUNSUPPORTED, "RoPE needs a head dim that is a multiple of 16, got %d", D);
+  if (rope_rows <= 0 || rope_stride < D)
+    return fail(SK_EINVAL, "rope table of %d rows with row stride %lld for head dim %d", rope_rows,
+                (long long)rope_stride, D);
+  const uintptr_t esz = (uintptr_t)elem_bytes(rope_dtype);
+  if (((uintptr_t)cos | (uintptr_t)sin) % esz != 0)
+    return fail(SK_EINVAL, "rope table pointers are not element-aligned");
+  if (!rope_pos && tokens > 0 &&
+      (rope_start < 0 || (int64_t)rope_start + tokens > (int64_t)rope_rows))
+    return fail(SK_EINVAL, "positions [%d, %lld) lie outside the rope table of %d rows", rope_start,
+                (long long)rope_start + tokens, rope_rows);
+  r->cos = cos, r->sin = sin;
+  r->stride = rope_stride;
+  r->rows = rope_rows;
+  r->dtype = rope_dtype;
+  r->pos_b = rope_pos;
+  r->start = rope_start;
+  return SK_OK;
+}
+
 size_t bwd_ws_bytes(int B, int Hq, int Sq) {
   const size_t rows = (size_t)B * Hq * Sq;
   return 2 * ((rows * sizeof(float) + 255) / 256 * 256);
@@ -125,11 +159,14 @@ int sk_abi_version(void) { return SK_ABI_VERSION; }
 
 const char* sk_last_error(void) { return g_err; }
 
-int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-                int B, int Hq, int Hkv, int Sq, int Sk, int D, const int64_t* q_strides,
-                const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
-                int is_causal, float sm_scale, void* stream) {
-  g_err[0] = 0;
+}  // extern "C"
+
+// sk_attn_fwd and sk_attn_fwd_rope.
+static int fwd_impl(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                    int B, int Hq, int Hkv, int Sq, int Sk, int D, const int64_t* q_strides,
+                    const int64_t* k_strides, const int64_t* v_strides,
+                    const int64_t* o_strides, int is_causal, const sk::RopeParams& rope,
+                    float sm_scale, void* stream) {
   int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
   if (rc) return rc;
   if ((rc = check_strides(dtype, "q", q_strides)) || (rc = check_strides(dtype, "k", k_strides)) ||
@@ -163,6 +200,7 @@ int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
   p.pair_items = dtype != SK_F32 && is_causal && p.n_mblocks >= 2 &&
                  (int64_t)((p.n_mblocks + 1) / 2) * B * Hq >= 512;
   p.n_items = p.pair_items ? (p.n_mblocks + 1) / 2 : p.n_mblocks;
+  p.rope = rope;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == SK_F32) {
@@ -174,6 +212,32 @@ int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
   }
   if (e != hipSuccess) return hip_fail(e, "sk_attn_fwd launch");
   return SK_OK;
+}
+
+extern "C" {
+
+int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                int B, int Hq, int Hkv, int Sq, int Sk, int D, const int64_t* q_strides,
+                const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                int is_causal, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  return fwd_impl(dtype, q, k, v, o, lse, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides,
+                  o_strides, is_causal, sk::RopeParams{}, sm_scale, stream);
+}
+
+int sk_attn_fwd_rope(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                     int B, int Hq, int Hkv, int Sq, int Sk, int D, const int64_t* q_strides,
+                     const int64_t* k_strides, const int64_t* v_strides,
+                     const int64_t* o_strides, int is_causal, const void* rope_cos,
+                     const void* rope_sin, int rope_dtype, int rope_rows, int64_t rope_stride,
+                     const int32_t* rope_pos, int rope_start, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  sk::RopeParams r{};
+  const int rc = make_rope(rope_cos, rope_sin, rope_dtype, rope_rows, rope_stride, rope_pos,
+                           rope_start, D, (int64_t)B * Hq > 0 ? Sq : 0, &r);
+  if (rc) return rc;
+  return fwd_impl(dtype, q, k, v, o, lse, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides,
+                  o_strides, is_causal, r, sm_scale, stream);
 }
 
 int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
@@ -267,6 +331,23 @@ struct PagedCache {
   int page_size = 0, max_pages = 0, num_pages = 0;
 };
 
+// Paged-pool arguments of sk_decode_paged / sk_decode_paged_rope -> pc.
+static int paged_args(int B, int num_pages, int page_size, int max_pages,
+                      const int32_t* block_table, const int32_t* cache_seqlens, PagedCache* pc) {
+  if (page_size <= 0 || page_size % 32 != 0)
+    return fail(SK_EINVAL, "page_size=%d must be a positive multiple of 32", page_size);
+  if (num_pages < 0 || max_pages < 0)
+    return fail(SK_EINVAL, "invalid num_pages=%d max_pages=%d", num_pages, max_pages);
+  if ((int64_t)max_pages * page_size > 0x7fffffffLL)
+    return fail(SK_EINVAL, "max_pages * page_size overflows int");
+  if (B > 0 && max_pages > 0 && (!block_table || !cache_seqlens))
+    return fail(SK_EINVAL, "block_table and cache_seqlens are required");
+  if (max_pages > 0 && num_pages == 0) return fail(SK_EINVAL, "empty page pool");
+  pc->block_table = block_table;
+  pc->page_size = page_size, pc->max_pages = max_pages, pc->num_pages = num_pages;
+  return SK_OK;
+}
+
 // sk_decode, sk_decode_varlen and sk_decode_paged: seqlens is null (every row
 // sees all Sk keys) or a device array of B per-row key counts; pc describes a
 // paged cache (then Sk = max_pages * page_size).
@@ -274,9 +355,8 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
                        void* workspace, size_t workspace_bytes, int num_splits, int B, int Hq,
                        int Hkv, int Sk, int D, const int64_t* q_strides, const int64_t* k_strides,
                        const int64_t* v_strides, const int64_t* o_strides,
-                       const int32_t* seqlens, const PagedCache& pc, float sm_scale,
-                       void* stream) {
-  g_err[0] = 0;
+                       const int32_t* seqlens, const PagedCache& pc,
+                       const sk::RopeParams& rope, float sm_scale, void* stream) {
   int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
   if (rc) return rc;
   if ((rc = check_strides(dtype, "q", q_strides)) || (rc = check_strides(dtype, "k", k_strides)) ||
@@ -317,6 +397,7 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
     p.seqlens = seqlens;
     p.block_table = pc.block_table;
     p.page_size = pc.page_size, p.max_pages = pc.max_pages, p.num_pages = pc.num_pages;
+    p.rope = rope;
     hipError_t e = sk::launch_fwd_f32(p, false, s);
     if (e != hipSuccess) return hip_fail(e, "sk_decode launch");
     return SK_OK;
@@ -338,6 +419,7 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
   p.seqlens = seqlens;
   p.block_table = pc.block_table;
   p.page_size = pc.page_size, p.max_pages = pc.max_pages, p.num_pages = pc.num_pages;
+  p.rope = rope;
   if (num_splits > 1) {
     p.part_o = (float*)workspace;
     p.part_lse = p.part_o + (size_t)B * Hq * num_splits * p.dpad;
@@ -357,9 +439,10 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
               size_t workspace_bytes, int num_splits, int B, int Hq, int Hkv, int Sk, int D,
               const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
               const int64_t* o_strides, float sm_scale, void* stream) {
+  g_err[0] = 0;
   return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
-                     q_strides, k_strides, v_strides, o_strides, nullptr, PagedCache{}, sm_scale,
-                     stream);
+                     q_strides, k_strides, v_strides, o_strides, nullptr, PagedCache{},
+                     sk::RopeParams{}, sm_scale, stream);
 }
 
 }  // extern "C"
@@ -370,7 +453,8 @@ static int cache_update_impl(int dtype, const void* k, const void* v, void* k_ca
                              void* v_cache, const int64_t* slots, int B, int Hkv, int T,
                              int64_t S_cache, int page_size, int D, const int64_t* k_strides,
                              const int64_t* v_strides, const int64_t* kc_strides,
-                             const int64_t* vc_strides, void* stream) {
+                             const int64_t* vc_strides, const sk::RopeParams& rope,
+                             void* stream) {
   if (dtype != SK_F32 && dtype != SK_F16 && dtype != SK_BF16)
     return fail(SK_EUNSUPPORTED, "unsupported dtype code %d", dtype);
   if (B < 0 || Hkv <= 0 || T < 0 || S_cache < 0 || D <= 0)
@@ -400,6 +484,20 @@ static int cache_update_impl(int dtype, const void* k, const void* v, void* k_ca
   p.page_size = page_size;
   p.esize = elem_bytes(dtype);
   p.row_bytes = D * p.esize;
+  p.dtype = dtype;
+  p.D = D;
+  p.rope = rope;
+  if (rope.cos) {
+    // The rotating kernel moves aligned 16-byte chunks.
+    const void* rp[4] = {k, v, k_cache, v_cache};
+    for (int i = 0; i < 4; ++i)
+      if (!aligned16(rp[i])) return fail(SK_EINVAL, "%s pointer is not 16-byte aligned", names[i]);
+    for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 3; ++j)
+        if ((sts[i][j] * p.esize) % 16 != 0)
+          return fail(SK_EINVAL, "%s stride[%d]=%lld is not a multiple of 16 bytes", names[i], j,
+                      (long long)sts[i][j]);
+  }
   hipError_t e = sk::launch_kv_cache_update(p, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sk_kv_cache_update launch");
   return SK_OK;
@@ -413,7 +511,8 @@ int sk_kv_cache_update(int dtype, const void* k, const void* v, void* k_cache, v
                        const int64_t* kc_strides, const int64_t* vc_strides, void* stream) {
   g_err[0] = 0;
   return cache_update_impl(dtype, k, v, k_cache, v_cache, slots, B, Hkv, T, S_cache, 0, D,
-                           k_strides, v_strides, kc_strides, vc_strides, stream);
+                           k_strides, v_strides, kc_strides, vc_strides, sk::RopeParams{},
+                           stream);
 }
 
 int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, void* k_pool,
@@ -426,7 +525,7 @@ int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, void* k_po
     return fail(SK_EINVAL, "invalid page_size=%d num_pages=%d", page_size, num_pages);
   return cache_update_impl(dtype, k, v, k_pool, v_pool, slot_mapping, B, Hkv, T,
                            (int64_t)num_pages * page_size, page_size, D, k_strides, v_strides,
-                           kp_strides, vp_strides, stream);
+                           kp_strides, vp_strides, sk::RopeParams{}, stream);
 }
 
 int sk_decode_varlen(int dtype, const void* q, const void* k, const void* v, void* o,
@@ -438,7 +537,7 @@ int sk_decode_varlen(int dtype, const void* q, const void* k, const void* v, voi
   if (B > 0 && !cache_seqlens) return fail(SK_EINVAL, "cache_seqlens is null");
   return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
                      q_strides, k_strides, v_strides, o_strides, cache_seqlens, PagedCache{},
-                     sm_scale, stream);
+                     sk::RopeParams{}, sm_scale, stream);
 }
 
 int sk_decode_paged(int dtype, const void* q, const void* k_pool, const void* v_pool, void* o,
@@ -449,22 +548,87 @@ int sk_decode_paged(int dtype, const void* q, const void* k_pool, const void* v_
                     const int32_t* block_table, const int32_t* cache_seqlens, float sm_scale,
                     void* stream) {
   g_err[0] = 0;
-  if (page_size <= 0 || page_size % 32 != 0)
-    return fail(SK_EINVAL, "page_size=%d must be a positive multiple of 32", page_size);
-  if (num_pages < 0 || max_pages < 0)
-    return fail(SK_EINVAL, "invalid num_pages=%d max_pages=%d", num_pages, max_pages);
-  if ((int64_t)max_pages * page_size > 0x7fffffffLL)
-    return fail(SK_EINVAL, "max_pages * page_size overflows int");
-  if (B > 0 && max_pages > 0 && (!block_table || !cache_seqlens))
-    return fail(SK_EINVAL, "block_table and cache_seqlens are required");
   PagedCache pc;
-  pc.block_table = block_table;
-  pc.page_size = page_size, pc.max_pages = max_pages, pc.num_pages = num_pages;
-  const int sk = max_pages * page_size;
-  if (sk > 0 && num_pages == 0) return fail(SK_EINVAL, "empty page pool");
+  const int rc = paged_args(B, num_pages, page_size, max_pages, block_table, cache_seqlens, &pc);
+  if (rc) return rc;
   return decode_impl(dtype, q, k_pool, v_pool, o, workspace, workspace_bytes, num_splits, B, Hq,
-                     Hkv, sk, D, q_strides, kp_strides, vp_strides, o_strides, cache_seqlens, pc,
+                     Hkv, max_pages * page_size, D, q_strides, kp_strides, vp_strides, o_strides,
+                     cache_seqlens, pc, sk::RopeParams{}, sm_scale, stream);
+}
+
+int sk_decode_rope(int dtype, const void* q, const void* k, const void* v, void* o,
+                   void* workspace, size_t workspace_bytes, int num_splits, int B, int Hq,
+                   int Hkv, int Sk, int D, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* o_strides,
+                   const int32_t* cache_seqlens, const void* rope_cos, const void* rope_sin,
+                   int rope_dtype, int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                   int rope_start, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  sk::RopeParams r{};
+  const int rc = make_rope(rope_cos, rope_sin, rope_dtype, rope_rows, rope_stride, rope_pos,
+                           rope_start, D, B > 0 ? 1 : 0, &r);
+  if (rc) return rc;
+  return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
+                     q_strides, k_strides, v_strides, o_strides, cache_seqlens, PagedCache{}, r,
                      sm_scale, stream);
+}
+
+int sk_decode_paged_rope(int dtype, const void* q, const void* k_pool, const void* v_pool,
+                         void* o, void* workspace, size_t workspace_bytes, int num_splits, int B,
+                         int Hq, int Hkv, int num_pages, int page_size, int max_pages, int D,
+                         const int64_t* q_strides, const int64_t* kp_strides,
+                         const int64_t* vp_strides, const int64_t* o_strides,
+                         const int32_t* block_table, const int32_t* cache_seqlens,
+                         const void* rope_cos, const void* rope_sin, int rope_dtype,
+                         int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                         int rope_start, float sm_scale, void* stream) {
+  g_err[0] = 0;
+  PagedCache pc;
+  int rc = paged_args(B, num_pages, page_size, max_pages, block_table, cache_seqlens, &pc);
+  if (rc) return rc;
+  sk::RopeParams r{};
+  rc = make_rope(rope_cos, rope_sin, rope_dtype, rope_rows, rope_stride, rope_pos, rope_start, D,
+                 B > 0 ? 1 : 0, &r);
+  if (rc) return rc;
+  return decode_impl(dtype, q, k_pool, v_pool, o, workspace, workspace_bytes, num_splits, B, Hq,
+                     Hkv, max_pages * page_size, D, q_strides, kp_strides, vp_strides, o_strides,
+                     cache_seqlens, pc, r, sm_scale, stream);
+}
+
+int sk_kv_cache_update_rope(int dtype, const void* k, const void* v, void* k_cache, void* v_cache,
+                            const int64_t* slots, int B, int Hkv, int T, int S_cache, int D,
+                            const int64_t* k_strides, const int64_t* v_strides,
+                            const int64_t* kc_strides, const int64_t* vc_strides,
+                            const void* rope_cos, const void* rope_sin, int rope_dtype,
+                            int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                            int rope_start, void* stream) {
+  g_err[0] = 0;
+  sk::RopeParams r{};
+  const int rc = make_rope(rope_cos, rope_sin, rope_dtype, rope_rows, rope_stride, rope_pos,
+                           rope_start, D, B > 0 ? T : 0, &r);
+  if (rc) return rc;
+  return cache_update_impl(dtype, k, v, k_cache, v_cache, slots, B, Hkv, T, S_cache, 0, D,
+                           k_strides, v_strides, kc_strides, vc_strides, r, stream);
+}
+
+int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v, void* k_pool,
+                                  void* v_pool, const int64_t* slot_mapping, int B, int Hkv,
+                                  int T, int num_pages, int page_size, int D,
+                                  const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* kp_strides, const int64_t* vp_strides,
+                                  const void* rope_cos, const void* rope_sin, int rope_dtype,
+                                  int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
+                                  int rope_start, void* stream) {
+  g_err[0] = 0;
+  if (page_size <= 0 || num_pages < 0)
+    return fail(SK_EINVAL, "invalid page_size=%d num_pages=%d", page_size, num_pages);
+  sk::RopeParams r{};
+  const int rc = make_rope(rope_cos, rope_sin, rope_dtype, rope_rows, rope_stride, rope_pos,
+                           rope_start, D, B > 0 ? T : 0, &r);
+  if (rc) return rc;
+  return cache_update_impl(dtype, k, v, k_pool, v_pool, slot_mapping, B, Hkv, T,
+                           (int64_t)num_pages * page_size, page_size, D, k_strides, v_strides,
+                           kp_strides, vp_strides, r, stream);
 }
 
 }  // extern "C"

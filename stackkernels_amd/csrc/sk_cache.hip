@@ -12,8 +12,14 @@
 // A slot outside [0, S) skips the token, which lets callers pad ragged
 // batches with -1.  Plain byte copies: the cache holds exactly the input's
 // bits.
+//
+// With RoPE tables the keys are rotated on their way into the cache (the
+// reference's apply_rope on k followed by the append, in one pass over the
+// new rows): one thread then moves an aligned 16-byte chunk of a K row, which
+// it rotates with the chunk half a head away, and the same chunk of V.
 #include "sk_common.h"
 #include "sk_kernels.h"
+#include "sk_rope.h"
 
 namespace sk {
 
@@ -65,6 +71,55 @@ __global__ void __launch_bounds__(256) kv_cache_update_kernel(CacheParams p) {
   *reinterpret_cast<U*>(vd) = vx;
 }
 
+// Rotating append.  Thread i moves 16-byte chunk c of row r = (b, h, t).
+// T: BF16 / F16 (8 elements per chunk) or float (4).
+template <class T>
+__global__ void __launch_bounds__(256) kv_cache_update_rope_kernel(CacheParams p) {
+  constexpr bool kF32 = __is_same(T, float);
+  constexpr int EPC = kF32 ? 4 : 8;  // elements per 16-byte chunk
+  const int chunks = p.D / EPC;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t rows = (int64_t)p.B * p.Hkv * p.T;
+  if (i >= rows * chunks) return;
+  const int64_t r = i / chunks;
+  const int c = (int)(i - r * chunks);
+  const int t = (int)(r % p.T);
+  const int64_t bh = r / p.T;
+  const int h = (int)(bh % p.Hkv);
+  const int b = (int)(bh / p.Hkv);
+  const int64_t slot = p.slots[(int64_t)b * p.T + t];
+  if (slot < 0 || slot >= p.S) return;
+  const int64_t unit = p.page_size > 0 ? slot / p.page_size : b;
+  const int64_t row = p.page_size > 0 ? slot % p.page_size : slot;
+  const int d0 = c * EPC;
+  const int half = p.D >> 1;
+  const int dp = d0 < half ? d0 + half : d0 - half;  // partner chunk (same half-offset)
+  const int rrow = rope_row(p.rope, b, t);
+  using E = typename std::conditional<kF32, float, uint16_t>::type;
+  const E* ks = (const E*)p.k + b * p.k_sb + h * p.k_sh + t * p.k_ss;
+  const E* vs = (const E*)p.v + b * p.v_sb + h * p.v_sh + t * p.v_ss;
+  E* kd = (E*)p.kc + unit * p.kc_sb + h * p.kc_sh + row * p.kc_ss;
+  E* vd = (E*)p.vc + unit * p.vc_sb + h * p.vc_sh + row * p.vc_ss;
+  const u32x4 vx = *reinterpret_cast<const u32x4*>(vs + d0);
+  u32x4 kx = *reinterpret_cast<const u32x4*>(ks + d0);
+  if (rrow >= 0) {
+    const u32x4 kp = *reinterpret_cast<const u32x4*>(ks + dp);
+    if constexpr (kF32) {
+      const int64_t e = (int64_t)rrow * p.rope.stride + d0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        kx[j] = __builtin_bit_cast(
+            uint32_t, rope_mix(__builtin_bit_cast(float, kx[j]), __builtin_bit_cast(float, kp[j]),
+                               d0 < half, rope_entry(p.rope, p.rope.cos, e + j),
+                               rope_entry(p.rope, p.rope.sin, e + j)));
+    } else {
+      kx = rope8<T>(kx, kp, d0, half, p.rope, rrow);
+    }
+  }
+  *reinterpret_cast<u32x4*>(kd + d0) = kx;
+  *reinterpret_cast<u32x4*>(vd + d0) = vx;
+}
+
 // Largest copy unit (16, 8, 4 or 2 bytes) that divides the row and every
 // byte address and stride involved.
 static int copy_unit(const CacheParams& p) {
@@ -81,6 +136,22 @@ static int copy_unit(const CacheParams& p) {
 
 hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s) {
   const int unit = copy_unit(p);
+  if (p.rope.cos) {
+    // Rotating path: 16-byte chunks; D / 2 a multiple of the chunk.
+    const int epc = 16 / p.esize;
+    if (unit < 16 || p.D % (2 * epc) != 0) return hipErrorInvalidValue;
+    const int64_t threads = (int64_t)p.B * p.Hkv * p.T * (p.D / epc);
+    if (threads == 0) return hipSuccess;
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)blocks);
+    switch (p.dtype) {
+      case 0: hipLaunchKernelGGL(kv_cache_update_rope_kernel<float>, grid, dim3(256), 0, s, p); break;
+      case 1: hipLaunchKernelGGL(kv_cache_update_rope_kernel<F16>, grid, dim3(256), 0, s, p); break;
+      default: hipLaunchKernelGGL(kv_cache_update_rope_kernel<BF16>, grid, dim3(256), 0, s, p); break;
+    }
+    return hipGetLastError();
+  }
   if (unit < 2) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)p.B * p.Hkv * p.T * (p.row_bytes / unit);
   if (threads == 0) return hipSuccess;

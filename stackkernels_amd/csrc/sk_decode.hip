@@ -21,6 +21,7 @@
 //   normalised partials.  With one split the kernel writes O directly.
 #include "sk_common.h"
 #include "sk_kernels.h"
+#include "sk_rope.h"
 
 namespace sk {
 
@@ -55,6 +56,30 @@ __device__ __forceinline__ TileRows tile_rows(const DecParams& p, const uint16_t
   const int64_t off = n0 % p.page_size;
   return {(const uint16_t*)p.k + pg * p.k_sb + (int64_t)hkv * p.k_sh + off * p.k_ss,
           (const uint16_t*)p.v + pg * p.v_sb + (int64_t)hkv * p.v_sh + off * p.v_ss, ok};
+}
+
+// Q^T operand: lane holds q[hq][32*s + 8*g .. +7] (zeros past D and for
+// lanes without a head), rotated when the call carries RoPE tables and
+// sign-flipped when sm_scale < 0 (the rotation is linear, so the order of the
+// two does not matter).
+template <class T, int KD>
+__device__ __forceinline__ void load_q(const DecParams& p, int b, int hq, bool head_ok, int g,
+                                       u32x4 (&qreg)[KD]) {
+  const uint16_t* qp = (const uint16_t*)p.q + b * p.q_sb + hq * p.q_sh;
+  const int row = rope_row(p.rope, b, 0);
+  const int half = p.D >> 1;
+#pragma unroll
+  for (int s = 0; s < KD; ++s) {
+    const int d0 = 32 * s + 8 * g;
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (head_ok && d0 < p.D) {
+      x = ldg_b128_cached(qp + d0);
+      if (row >= 0)
+        x = rope8<T>(x, ldg_b128_cached(qp + (d0 < half ? d0 + half : d0 - half)), d0, half,
+                     p.rope, row);
+    }
+    qreg[s] = x ^ p.q_sign;
+  }
 }
 
 template <class T, int DP, int NWH, bool PAGED>
@@ -98,18 +123,8 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   const uint16_t* kbase = (const uint16_t*)p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = (const uint16_t*)p.v + b * p.v_sb + hkv * p.v_sh;
 
-  // Q^T operand: lane holds q[hq][32*s + 8*g .. +7].
   u32x4 qreg[KD];
-  {
-    const uint16_t* qp = (const uint16_t*)p.q + b * p.q_sb + hq * p.q_sh;
-#pragma unroll
-    for (int s = 0; s < KD; ++s) {
-      const int d0 = 32 * s + 8 * g;
-      u32x4 x = {0u, 0u, 0u, 0u};
-      if (head_ok && d0 < p.D) x = ldg_b128_cached(qp + d0);
-      qreg[s] = x ^ p.q_sign;
-    }
-  }
+  load_q<T>(p, b, hq, head_ok, g, qreg);
 
   u32x4 kreg[LOADS], vreg[LOADS];
   auto load_tile = [&](int t) {
@@ -292,18 +307,8 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
   const uint16_t* kbase = (const uint16_t*)p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = (const uint16_t*)p.v + b * p.v_sb + hkv * p.v_sh;
 
-  // Q^T operand: lane holds q[hq][32*s + 8*g .. +7].
   u32x4 qreg[KD];
-  {
-    const uint16_t* qp = (const uint16_t*)p.q + b * p.q_sb + hq * p.q_sh;
-#pragma unroll
-    for (int s = 0; s < KD; ++s) {
-      const int d0 = 32 * s + 8 * g;
-      u32x4 x = {0u, 0u, 0u, 0u};
-      if (head_ok && d0 < p.D) x = ldg_b128_cached(qp + d0);
-      qreg[s] = x ^ p.q_sign;
-    }
-  }
+  load_q<T>(p, b, hq, head_ok, g, qreg);
 
   // Per-lane byte offsets of this wave's load segments (tile-relative).
   uint32_t koff[LW], voff[LW];

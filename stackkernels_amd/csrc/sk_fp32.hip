@@ -9,6 +9,7 @@
 // tile.
 #include "sk_common.h"
 #include "sk_kernels.h"
+#include "sk_rope.h"
 
 namespace sk {
 
@@ -46,11 +47,16 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
   const float* vbase = (const float*)p.v + b * p.v_sb + hkv * p.v_sh;
   const float sgn = p.q_sign ? -1.f : 1.f;
 
+  // q, rotated when the call carries RoPE tables (query row i is token i).
+  const int rrow = row_ok ? rope_row(p.rope, b, row) : -1;
+  const int half = p.D >> 1;
   float q[DC], acc[DC];
 #pragma unroll
   for (int i = 0; i < DC; ++i) {
     const int d = part * DC + i;
-    q[i] = (row_ok && d < p.D) ? qp[d] * sgn : 0.f;
+    float x = 0.f;
+    if (row_ok && d < p.D) x = rrow >= 0 ? rope1(qp, d, half, p.rope, rrow) : qp[d];
+    q[i] = x * sgn;
     acc[i] = 0.f;
   }
   float m_run = kNegInf, l_run = 0.f;

@@ -51,6 +51,7 @@
 //   workgroup and halves the per-item fixed cost.
 #include "sk_common.h"
 #include "sk_kernels.h"
+#include "sk_rope.h"
 
 namespace sk {
 
@@ -89,7 +90,7 @@ constexpr bool softmax_pairs_fit(int ns, int db, int fl, int ng) {
   return true;
 }
 
-template <class T, int DP, int BN, int NW, int STAGES, int OCC, bool CAUSAL>
+template <class T, int DP, int BN, int NW, int STAGES, int OCC, bool CAUSAL, bool ROPE>
 __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   using L = FwdLds<DP, BN>;
   constexpr int BM = 32 * NW;
@@ -179,8 +180,24 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
     for (int s = 0; s < KD; ++s) {
       const int d0 = 16 * s + 8 * hl;
       const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.q_ss + d0) * 2) : kBufferOob;
-      qreg[s] = buffer_load_b128(qr, off) ^ p.q_sign;
+      qreg[s] = buffer_load_b128(qr, off);
     }
+    if constexpr (ROPE) {
+      // RoPE on load: query row i is token i of its batch row.  Rows past
+      // S_q read zeros and stay zero.
+      const int rrow = rope_row(p.rope, b, row);
+      const int half = p.D >> 1;
+#pragma unroll
+      for (int s = 0; s < KD; ++s) {
+        const int d0 = 16 * s + 8 * hl;
+        const int dq = d0 < half ? d0 + half : d0 - half;
+        const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.q_ss + dq) * 2) : kBufferOob;
+        const u32x4 y = buffer_load_b128(qr, off);
+        if (rrow >= 0 && d0 < p.D) qreg[s] = rope8<T>(qreg[s], y, d0, half, p.rope, rrow);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KD; ++s) qreg[s] ^= p.q_sign;
   }
 
   // Issue cursors of K and V (first key, base pointer).  K and V tiles are
@@ -500,10 +517,15 @@ template <class T, int DP, int BN, int NW, int OCC>
 static hipError_t launch_fwd_t(const FwdParams& p, bool causal, hipStream_t s) {
   const dim3 grid((unsigned)(p.n_items * p.B * p.Hq));
   const dim3 block(NW * 64);
-  if (causal)
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true>), grid, block, 0, s, p);
+  const bool rope = p.rope.cos != nullptr;
+  if (causal && !rope)
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, false>), grid, block, 0, s, p);
+  else if (!rope)
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, false>), grid, block, 0, s, p);
+  else if (causal)
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, true>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, true>), grid, block, 0, s, p);
   return hipGetLastError();
 }
 

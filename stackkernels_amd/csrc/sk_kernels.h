@@ -8,6 +8,25 @@
 
 namespace sk {
 
+// Rotary position embedding (rotate-half form) applied to a vector as it is
+// loaded.  Token t of batch row b sits at position
+// pos = (pos_b ? pos_b[b] : 0) + start + t, and element d of its rotated
+// head vector is
+//   x[d] * cos[pos][d] - x[d + D/2] * sin[pos][d]   for d <  D/2,
+//   x[d] * cos[pos][d] + x[d - D/2] * sin[pos][d]   for d >= D/2,
+// each product and the sum rounded to fp32 (no fused multiply-add), then
+// rounded to the tensor's element type.  A position outside [0, rows) leaves
+// the vector as it is.  cos == nullptr switches the rotation off.
+struct RopeParams {
+  const void* cos;  // (rows, >= D) tables, element stride `stride` between rows
+  const void* sin;
+  int64_t stride;
+  int rows;
+  int dtype;  // SK_F32 / SK_F16 / SK_BF16 element type of both tables
+  const int* pos_b;
+  int start;
+};
+
 // Forward attention, prefill shape.  Strides are element strides.
 struct FwdParams {
   const void* q;
@@ -32,6 +51,8 @@ struct FwdParams {
   // Decode only: null, or a paged cache (see DecParams).
   const int* block_table;
   int page_size, max_pages, num_pages;
+  // Rotation of q on load; query row i of batch row b is token i.
+  RopeParams rope;
 };
 
 // Split-KV decode (Sq == 1).
@@ -59,6 +80,8 @@ struct DecParams {
   // page_size is a multiple of 32; a page index outside the pool masks its keys.
   const int* block_table;
   int page_size, max_pages, num_pages;
+  // Rotation of q on load (the query is token 0 of its batch row).
+  RopeParams rope;
 };
 
 // Backward attention; every tensor contiguous BHSD.
@@ -105,6 +128,11 @@ struct CacheParams {
   int64_t S;      // slots: rows per batch row's cache, or num_pages * page_size
   int esize;      // bytes per element
   int row_bytes;  // D * esize
+  int dtype;      // SK_F32 / SK_F16 / SK_BF16 (used by the rotating kernel)
+  int D;
+  // Rotation of the new keys before they are written (new token t of batch
+  // row b is token t); values are copied unchanged.
+  RopeParams rope;
 };
 
 // Launchers: return hipSuccess or the launch error.  dtype is SK_F32/F16/BF16.

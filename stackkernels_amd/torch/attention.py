@@ -25,6 +25,7 @@ from stackkernels_amd._reference.torch.attention import (
     attention_reference,
     attention_reference_backward,
 )
+from stackkernels_amd._reference.torch.rope import apply_rope_at, rope_positions
 from stackkernels_amd.torch._dispatch import should_use_hip
 from stackkernels_amd.torch._utils import ensure_contiguous
 
@@ -83,6 +84,10 @@ def flash_attention(
     v: torch.Tensor,
     is_causal: bool = False,
     sm_scale: float | None = None,
+    *,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    start_pos: int | torch.Tensor = 0,
 ) -> torch.Tensor:
     """Flash Attention forward (differentiable).
 
@@ -94,11 +99,42 @@ def flash_attention(
         q: (B, H_q, S_q, D).  k, v: (B, H_kv, S_k, D).
         is_causal: apply the bottom-right causal mask.
         sm_scale: score scale, default 1/sqrt(D).
+        rope_cos, rope_sin: optional (max_seq_len, D) RoPE tables
+            (``precompute_freqs``).  q is then rotated as the reference's
+            ``apply_rope(q, cos=..., sin=..., start_pos=...)`` would, inside the
+            kernel's prologue: query row i at position ``start_pos + i``.  k is
+            taken as already rotated (as ``kv_cache_update`` with the same tables
+            stores it).  Inference only: raises if a gradient would be needed.
+            Not in the reference, which rotates in a separate pass.
+        start_pos: int, or integer (B,) tensor of per-row positions.
 
     Returns:
         (B, H_q, S_q, D) in q's dtype.
     """
-    return FlashAttentionFunction.apply(q, k, v, is_causal, sm_scale)
+    if rope_cos is None and rope_sin is None:
+        return FlashAttentionFunction.apply(q, k, v, is_causal, sm_scale)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise NotImplementedError(
+            "flash_attention with fused RoPE is forward-only; rotate q first to train")
+    if should_use_hip(q):
+        out, _ = flash_attn_fwd(ensure_contiguous(q), ensure_contiguous(k), ensure_contiguous(v),
+                                is_causal=is_causal, sm_scale=sm_scale, rope_cos=rope_cos,
+                                rope_sin=rope_sin, start_pos=start_pos)
+        return out
+    qr = _rope_reference(q, rope_cos, rope_sin, start_pos)
+    out, _ = attention_reference(qr, k, v, is_causal=is_causal, sm_scale=sm_scale)
+    return out
+
+
+def _rope_reference(x, cos, sin, start_pos):
+    """CPU path of the fused rotation: token t of row b at start_pos(+[b]) + t."""
+    if cos is None or sin is None:
+        raise ValueError("RoPE needs both cos and sin tables")
+    if cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] != x.shape[-1]:
+        raise ValueError(f"RoPE tables must be (max_seq_len, {x.shape[-1]}), got "
+                         f"{tuple(cos.shape)} and {tuple(sin.shape)}")
+    pos = rope_positions(start_pos, x.shape[0], x.shape[2], cos.shape[0])
+    return apply_rope_at(x, cos, sin, pos)
 
 
 def flash_decode(
@@ -108,6 +144,10 @@ def flash_decode(
     sm_scale: float | None = None,
     cache_seqlens: torch.Tensor | None = None,
     block_table: torch.Tensor | None = None,
+    *,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    start_pos: int | torch.Tensor = 0,
 ) -> torch.Tensor:
     """Split-KV decode for one query token (S_q = 1) over the whole cache.
 
@@ -122,18 +162,32 @@ def flash_decode(
             k, v are page pools (num_pages, H_kv, page_size, D), page_size a
             multiple of 32, key j of row b is row ``j % page_size`` of page
             ``block_table[b, j // page_size]``, and cache_seqlens is required.
+        rope_cos, rope_sin: optional (max_seq_len, D) RoPE tables; q is then
+            rotated to position ``start_pos`` inside the decode kernel (the
+            reference's ``apply_rope`` on q, fused).  The cache holds rotated
+            keys (``kv_cache_update`` with the same tables writes them so).
+        start_pos: int, or integer (B,) tensor: each row's query position
+            (typically ``cache_seqlens - 1``).
 
     Returns:
         (B, H_q, 1, D) in q's dtype.
     """
+    rope = {}
+    if rope_cos is not None or rope_sin is not None:
+        rope = dict(rope_cos=rope_cos, rope_sin=rope_sin, start_pos=start_pos)
     if block_table is not None:
         if cache_seqlens is None:
             raise ValueError("a paged decode (block_table) needs cache_seqlens")
         if should_use_hip(q):
-            return core_flash_decode_paged(q, k, v, block_table, cache_seqlens, sm_scale=sm_scale)
+            return core_flash_decode_paged(q, k, v, block_table, cache_seqlens, sm_scale=sm_scale,
+                                           **rope)
+        if rope:
+            q = _rope_reference(q, rope_cos, rope_sin, start_pos)
         return _decode_paged_reference(q, k, v, sm_scale, cache_seqlens, block_table)
     elif should_use_hip(q):
-        return core_flash_decode(q, k, v, sm_scale=sm_scale, cache_seqlens=cache_seqlens)
+        return core_flash_decode(q, k, v, sm_scale=sm_scale, cache_seqlens=cache_seqlens, **rope)
+    if rope:
+        q = _rope_reference(q, rope_cos, rope_sin, start_pos)
     if cache_seqlens is None:
         out, _ = attention_reference(q, k, v, is_causal=False, sm_scale=sm_scale)
         return out

@@ -22,6 +22,10 @@ def kv_cache_update(
     v_cache: torch.Tensor,
     slot_indices: torch.Tensor,
     paged: bool = False,
+    *,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    start_pos: int | torch.Tensor = 0,
 ) -> None:
     """Insert new key/value rows into the caches in place.
 
@@ -38,11 +42,22 @@ def kv_cache_update(
         paged: the caches are page pools (num_pages, H_kv, page_size, D) shared by
             all rows, and a position s is row ``s % page_size`` of page
             ``s // page_size`` (S_cache = num_pages * page_size).
+        rope_cos, rope_sin: optional (max_seq_len, D) RoPE tables: the new keys are
+            rotated (the reference's ``apply_rope`` on k) as they are written, new
+            token t of row b at position ``start_pos + t``; values are copied as
+            they are.
+        start_pos: int, or integer (B,) tensor of per-row positions of token 0.
     """
+    rope = rope_cos is not None or rope_sin is not None
     if should_use_hip(k_cache):
-        _core_kv_cache_update(k, v, k_cache, v_cache, slot_indices, paged)
+        extra = dict(rope_cos=rope_cos, rope_sin=rope_sin, start_pos=start_pos) if rope else {}
+        _core_kv_cache_update(k, v, k_cache, v_cache, slot_indices, paged, **extra)
         return
     b, _, t, s, _ = validate_cache_update(k, v, k_cache, v_cache, slot_indices, paged)
+    if rope:
+        from stackkernels_amd.torch.attention import _rope_reference
+
+        k = _rope_reference(k, rope_cos, rope_sin, start_pos)
     slots = slot_indices.to("cpu", torch.int64)
     if paged:
         ps = k_cache.shape[2]

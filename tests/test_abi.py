@@ -32,7 +32,9 @@ def test_header_declares_expected_api():
     assert {"sk_abi_version", "sk_last_error", "sk_attn_fwd", "sk_attn_bwd",
             "sk_attn_bwd_workspace", "sk_decode_plan", "sk_decode", "sk_decode_workspace",
             "sk_decode_varlen", "sk_kv_cache_update", "sk_decode_paged",
-            "sk_kv_cache_update_paged"} <= names
+            "sk_kv_cache_update_paged", "sk_attn_fwd_rope", "sk_decode_rope",
+            "sk_decode_paged_rope", "sk_kv_cache_update_rope",
+            "sk_kv_cache_update_paged_rope"} <= names
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -160,3 +162,55 @@ def test_paged_argument_errors(lib):
     assert upd(page_size=0) == _lib.SK_EINVAL
     assert upd(num_pages=-1) == _lib.SK_EINVAL
     assert upd(T=0) == _lib.SK_OK
+
+
+def test_rope_argument_errors(lib):
+    """The RoPE arguments are checked before anything else is launched."""
+    from stackkernels_amd._core.attention import _lib
+
+    st = _st(1024, 512, 64)
+
+    def rope(cos=16, sin=16, dt=0, rows=128, stride=64, pos=None, start=0):
+        return (cos, sin, dt, rows, stride, pos, start)
+
+    def dec(D=64, B=1, **kw):
+        return lib.sk_decode_rope(2, 16, 16, 16, 16, 16, 1 << 20, 1, B, 4, 2, 8, D,
+                                  st, st, st, st, None, *rope(**kw), 0.125, None)
+
+    assert dec(cos=None) == _lib.SK_EINVAL and "cos/sin" in _lib.last_error()
+    assert dec(dt=5) == _lib.SK_EUNSUPPORTED and "table dtype" in _lib.last_error()
+    assert dec(D=72) == _lib.SK_EUNSUPPORTED and "multiple of 16" in _lib.last_error()
+    assert dec(rows=0) == _lib.SK_EINVAL
+    assert dec(stride=32) == _lib.SK_EINVAL and "row stride" in _lib.last_error()
+    assert dec(cos=18) == _lib.SK_EINVAL and "element-aligned" in _lib.last_error()
+    assert dec(start=128) == _lib.SK_EINVAL and "outside the rope table" in _lib.last_error()
+    assert dec(start=-1) == _lib.SK_EINVAL
+    assert dec(B=0) == _lib.SK_OK
+
+    def fwd(Sq=8, **kw):
+        return lib.sk_attn_fwd_rope(2, 16, 16, 16, 16, 16, 1, 4, 2, Sq, 8, 64, st, st, st, st, 1,
+                                    *rope(**kw), 0.125, None)
+
+    # one base for the batch: all of [start, start + S_q) must be in the table
+    assert fwd(start=121) == _lib.SK_EINVAL and "[121, 129)" in _lib.last_error()
+    assert fwd(Sq=0, start=121) == _lib.SK_OK
+
+    def upd(T=3, **kw):
+        return lib.sk_kv_cache_update_rope(2, 16, 16, 16, 16, 16, 1, 2, T, 8, 64, st, st, st, st,
+                                           *rope(**kw), None)
+
+    assert upd(start=126) == _lib.SK_EINVAL and "outside the rope table" in _lib.last_error()
+    assert upd(T=0) == _lib.SK_OK
+
+    def pupd(page_size=32, **kw):
+        return lib.sk_kv_cache_update_paged_rope(2, 16, 16, 16, 16, 16, 1, 2, 3, 4, page_size, 64,
+                                                 st, st, st, st, *rope(**kw), None)
+
+    assert pupd(page_size=0) == _lib.SK_EINVAL
+    assert pupd(sin=None) == _lib.SK_EINVAL
+
+    def pdec(**kw):
+        return lib.sk_decode_paged_rope(2, 16, 16, 16, 16, 16, 1 << 20, 1, 1, 4, 2, 4, 48, 2, 64,
+                                        st, st, st, st, 16, 16, *rope(**kw), 0.125, None)
+
+    assert pdec() == _lib.SK_EINVAL and "multiple of 32" in _lib.last_error()

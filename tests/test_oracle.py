@@ -6,6 +6,7 @@ differences, and invariants chosen so that a dropped term, wrong sign, wrong
 mask alignment or wrong GQA mapping fails at least one of them.
 """
 
+import math
 import os
 
 import numpy as np
@@ -322,3 +323,128 @@ def test_kv_cache_update_paged_matches_loops():
                         ek[s // 8, h, s % 8, d] = k[b, h, t, d]
                         ev[s // 8, h, s % 8, d] = v[b, h, t, d]
     assert np.array_equal(nk, ek) and np.array_equal(nv, ev)
+
+
+# ---------------------------------------------------------------- RoPE pins
+
+def test_rope_tables_entries_closed_form():
+    d, n = 64, 40
+    cos, sin = orc.rope_tables(d, n)
+    assert cos.shape == sin.shape == (n, d)
+    half = d // 2
+    for t in (0, 1, 7, 39):
+        for i in (0, 1, 5, half - 1):
+            ang = t / 10000.0 ** (i / half)
+            assert cos[t, i] == pytest.approx(math.cos(ang), abs=1e-12)
+            assert sin[t, i] == pytest.approx(math.sin(ang), abs=1e-12)
+    np.testing.assert_array_equal(cos[:, :half], cos[:, half:])
+    np.testing.assert_array_equal(sin[:, :half], sin[:, half:])
+    np.testing.assert_array_equal(cos[0], np.ones(d))
+    np.testing.assert_array_equal(sin[0], np.zeros(d))
+
+
+def _rope_complex(x, cos, sin, pos):
+    """The rotation as a complex product (x_d + i x_{d+D/2}) * (cos + i sin), float64."""
+    x = np.asarray(x, dtype=np.float64)
+    half = x.shape[-1] // 2
+    z = x[..., :half] + 1j * x[..., half:]
+    c = np.asarray(cos, dtype=np.float64)[pos][:, None, :, :half]
+    s = np.asarray(sin, dtype=np.float64)[pos][:, None, :, :half]
+    w = z * (c + 1j * s)
+    return np.concatenate([w.real, w.imag], axis=-1)
+
+
+@pytest.mark.parametrize("start_pos", [0, 15, 23, 31, 64])
+def test_rope_rotate_matches_complex_product(start_pos):
+    rng = np.random.default_rng(start_pos)
+    b, h, s, d = 2, 3, 8, 64
+    x = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    cos, sin = orc.rope_tables(d, start_pos + s + 64)
+    pos = orc.rope_positions(start_pos, b, s)
+    got = orc.rope_rotate(x, cos, sin, pos)
+    want = _rope_complex(x, cos, sin, pos)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_rope_rotate_matches_loops_bitwise():
+    rng = np.random.default_rng(1)
+    b, h, s, d = 2, 2, 5, 32
+    x = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    cos, sin = (t.astype(np.float32) for t in orc.rope_tables(d, 16))
+    pos = np.array([[0, 3, 9, 15, 2], [1, 1, 4, 7, 11]])
+    got = orc.rope_rotate(x, cos, sin, pos)
+    half = d // 2
+    for bi in range(b):
+        for hi in range(h):
+            for si in range(s):
+                p = pos[bi, si]
+                for j in range(d):
+                    if j < half:
+                        other = np.float32(-x[bi, hi, si, j + half])
+                    else:
+                        other = x[bi, hi, si, j - half]
+                    a = np.float32(x[bi, hi, si, j] * cos[p, j])
+                    c = np.float32(other * sin[p, j])
+                    assert got[bi, hi, si, j] == np.float32(a + c)
+
+
+def test_rope_rotate_invariants():
+    rng = np.random.default_rng(2)
+    b, h, s, d = 1, 2, 6, 128
+    x = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    cos, sin = orc.rope_tables(d, 200)
+    half = d // 2
+    # position 0 is the identity
+    zero = orc.rope_rotate(x, cos, sin, np.zeros((b, s), dtype=np.int64))
+    np.testing.assert_array_equal(zero, x)
+    # each (d, d + D/2) pair keeps its norm
+    pos = orc.rope_positions(37, b, s)
+    y = orc.rope_rotate(x, cos, sin, pos).astype(np.float64)
+    xn = np.hypot(x[..., :half].astype(np.float64), x[..., half:])
+    yn = np.hypot(y[..., :half], y[..., half:])
+    np.testing.assert_allclose(yn, xn, rtol=1e-5, atol=1e-6)
+    # rotation by p1 then by p2 is rotation by p1 + p2
+    p1 = orc.rope_positions(11, b, s) * 0 + 11
+    p2 = orc.rope_positions(0, b, s) + 50
+    two = orc.rope_rotate(orc.rope_rotate(x, cos, sin, p1), cos, sin, p2)
+    one = orc.rope_rotate(x, cos, sin, p1 + p2)
+    np.testing.assert_allclose(two, one, rtol=0, atol=2e-5)
+
+
+def test_rope_rotate_out_of_table_positions_leave_tokens():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 1, 3, 16)).astype(np.float32)
+    cos, sin = orc.rope_tables(16, 10)
+    pos = np.array([[-1, 4, 10], [9, 12, 0]])
+    y = orc.rope_rotate(x, cos, sin, pos)
+    np.testing.assert_array_equal(y[0, :, 0], x[0, :, 0])
+    np.testing.assert_array_equal(y[0, :, 2], x[0, :, 2])
+    np.testing.assert_array_equal(y[1, :, 1], x[1, :, 1])
+    assert not np.array_equal(y[0, :, 1], x[0, :, 1])
+
+
+def test_planted_rope_sign_slip_is_caught():
+    """A rotation that negates the wrong half fails the complex-product pin."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((1, 1, 4, 32)).astype(np.float32)
+    cos, sin = orc.rope_tables(32, 20)
+    pos = orc.rope_positions(5, 1, 4)
+    half = 16
+    c = cos[pos][:, None]
+    s = sin[pos][:, None]
+    wrong = x * c + np.concatenate([x[..., half:], -x[..., :half]], axis=-1) * s
+    assert np.abs(wrong - _rope_complex(x, cos, sin, pos)).max() > 1e-2
+
+
+def test_round_to_matches_torch_casts():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(4096).astype(np.float32) * 3
+    # exact ties for bf16: low 16 bits 0x8000 with even and odd kept bits
+    ties = (np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x40008000], dtype=np.uint32)
+            .view(np.float32))
+    x = np.concatenate([x, ties, np.array([0.0, -0.0, 1e-40], dtype=np.float32)])
+    t = torch.from_numpy(x)
+    np.testing.assert_array_equal(orc.round_to(x, "bf16"), t.to(torch.bfloat16).float().numpy())
+    np.testing.assert_array_equal(orc.round_to(x, "f16"), t.to(torch.float16).float().numpy())
+    np.testing.assert_array_equal(orc.round_to(x, "f32"), x)

@@ -146,3 +146,93 @@ def test_decode_paged_and_cache_update_paged_reference_path():
     ek, ev = orc.kv_cache_update_paged(_np(k), _np(v), _np(kp), _np(vp), slots.numpy())
     kv_cache_update(k, v, kp, vp, slots, paged=True)
     assert np.array_equal(_np(kp), ek) and np.array_equal(_np(vp), ev)
+
+
+# ------------------------------------------------------- fused RoPE (CPU path)
+
+_NP_DT = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+
+
+def _tables(d, rows, dtype=torch.float32):
+    from stackkernels_amd._reference.torch.rope import precompute_freqs
+
+    return precompute_freqs(d, rows, dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("start_pos", [0, 15, 64])
+def test_rope_reference_matches_oracle_bitwise(dtype, start_pos):
+    from stackkernels_amd._reference.torch.rope import apply_rope_at, rope_positions
+
+    g = torch.Generator().manual_seed(start_pos)
+    x = torch.randn(2, 4, 8, 64, generator=g).to(dtype)
+    cos, sin = _tables(64, start_pos + 8 + 64)
+    pos = rope_positions(start_pos, 2, 8, cos.shape[0])
+    got = apply_rope_at(x, cos, sin, pos).float().numpy()
+    want = orc.round_to(orc.rope_rotate(x.float().numpy(), cos.numpy(), sin.numpy(),
+                                        pos.numpy()), _NP_DT[dtype])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_flash_decode_rope_reference_path():
+    from stackkernels_amd.torch import kv_cache_update
+
+    g = torch.Generator().manual_seed(7)
+    b, hq, hkv, sk, d = 3, 8, 2, 40, 64
+    q = torch.randn(b, hq, 1, d, generator=g)
+    k = torch.randn(b, hkv, sk, d, generator=g)
+    v = torch.randn(b, hkv, sk, d, generator=g)
+    cos, sin = _tables(d, 128)
+    lens = torch.tensor([40, 17, 1])
+    pos = lens - 1
+    out = flash_decode(q, k, v, cache_seqlens=lens, rope_cos=cos, rope_sin=sin, start_pos=pos)
+    qr = orc.rope_rotate(q.numpy(), cos.numpy(), sin.numpy(), pos.numpy()[:, None])
+    want = orc.decode_varlen(qr, k.numpy(), v.numpy(), lens.numpy())
+    np.testing.assert_allclose(out.numpy(), want, rtol=0, atol=1e-5)
+    # scalar start_pos, full cache
+    out = flash_decode(q, k, v, rope_cos=cos, rope_sin=sin, start_pos=39)
+    qr = orc.rope_rotate(q.numpy(), cos.numpy(), sin.numpy(), orc.rope_positions(39, b, 1))
+    np.testing.assert_allclose(out.numpy(), orc.decode(qr, k.numpy(), v.numpy()), rtol=0, atol=1e-5)
+    with pytest.raises(ValueError, match="outside the rope table"):
+        flash_decode(q, k, v, rope_cos=cos, rope_sin=sin, start_pos=128)
+    # paged
+    page = 32
+    pool_k = torch.randn(6, hkv, page, d, generator=g)
+    pool_v = torch.randn(6, hkv, page, d, generator=g)
+    table = torch.tensor([[0, 1], [5, 2], [3, 4]])
+    out = flash_decode(q, pool_k, pool_v, cache_seqlens=lens, block_table=table, rope_cos=cos,
+                       rope_sin=sin, start_pos=pos)
+    qr = orc.rope_rotate(q.numpy(), cos.numpy(), sin.numpy(), pos.numpy()[:, None])
+    want = orc.decode_paged(qr, pool_k.numpy(), pool_v.numpy(), table.numpy(), lens.numpy())
+    np.testing.assert_allclose(out.numpy(), want, rtol=0, atol=1e-5)
+    # rotated append: keys rotated at start_pos + t, values as they are
+    kc = torch.zeros(b, hkv, 16, d)
+    vc = torch.zeros(b, hkv, 16, d)
+    kn = torch.randn(b, hkv, 3, d, generator=g)
+    vn = torch.randn(b, hkv, 3, d, generator=g)
+    slots = torch.tensor([[0, 1, 2], [5, 6, -1], [13, 14, 15]])
+    starts = torch.tensor([0, 5, 13])
+    kv_cache_update(kn, vn, kc, vc, slots, rope_cos=cos, rope_sin=sin, start_pos=starts)
+    kr = orc.rope_rotate(kn.numpy(), cos.numpy(), sin.numpy(),
+                         orc.rope_positions(starts.numpy(), b, 3))
+    wk, wv = orc.kv_cache_update(kr, vn.numpy(), np.zeros(kc.shape, np.float32),
+                                 np.zeros(vc.shape, np.float32), slots.numpy())
+    np.testing.assert_array_equal(kc.numpy(), wk)
+    np.testing.assert_array_equal(vc.numpy(), wv)
+
+
+def test_flash_attention_rope_reference_path():
+    g = torch.Generator().manual_seed(8)
+    b, hq, hkv, sq, sk, d = 2, 4, 2, 6, 10, 32
+    q = torch.randn(b, hq, sq, d, generator=g)
+    k = torch.randn(b, hkv, sk, d, generator=g)
+    v = torch.randn(b, hkv, sk, d, generator=g)
+    cos, sin = _tables(d, 64)
+    out = flash_attention(q, k, v, True, rope_cos=cos, rope_sin=sin, start_pos=4)
+    qr = orc.rope_rotate(q.numpy(), cos.numpy(), sin.numpy(), orc.rope_positions(4, b, sq))
+    want, _ = orc.attention_forward(qr, k.numpy(), v.numpy(), is_causal=True)
+    np.testing.assert_allclose(out.numpy(), want, rtol=0, atol=1e-5)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        flash_attention(q.requires_grad_(True), k, v, True, rope_cos=cos, rope_sin=sin)
+    with pytest.raises(ValueError, match="RoPE tables"):
+        flash_attention(q.detach(), k, v, rope_cos=cos[:, :16], rope_sin=sin[:, :16])

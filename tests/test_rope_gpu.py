@@ -1,0 +1,210 @@
+"""GPU parity of RoPE fused into the attention prologue (C ABI
+``sk_attn_fwd_rope``, ``sk_decode_rope``, ``sk_decode_paged_rope``,
+``sk_kv_cache_update_rope``, ``sk_kv_cache_update_paged_rope``).
+
+The rotation inside a kernel is bit-exact against the oracle's ``rope_rotate``
+rounded to the tensor type, so:
+
+* the rotating cache append must write exactly the oracle's rotated keys and
+  the unrotated values (bit-exact, every dtype and table dtype, contiguous and
+  paged caches, per-row and shared positions, out-of-table positions);
+* a fused decode / forward must equal, bit for bit, the same call without
+  RoPE on the oracle-rotated q (same kernels, same split plan), at small
+  shapes and at the C4 decode shape; and it must be within the decode /
+  forward tolerance (max-abs 1e-4 fp32, 2e-2 fp16/bf16) of the oracle's
+  float64 attention on the rotated q.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import stackkernels_amd
+from stackkernels_amd._reference.torch.rope import precompute_freqs
+from stackkernels_amd.torch import flash_attention, flash_decode, kv_cache_update
+
+from _gpu_util import TOL, assert_close_maxabs, make_qkv, native_loaded, np64
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+NP_DT = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+
+@pytest.fixture(autouse=True)
+def _auto_backend():
+    original = stackkernels_amd.get_backend()
+    stackkernels_amd.set_backend("auto")
+    yield
+    stackkernels_amd.set_backend(original)
+
+
+def _tables(d, rows, table_dtype=torch.float32, device="cuda"):
+    cos, sin = precompute_freqs(d, rows, dtype=table_dtype)
+    return cos.to(device), sin.to(device)
+
+
+def _rotated(x, cos, sin, positions):
+    """Oracle rotation of device tensor x (B, H, S, D) at positions (B, S), as
+    a device tensor of x's dtype."""
+    r = orc.rope_rotate(x.float().cpu().numpy(), cos.float().cpu().numpy(),
+                        sin.float().cpu().numpy(), positions)
+    r = orc.round_to(r, NP_DT[x.dtype])
+    return torch.from_numpy(r).to(x.dtype).to(x.device)
+
+
+# ------------------------------------------------------------ cache append
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("table_dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_kv_cache_update_rope_bitexact(dtype, table_dtype, d):
+    b, h, t, s = 3, 2, 5, 24
+    g = torch.Generator().manual_seed(d)
+    k = torch.randn(b, h, t, d, generator=g).to(dtype).cuda()
+    v = torch.randn(b, h, t, d, generator=g).to(dtype).cuda()
+    kc0 = torch.randn(b, h, s, d, generator=g).to(dtype)
+    vc0 = torch.randn(b, h, s, d, generator=g).to(dtype)
+    kc, vc = kc0.cuda(), vc0.cuda()
+    cos, sin = _tables(d, 40, table_dtype)
+    slots = torch.tensor([[0, 1, 2, 3, 4], [7, -1, 9, 30, 8], [23, 22, 21, 20, 19]])
+    # per-row positions; row 2 runs past the 40-row table (tokens left unrotated)
+    starts = torch.tensor([0, 17, 37], dtype=torch.int32)
+    kv_cache_update(k, v, kc, vc, slots.cuda(), rope_cos=cos, rope_sin=sin,
+                    start_pos=starts.cuda())
+    torch.cuda.synchronize()
+    pos = orc.rope_positions(starts.numpy(), b, t)
+    kr = orc.round_to(orc.rope_rotate(np64(k).astype(np.float32), np64(cos), np64(sin), pos),
+                      NP_DT[dtype])
+    wk, wv = orc.kv_cache_update(kr, np64(v), np64(kc0), np64(vc0), slots.numpy())
+    np.testing.assert_array_equal(np64(kc), wk)
+    np.testing.assert_array_equal(np64(vc), wv)
+    assert native_loaded()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_kv_cache_update_paged_rope_bitexact(dtype):
+    b, h, t, d, page, pages = 2, 4, 3, 128, 32, 5
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(b, h, t, d, generator=g).to(dtype).cuda()
+    v = torch.randn(b, h, t, d, generator=g).to(dtype).cuda()
+    kp0 = torch.randn(pages, h, page, d, generator=g).to(dtype)
+    vp0 = torch.randn(pages, h, page, d, generator=g).to(dtype)
+    kp, vp = kp0.cuda(), vp0.cuda()
+    cos, sin = _tables(d, 64)
+    slots = torch.tensor([[33, 34, 35], [159, -1, 3]])
+    kv_cache_update(k, v, kp, vp, slots.cuda(), paged=True, rope_cos=cos, rope_sin=sin,
+                    start_pos=9)
+    torch.cuda.synchronize()
+    kr = orc.round_to(orc.rope_rotate(np64(k).astype(np.float32), np64(cos), np64(sin),
+                                      orc.rope_positions(9, b, t)), NP_DT[dtype])
+    wk, wv = orc.kv_cache_update_paged(kr, np64(v), np64(kp0), np64(vp0), slots.numpy())
+    np.testing.assert_array_equal(np64(kp), wk)
+    np.testing.assert_array_equal(np64(vp), wv)
+
+
+# ------------------------------------------------------------------ decode
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (32, 1), (64, 2)])
+@pytest.mark.parametrize("d", [64, 96, 128, 256])
+def test_decode_rope_equals_decode_on_rotated_q(dtype, hq, hkv, d):
+    b, sk = 3, 700
+    q, k, v = make_qkv(b, hq, hkv, 1, sk, d, dtype, seed=hq + d)
+    cos, sin = _tables(d, 2048)
+    lens = torch.tensor([700, 333, 1], dtype=torch.int32)
+    pos = (lens - 1).cuda()
+    out = flash_decode(q, k, v, cache_seqlens=lens.cuda(), rope_cos=cos, rope_sin=sin,
+                       start_pos=pos)
+    qr = _rotated(q, cos, sin, (lens - 1).numpy()[:, None])
+    base = flash_decode(qr, k, v, cache_seqlens=lens.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    want = orc.decode_varlen(np64(qr), np64(k), np64(v), lens.numpy())
+    assert_close_maxabs(out, want, TOL[dtype], f"decode rope {dtype} {hq}/{hkv} d={d}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_decode_rope_shared_start_negative_scale_and_half_tables(dtype):
+    b, hq, hkv, sk, d = 2, 16, 4, 512, 128
+    q, k, v = make_qkv(b, hq, hkv, 1, sk, d, dtype, seed=5)
+    cos, sin = _tables(d, 1024, dtype)
+    out = flash_decode(q, k, v, sm_scale=-0.05, rope_cos=cos, rope_sin=sin, start_pos=511)
+    qr = _rotated(q, cos, sin, orc.rope_positions(511, b, 1))
+    base = flash_decode(qr, k, v, sm_scale=-0.05)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    assert_close_maxabs(out, orc.decode(np64(qr), np64(k), np64(v), -0.05), TOL[dtype],
+                        "decode rope negative scale")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_decode_paged_rope_equals_paged_on_rotated_q(dtype):
+    b, hq, hkv, d, page, pages, max_pages = 3, 32, 2, 128, 64, 12, 4
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(b, hq, 1, d, generator=g).to(dtype).cuda()
+    kp = torch.randn(pages, hkv, page, d, generator=g).to(dtype).cuda()
+    vp = torch.randn(pages, hkv, page, d, generator=g).to(dtype).cuda()
+    table = torch.tensor([[0, 3, 5, 7], [11, 10, 9, 8], [1, 2, 4, 6]], dtype=torch.int32).cuda()
+    lens = torch.tensor([256, 130, 7], dtype=torch.int32)
+    cos, sin = _tables(d, 300)
+    out = flash_decode(q, kp, vp, cache_seqlens=lens.cuda(), block_table=table, rope_cos=cos,
+                       rope_sin=sin, start_pos=(lens - 1).cuda())
+    qr = _rotated(q, cos, sin, (lens - 1).numpy()[:, None])
+    base = flash_decode(qr, kp, vp, cache_seqlens=lens.cuda(), block_table=table)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    want = orc.decode_paged(np64(qr), np64(kp), np64(vp), table.cpu().numpy(), lens.numpy())
+    assert_close_maxabs(out, want, TOL[dtype], "paged decode rope")
+
+
+def test_decode_rope_c4_shape_equals_decode_on_rotated_q():
+    """C4 (bf16, B=64, Hq=32, Hkv=8, S_k=32768, D=128): fused rotation of q
+    gives the bits of the plain decode on the oracle-rotated q."""
+    b, hq, hkv, sk, d = 64, 32, 8, 32768, 128
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(21)
+    q = torch.randn(b, hq, 1, d, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(b, hkv, sk, d, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(b, hkv, sk, d, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = _tables(d, sk)
+    pos = torch.randint(0, sk, (b,), generator=torch.Generator().manual_seed(2), dtype=torch.int32)
+    out = flash_decode(q, k, v, rope_cos=cos, rope_sin=sin, start_pos=pos.cuda())
+    qr = _rotated(q, cos, sin, pos.numpy()[:, None])
+    base = flash_decode(qr, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+
+
+# ----------------------------------------------------------------- forward
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_forward_rope_equals_forward_on_rotated_q(dtype, causal, d):
+    b, hq, hkv, sq, sk = 2, 4, 2, 300, 420
+    q, k, v = make_qkv(b, hq, hkv, sq, sk, d, dtype, seed=d + causal)
+    cos, sin = _tables(d, 1024)
+    starts = torch.tensor([0, 500], dtype=torch.int32)
+    with torch.no_grad():
+        out = flash_attention(q, k, v, causal, rope_cos=cos, rope_sin=sin,
+                              start_pos=starts.cuda())
+        qr = _rotated(q, cos, sin, orc.rope_positions(starts.numpy(), b, sq))
+        base = flash_attention(qr, k, v, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    want, _ = orc.attention_forward(np64(qr), np64(k), np64(v), causal)
+    assert_close_maxabs(out, want, TOL[dtype], f"forward rope {dtype} causal={causal} d={d}")
+
+
+def test_forward_rope_paired_causal_blocks():
+    """Enough causal work for the kernel to pair query blocks per workgroup."""
+    b, hq, hkv, s, d = 2, 32, 8, 2048, 128
+    q, k, v = make_qkv(b, hq, hkv, s, s, d, torch.bfloat16, seed=9)
+    cos, sin = _tables(d, 4096)
+    with torch.no_grad():
+        out = flash_attention(q, k, v, True, rope_cos=cos, rope_sin=sin, start_pos=1000)
+        qr = _rotated(q, cos, sin, orc.rope_positions(1000, b, s))
+        base = flash_attention(qr, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
