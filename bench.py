@@ -71,6 +71,8 @@ HBM_TRAFFIC_BYTES = {
     "decode_varlen": 4_305_177_417,
     "kv_update": 67_274_953,
     "decode_paged": 4_305_404_288,
+    "decode_rope": 8_612_555_565,
+    "kv_update_rope": 75_530_834,
 }
 
 

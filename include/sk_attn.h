@@ -220,8 +220,9 @@ SK_API int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, voi
  *
  *   rope_cos, rope_sin  device tables of rope_rows rows (element stride
  *                       rope_stride >= D between rows; the first D columns are
- *                       read), element type rope_dtype (SK_F32/F16/BF16) --
- *                       the (max_seq_len, D) tables of precompute_freqs
+ *                       read), element type rope_dtype (SK_F32/F16/BF16),
+ *                       16-byte aligned with rows a multiple of 16 bytes apart
+ *                       -- the (max_seq_len, D) tables of precompute_freqs
  *                       (src/stackkernels/_reference/torch/rope.py:6-29);
  *   rope_pos            NULL, or a device array of B int32 per-row base positions;
  *   rope_start          added to every position (the reference's start_pos).

@@ -41,8 +41,15 @@ class RopeArgs:
         if d % 16 != 0:
             raise NotImplementedError(f"fused RoPE needs a head dim that is a multiple of 16, "
                                       f"got {d}")
-        if cos.stride(1) != 1 or sin.stride(1) != 1 or cos.stride(0) != sin.stride(0):
+        # The kernels read the tables with 16-byte vector loads.
+        esz = cos.element_size()
+        if (cos.stride(1) != 1 or sin.stride(1) != 1 or cos.stride(0) != sin.stride(0)
+                or (cos.stride(0) * esz) % 16 or cos.data_ptr() % 16 or sin.data_ptr() % 16):
             cos, sin = cos.contiguous(), sin.contiguous()
+            if cos.data_ptr() % 16:
+                cos = cos.clone()
+            if sin.data_ptr() % 16:
+                sin = sin.clone()
         self.cos, self.sin = cos, sin
         self.pos = None
         start = 0

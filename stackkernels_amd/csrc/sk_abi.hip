@@ -130,9 +130,9 @@ int make_rope(const void* cos, const void* sin, int rope_dtype, int rope_rows,
   if (rope_rows <= 0 || rope_stride < D)
     return fail(SK_EINVAL, "rope table of %d rows with row stride %lld for head dim %d", rope_rows,
                 (long long)rope_stride, D);
-  const uintptr_t esz = (uintptr_t)elem_bytes(rope_dtype);
-  if (((uintptr_t)cos | (uintptr_t)sin) % esz != 0)
-    return fail(SK_EINVAL, "rope table pointers are not element-aligned");
+  if (!aligned16(cos) || !aligned16(sin) || (rope_stride * elem_bytes(rope_dtype)) % 16 != 0)
+    return fail(SK_EINVAL, "rope tables must be 16-byte aligned with a row stride that is a "
+                "multiple of 16 bytes");
   if (!rope_pos && tokens > 0 &&
       (rope_start < 0 || (int64_t)rope_start + tokens > (int64_t)rope_rows))
     return fail(SK_EINVAL, "positions [%d, %lld) lie outside the rope table of %d rows", rope_start,

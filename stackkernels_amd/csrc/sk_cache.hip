@@ -15,8 +15,10 @@
 //
 // With RoPE tables the keys are rotated on their way into the cache (the
 // reference's apply_rope on k followed by the append, in one pass over the
-// new rows): one thread then moves an aligned 16-byte chunk of a K row, which
-// it rotates with the chunk half a head away, and the same chunk of V.
+// new rows): one thread then moves an aligned 16-byte chunk of a token's K
+// row, which it rotates with the chunk half a head away, and the same chunk of
+// V, for up to four KV heads, so the token's slot, position and table entries
+// are read once per four heads.
 #include "sk_common.h"
 #include "sk_kernels.h"
 #include "sk_rope.h"
@@ -71,53 +73,66 @@ __global__ void __launch_bounds__(256) kv_cache_update_kernel(CacheParams p) {
   *reinterpret_cast<U*>(vd) = vx;
 }
 
-// Rotating append.  Thread i moves 16-byte chunk c of row r = (b, h, t).
-// T: BF16 / F16 (8 elements per chunk) or float (4).
+// Rotating append.  Thread i of grid row y handles 16-byte chunk c of new
+// token t of batch row b, (b, t, c) = split(i), for the KV heads
+// [kRopeHeads * y, kRopeHeads * (y + 1)): the slot, the position and the
+// table entries are loaded once for all of them.  T: BF16 / F16 (8 elements
+// per chunk) or float (4).
+constexpr int kRopeHeads = 4;
+
 template <class T>
 __global__ void __launch_bounds__(256) kv_cache_update_rope_kernel(CacheParams p) {
   constexpr bool kF32 = __is_same(T, float);
   constexpr int EPC = kF32 ? 4 : 8;  // elements per 16-byte chunk
+  using E = typename std::conditional<kF32, float, uint16_t>::type;
   const int chunks = p.D / EPC;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t rows = (int64_t)p.B * p.Hkv * p.T;
-  if (i >= rows * chunks) return;
-  const int64_t r = i / chunks;
-  const int c = (int)(i - r * chunks);
-  const int t = (int)(r % p.T);
-  const int64_t bh = r / p.T;
-  const int h = (int)(bh % p.Hkv);
-  const int b = (int)(bh / p.Hkv);
-  const int64_t slot = p.slots[(int64_t)b * p.T + t];
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < B * T * chunks (checked on the host)
+  if (i >= p.B * p.T * chunks) return;
+  const int bt = i / chunks;
+  const int c = i - bt * chunks;
+  const int b = bt / p.T;
+  const int t = bt - b * p.T;
+  const int64_t slot = p.slots[bt];
   if (slot < 0 || slot >= p.S) return;
   const int64_t unit = p.page_size > 0 ? slot / p.page_size : b;
   const int64_t row = p.page_size > 0 ? slot % p.page_size : slot;
   const int d0 = c * EPC;
   const int half = p.D >> 1;
-  const int dp = d0 < half ? d0 + half : d0 - half;  // partner chunk (same half-offset)
+  const bool lo = d0 < half;
+  const int dp = lo ? d0 + half : d0 - half;  // partner chunk, half a head away
   const int rrow = rope_row(p.rope, b, t);
-  using E = typename std::conditional<kF32, float, uint16_t>::type;
-  const E* ks = (const E*)p.k + b * p.k_sb + h * p.k_sh + t * p.k_ss;
-  const E* vs = (const E*)p.v + b * p.v_sb + h * p.v_sh + t * p.v_ss;
-  E* kd = (E*)p.kc + unit * p.kc_sb + h * p.kc_sh + row * p.kc_ss;
-  E* vd = (E*)p.vc + unit * p.vc_sb + h * p.vc_sh + row * p.vc_ss;
-  const u32x4 vx = *reinterpret_cast<const u32x4*>(vs + d0);
-  u32x4 kx = *reinterpret_cast<const u32x4*>(ks + d0);
-  if (rrow >= 0) {
-    const u32x4 kp = *reinterpret_cast<const u32x4*>(ks + dp);
-    if constexpr (kF32) {
-      const int64_t e = (int64_t)rrow * p.rope.stride + d0;
+  float cs[EPC], sn[EPC];
+  if (rrow >= 0) rope_coeffs<EPC>(p.rope, rrow, d0, cs, sn);
+  const int h0 = blockIdx.y * kRopeHeads;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        kx[j] = __builtin_bit_cast(
-            uint32_t, rope_mix(__builtin_bit_cast(float, kx[j]), __builtin_bit_cast(float, kp[j]),
-                               d0 < half, rope_entry(p.rope, p.rope.cos, e + j),
-                               rope_entry(p.rope, p.rope.sin, e + j)));
-    } else {
-      kx = rope8<T>(kx, kp, d0, half, p.rope, rrow);
+  for (int j = 0; j < kRopeHeads; ++j) {
+    const int h = h0 + j;
+    if (h >= p.Hkv) break;
+    const E* ks = (const E*)p.k + b * p.k_sb + h * p.k_sh + t * p.k_ss;
+    const E* vs = (const E*)p.v + b * p.v_sb + h * p.v_sh + t * p.v_ss;
+    E* kd = (E*)p.kc + unit * p.kc_sb + h * p.kc_sh + row * p.kc_ss;
+    E* vd = (E*)p.vc + unit * p.vc_sb + h * p.vc_sh + row * p.vc_ss;
+    const u32x4 vx = *reinterpret_cast<const u32x4*>(vs + d0);
+    u32x4 kx = *reinterpret_cast<const u32x4*>(ks + d0);
+    if (rrow >= 0) {
+      const u32x4 kp = *reinterpret_cast<const u32x4*>(ks + dp);
+      if constexpr (kF32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // (Elements are copied out before the bit casts: clang's bit cast
+          // of a vector element expression reads element 0 whatever the index.)
+          const uint32_t xw = kx[e], pw = kp[e];
+          const float r = rope_mix(__builtin_bit_cast(float, xw), __builtin_bit_cast(float, pw),
+                                   lo, cs[e], sn[e]);
+          kx[e] = __builtin_bit_cast(uint32_t, r);
+        }
+      } else {
+        kx = rope8<T>(kx, kp, lo, cs, sn);
+      }
     }
+    *reinterpret_cast<u32x4*>(kd + d0) = kx;
+    *reinterpret_cast<u32x4*>(vd + d0) = vx;
   }
-  *reinterpret_cast<u32x4*>(kd + d0) = kx;
-  *reinterpret_cast<u32x4*>(vd + d0) = vx;
 }
 
 // Largest copy unit (16, 8, 4 or 2 bytes) that divides the row and every
@@ -140,11 +155,12 @@ hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s) {
     // Rotating path: 16-byte chunks; D / 2 a multiple of the chunk.
     const int epc = 16 / p.esize;
     if (unit < 16 || p.D % (2 * epc) != 0) return hipErrorInvalidValue;
-    const int64_t threads = (int64_t)p.B * p.Hkv * p.T * (p.D / epc);
+    const int64_t threads = (int64_t)p.B * p.T * (p.D / epc);
     if (threads == 0) return hipSuccess;
-    const int64_t blocks = (threads + 255) / 256;
-    if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-    const dim3 grid((unsigned)blocks);
+    if (threads > 0x7fffffffLL - 255) return hipErrorInvalidConfiguration;
+    const int64_t head_groups = (p.Hkv + kRopeHeads - 1) / kRopeHeads;
+    if (head_groups > 65535) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)head_groups);
     switch (p.dtype) {
       case 0: hipLaunchKernelGGL(kv_cache_update_rope_kernel<float>, grid, dim3(256), 0, s, p); break;
       case 1: hipLaunchKernelGGL(kv_cache_update_rope_kernel<F16>, grid, dim3(256), 0, s, p); break;

@@ -75,7 +75,7 @@ __device__ __forceinline__ void load_q(const DecParams& p, int b, int hq, bool h
     if (head_ok && d0 < p.D) {
       x = ldg_b128_cached(qp + d0);
       if (row >= 0)
-        x = rope8<T>(x, ldg_b128_cached(qp + (d0 < half ? d0 + half : d0 - half)), d0, half,
+        x = rope8_at<T>(x, ldg_b128_cached(qp + (d0 < half ? d0 + half : d0 - half)), d0, half,
                      p.rope, row);
     }
     qreg[s] = x ^ p.q_sign;

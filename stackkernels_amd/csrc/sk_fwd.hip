@@ -193,7 +193,7 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
         const int dq = d0 < half ? d0 + half : d0 - half;
         const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.q_ss + dq) * 2) : kBufferOob;
         const u32x4 y = buffer_load_b128(qr, off);
-        if (rrow >= 0 && d0 < p.D) qreg[s] = rope8<T>(qreg[s], y, d0, half, p.rope, rrow);
+        if (rrow >= 0 && d0 < p.D) qreg[s] = rope8_at<T>(qreg[s], y, d0, half, p.rope, rrow);
       }
     }
 #pragma unroll

@@ -182,7 +182,8 @@ def test_rope_argument_errors(lib):
     assert dec(D=72) == _lib.SK_EUNSUPPORTED and "multiple of 16" in _lib.last_error()
     assert dec(rows=0) == _lib.SK_EINVAL
     assert dec(stride=32) == _lib.SK_EINVAL and "row stride" in _lib.last_error()
-    assert dec(cos=18) == _lib.SK_EINVAL and "element-aligned" in _lib.last_error()
+    assert dec(cos=24) == _lib.SK_EINVAL and "16-byte aligned" in _lib.last_error()
+    assert dec(stride=66) == _lib.SK_EINVAL and "16-byte aligned" in _lib.last_error()
     assert dec(start=128) == _lib.SK_EINVAL and "outside the rope table" in _lib.last_error()
     assert dec(start=-1) == _lib.SK_EINVAL
     assert dec(B=0) == _lib.SK_OK
