@@ -34,7 +34,7 @@ extern "C" {
 #define SK_API
 #endif
 
-#define SK_ABI_VERSION 4
+#define SK_ABI_VERSION 5
 
 /* Element type codes. */
 #define SK_F32 0
@@ -289,6 +289,55 @@ SK_API int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v
                                   const void* rope_cos, const void* rope_sin, int rope_dtype,
                                   int rope_rows, int64_t rope_stride, const int32_t* rope_pos,
                                   int rope_start, void* stream);
+
+/*
+ * Introspection: the kernel and launch configuration a call would run, from
+ * the same plan the launchers use.  Replaces what the reference's
+ * pick(op, shape, ..., explain=True) reports for this path
+ * (src/stackkernels/_opt/pick.py:18-226: the chosen BLOCK_M / BLOCK_N /
+ * num_warps / num_stages / SPLIT_KV and the grid), for the gfx950 table of
+ * this library instead of a Triton heuristic.
+ *
+ *   op       SK_OP_FWD, SK_OP_BWD_DKV, SK_OP_BWD_DQ, SK_OP_DECODE (the split
+ *            pass; fp32: the fp32 forward kernel with one query row) or
+ *            SK_OP_DECODE_COMBINE (grid 0 when one split writes O directly);
+ *   Sq       ignored for decode; num_splits: decode only (0 = the table's pick);
+ *   variant  SK_VARIANT_* bits: the decode over a paged pool, the RoPE
+ *            prologue (forward and decode);
+ *   query_device  0: no HIP call is made (works without a GPU) and the
+ *            device-reported slots hold -1; 1: also ask the HIP runtime for
+ *            the kernel's LDS bytes, registers per lane and resident
+ *            workgroups per CU on the current device.
+ *   cfg      int64_t[SK_CFG_LEN], slots below; kernel_name (optional) gets
+ *            the kernel and its template configuration.
+ */
+#define SK_OP_FWD 0
+#define SK_OP_BWD_DKV 1
+#define SK_OP_BWD_DQ 2
+#define SK_OP_DECODE 3
+#define SK_OP_DECODE_COMBINE 4
+
+#define SK_VARIANT_PAGED 1
+#define SK_VARIANT_ROPE 2
+
+#define SK_CFG_GRID 0           /* workgroups per launch                        */
+#define SK_CFG_THREADS 1        /* threads per workgroup (64 per wavefront)     */
+#define SK_CFG_BLOCK_M 2        /* query rows per workgroup (decode: query heads) */
+#define SK_CFG_BLOCK_N 3        /* keys per tile (dK/dV: keys per workgroup)    */
+#define SK_CFG_STAGES 4         /* tile ring depth; 0 = staged in registers     */
+#define SK_CFG_HEAD_DIM 5       /* padded head dim the kernel is compiled for   */
+#define SK_CFG_SPLITS 6         /* decode key splits (1 otherwise)              */
+#define SK_CFG_PAIRED 7         /* forward: causal query blocks paired per workgroup */
+#define SK_CFG_WORKSPACE 8      /* scratch bytes the call needs                 */
+#define SK_CFG_KEYS_PER_SPLIT 9 /* decode                                       */
+#define SK_CFG_LDS_BYTES 10     /* device-reported, or -1                       */
+#define SK_CFG_VGPRS 11         /* device-reported registers per lane, or -1    */
+#define SK_CFG_WG_PER_CU 12     /* device-reported resident workgroups per CU, or -1 */
+#define SK_CFG_LEN 16
+
+SK_API int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                     int is_causal, int num_splits, int variant, int query_device,
+                     int64_t* cfg, char* kernel_name, size_t name_len);
 
 #ifdef __cplusplus
 }

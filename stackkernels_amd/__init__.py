@@ -16,6 +16,7 @@ _LAZY: dict[str, str] = {
     "torch": "stackkernels_amd.torch",
     "_core": "stackkernels_amd._core",
     "_reference": "stackkernels_amd._reference",
+    "_opt": "stackkernels_amd._opt",
 }
 
 __all__ = ["__version__", "options", "get_backend", "set_backend", *_LAZY]

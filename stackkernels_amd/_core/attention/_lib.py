@@ -15,7 +15,7 @@ import threading
 
 SK_F32, SK_F16, SK_BF16 = 0, 1, 2
 SK_OK, SK_EINVAL, SK_EUNSUPPORTED, SK_EWORKSPACE = 0, -1, -2, -3
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "csrc")
 LIB_PATH = os.environ.get("SK_ATTN_LIB", os.path.join(_LIB_DIR, "libsk_attn.so"))
@@ -81,6 +81,9 @@ SIGNATURES: dict[str, tuple] = {
     "sk_kv_cache_update_paged_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,
                                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                                _i64p, _i64p, _i64p, _i64p, *_ROPE, _vp]),
+    "sk_kernel_config": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                  _c_int, _c_int, _c_int, _c_int, _i64p, ctypes.c_char_p,
+                                  ctypes.c_size_t]),
 }
 
 

@@ -161,6 +161,36 @@ const char* sk_last_error(void) { return g_err; }
 
 }  // extern "C"
 
+// Sizes and work split of the forward: query blocks per (b, h) and, under
+// the causal mask, whether blocks j and n_mblocks-1-j are paired in one
+// workgroup (when that still leaves at least two workgroups per CU).
+static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
+                     sk::FwdParams* p) {
+  p->B = B, p->Hq = Hq, p->Hkv = Hkv, p->Sq = Sq, p->Sk = Sk, p->D = D, p->group = Hq / Hkv;
+  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D);
+  p->n_mblocks = (Sq + rows - 1) / rows;
+  if ((int64_t)p->n_mblocks * B * Hq > 0x7fffffffLL)
+    return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p->n_mblocks * B * Hq);
+  p->pair_items = dtype != SK_F32 && is_causal && p->n_mblocks >= 2 &&
+                  (int64_t)((p->n_mblocks + 1) / 2) * B * Hq >= 512;
+  p->n_items = p->pair_items ? (p->n_mblocks + 1) / 2 : p->n_mblocks;
+  return SK_OK;
+}
+
+// Split count and keys per split of a decode call (num_splits 0: the gfx950
+// table's pick).  fp32 decode runs unsplit.
+static int decode_splits(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,
+                         int* splits, int* kps) {
+  if (dtype == SK_F32) num_splits = 1;
+  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk, D);
+  if (num_splits < 1 || num_splits > 1024)
+    return fail(SK_EINVAL, "num_splits=%d outside [1, 1024]", num_splits);
+  *kps = keys_per_split_for(Sk, num_splits);
+  if (Sk > 0) num_splits = std::min(num_splits, (Sk + *kps - 1) / *kps);
+  *splits = num_splits;
+  return SK_OK;
+}
+
 // sk_attn_fwd and sk_attn_fwd_rope.
 static int fwd_impl(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                     int B, int Hq, int Hkv, int Sq, int Sk, int D, const int64_t* q_strides,
@@ -187,19 +217,10 @@ static int fwd_impl(int dtype, const void* q, const void* k, const void* v, void
   p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_ss = k_strides[2];
   p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_ss = v_strides[2];
   p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_ss = o_strides[2];
-  p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
   p.scale = std::fabs(sm_scale);
   p.scale_log2 = p.scale * 1.4426950408889634f;
   const bool neg = sm_scale < 0.f;
-  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D);
-  p.n_mblocks = (Sq + rows - 1) / rows;
-  if ((int64_t)p.n_mblocks * B * Hq > 0x7fffffffLL)
-    return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p.n_mblocks * B * Hq);
-  // Causal: pair query block j with n_mblocks-1-j in one workgroup when that
-  // still leaves at least two workgroups per CU (256 CUs).
-  p.pair_items = dtype != SK_F32 && is_causal && p.n_mblocks >= 2 &&
-                 (int64_t)((p.n_mblocks + 1) / 2) * B * Hq >= 512;
-  p.n_items = p.pair_items ? (p.n_mblocks + 1) / 2 : p.n_mblocks;
+  if ((rc = fwd_shape(dtype, B, Hq, Hkv, Sq, Sk, D, is_causal, &p))) return rc;
   p.rope = rope;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
@@ -368,12 +389,8 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
   if (Hq / Hkv > 64 && dtype != SK_F32)
     return fail(SK_EUNSUPPORTED, "decode supports up to 64 query heads per KV head, got %d", Hq / Hkv);
 
-  if (dtype == SK_F32) num_splits = 1;
-  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk, D);
-  if (num_splits < 1 || num_splits > 1024)
-    return fail(SK_EINVAL, "num_splits=%d outside [1, 1024]", num_splits);
-  const int kps = keys_per_split_for(Sk, num_splits);
-  if (Sk > 0) num_splits = std::min(num_splits, (Sk + kps - 1) / kps);
+  int kps = 0;
+  if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &num_splits, &kps))) return rc;
   const size_t need = decode_ws_bytes(dtype, B, Hq, D, num_splits);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(SK_EWORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, need);
@@ -629,6 +646,101 @@ int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v, void*
   return cache_update_impl(dtype, k, v, k_pool, v_pool, slot_mapping, B, Hkv, T,
                            (int64_t)num_pages * page_size, page_size, D, k_strides, v_strides,
                            kp_strides, vp_strides, r, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- introspection
+
+static const char* elem_name(int e) {
+  return e == SK_BF16 ? "BF16" : e == SK_F16 ? "F16" : e == SK_F32 ? "F32" : "?";
+}
+
+extern "C" {
+
+int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                     int is_causal, int num_splits, int variant, int query_device, int64_t* cfg,
+                     char* kernel_name, size_t name_len) {
+  g_err[0] = 0;
+  if (!cfg) return fail(SK_EINVAL, "cfg pointer is NULL");
+  for (int i = 0; i < SK_CFG_LEN; ++i) cfg[i] = 0;
+  if (kernel_name && name_len) kernel_name[0] = 0;
+  const bool decode = op == SK_OP_DECODE || op == SK_OP_DECODE_COMBINE;
+  int rc = check_dims(dtype, B, Hq, Hkv, decode ? 1 : Sq, Sk, D);
+  if (rc) return rc;
+  if (decode && Hq / Hkv > 64 && dtype != SK_F32)
+    return fail(SK_EUNSUPPORTED, "decode supports up to 64 query heads per KV head, got %d", Hq / Hkv);
+  // Non-null stand-ins for the optional inputs a variant carries: the plan
+  // only tests them for null, and nothing is launched here.
+  static const int kStandIn = 0;
+  const bool rope = (variant & SK_VARIANT_ROPE) != 0;
+  const bool paged = (variant & SK_VARIANT_PAGED) != 0;
+  sk::KernelPlan k;
+  int64_t splits = 1, kps = 0, paired = 0;
+  size_t ws = 0;
+  if (op == SK_OP_FWD || (decode && dtype == SK_F32)) {
+    if (op == SK_OP_DECODE_COMBINE) return SK_OK;  // fp32 decode has no combine pass
+    sk::FwdParams p{};
+    if ((rc = fwd_shape(dtype, B, Hq, Hkv, decode ? 1 : Sq, Sk, D, decode ? 0 : is_causal, &p)))
+      return rc;
+    if (rope) p.rope.cos = &kStandIn;
+    if (paged && decode) p.block_table = &kStandIn;
+    k = dtype == SK_F32 ? sk::plan_fwd_f32(p, !decode && is_causal)
+                        : sk::plan_fwd_mfma(dtype, p, is_causal != 0);
+    paired = p.pair_items;
+    if (decode) ws = decode_ws_bytes(dtype, B, Hq, D, 1);
+  } else if (op == SK_OP_BWD_DKV || op == SK_OP_BWD_DQ) {
+    sk::BwdParams p{};
+    p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+    k = op == SK_OP_BWD_DKV ? sk::plan_bwd_dkv(dtype, p, is_causal != 0)
+                            : sk::plan_bwd_dq(dtype, p, is_causal != 0);
+    ws = bwd_ws_bytes(B, Hq, Sq);
+  } else if (decode) {
+    int ns = 0, per = 0;
+    if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &ns, &per))) return rc;
+    sk::DecParams p{};
+    p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+    p.num_splits = ns, p.keys_per_split = per, p.dpad = sk::padded_head_dim(D);
+    if (rope) p.rope.cos = &kStandIn;
+    if (paged) p.block_table = &kStandIn;
+    splits = ns, kps = per;
+    ws = decode_ws_bytes(dtype, B, Hq, D, ns);
+    if (op == SK_OP_DECODE_COMBINE && ns <= 1) {  // one split writes O directly
+      cfg[SK_CFG_SPLITS] = splits;
+      return SK_OK;
+    }
+    k = op == SK_OP_DECODE ? sk::plan_decode_mfma(dtype, p) : sk::plan_decode_combine(dtype, p);
+  } else {
+    return fail(SK_EINVAL, "unknown op %d", op);
+  }
+  if (!k.fn) return fail(SK_EUNSUPPORTED, "no kernel for op %d with these arguments", op);
+  cfg[SK_CFG_GRID] = (int64_t)k.grid.x * k.grid.y * k.grid.z;
+  cfg[SK_CFG_THREADS] = (int64_t)k.block.x * k.block.y * k.block.z;
+  cfg[SK_CFG_BLOCK_M] = k.block_m;
+  cfg[SK_CFG_BLOCK_N] = k.block_n;
+  cfg[SK_CFG_STAGES] = k.stages;
+  cfg[SK_CFG_HEAD_DIM] = k.head_dim;
+  cfg[SK_CFG_SPLITS] = splits;
+  cfg[SK_CFG_PAIRED] = paired;
+  cfg[SK_CFG_WORKSPACE] = (int64_t)ws;
+  cfg[SK_CFG_KEYS_PER_SPLIT] = kps;
+  cfg[SK_CFG_LDS_BYTES] = cfg[SK_CFG_VGPRS] = cfg[SK_CFG_WG_PER_CU] = -1;
+  if (kernel_name && name_len)
+    snprintf(kernel_name, name_len, "%s<%s, D=%d, BM=%d, BN=%d, stages=%d, causal=%d, paged=%d, rope=%d>",
+             k.kernel, elem_name(k.elem), k.head_dim, k.block_m, k.block_n, k.stages, (int)k.causal,
+             (int)k.paged, (int)k.rope);
+  if (query_device) {
+    hipFuncAttributes a{};
+    hipError_t e = hipFuncGetAttributes(&a, k.fn);
+    if (e != hipSuccess) return hip_fail(e, "sk_kernel_config attributes");
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k.fn, (int)cfg[SK_CFG_THREADS], 0);
+    if (e != hipSuccess) return hip_fail(e, "sk_kernel_config occupancy");
+    cfg[SK_CFG_LDS_BYTES] = (int64_t)a.sharedSizeBytes;
+    cfg[SK_CFG_VGPRS] = a.numRegs;
+    cfg[SK_CFG_WG_PER_CU] = per_cu;
+  }
+  return SK_OK;
 }
 
 }  // extern "C"

@@ -749,49 +749,87 @@ struct DqConfig<256> {
 };
 
 template <class T, int DP, int DO>
-static hipError_t launch_bwd_t(const BwdParams& p, bool causal, hipStream_t s) {
+static KernelPlan plan_dkv_t(BwdParams& p, bool causal) {
+  constexpr int STAGES = 4;
+  p.n_nblocks = (p.Sk + 127) / 128;
+  KernelPlan k;
+  k.fn = causal ? (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, true>
+                : (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, false>;
+  k.grid = dim3((unsigned)((int64_t)p.n_nblocks * p.B * p.Hkv * (DP / DO)));
+  k.block = dim3(512);
+  k.kernel = "bwd_dkv_kernel";
+  k.elem = T::code;
+  k.head_dim = DP;
+  k.block_m = 32;   // queries per streamed tile
+  k.block_n = 128;  // keys per workgroup
+  k.stages = STAGES;
+  k.causal = causal;
+  return k;
+}
+
+template <class T, int DP>
+static KernelPlan plan_dq_t(BwdParams& p, bool causal) {
   constexpr int NW = 4;  // dQ waves per workgroup
   constexpr int STAGES = 4;
   using QC = DqConfig<DP>;
-  BwdParams q = p;
-  q.n_nblocks = (p.Sk + 127) / 128;
-  q.n_mblocks = (p.Sq + 32 * NW - 1) / (32 * NW);
-  const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (DP / DO);
-  const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
-  if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  if (g_kv > 0) {
-    if (causal)
-      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, STAGES, true>), dim3((unsigned)g_kv), dim3(512),
-                         0, s, q);
-    else
-      hipLaunchKernelGGL((bwd_dkv_kernel<T, DP, DO, STAGES, false>), dim3((unsigned)g_kv), dim3(512),
-                         0, s, q);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  if (g_q > 0) {
-    if (causal)
-      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, true>),
-                         dim3((unsigned)g_q), dim3(NW * 64), 0, s, q);
-    else
-      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, false>),
-                         dim3((unsigned)g_q), dim3(NW * 64), 0, s, q);
-  }
-  return hipGetLastError();
+  p.n_mblocks = (p.Sq + 32 * NW - 1) / (32 * NW);
+  KernelPlan k;
+  k.fn = causal ? (const void*)bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, true>
+                : (const void*)bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, false>;
+  k.grid = dim3((unsigned)((int64_t)p.n_mblocks * p.B * p.Hq));
+  k.block = dim3(NW * 64);
+  k.kernel = "bwd_dq_kernel";
+  k.elem = T::code;
+  k.head_dim = DP;
+  k.block_m = 32 * NW;
+  k.block_n = QC::kBn;
+  k.stages = STAGES;
+  k.causal = causal;
+  return k;
 }
 
 template <class T>
-static hipError_t launch_bwd_dt(const BwdParams& p, bool causal, hipStream_t s) {
-  if (p.D <= 64) return launch_bwd_t<T, 64, 64>(p, causal, s);
-  if (p.D <= 128) return launch_bwd_t<T, 128, 128>(p, causal, s);
-  if (p.D <= 256) return launch_bwd_t<T, 256, 128>(p, causal, s);
-  return hipErrorInvalidValue;
+static KernelPlan plan_dkv_dt(BwdParams& p, bool causal) {
+  if (p.D <= 64) return plan_dkv_t<T, 64, 64>(p, causal);
+  if (p.D <= 128) return plan_dkv_t<T, 128, 128>(p, causal);
+  if (p.D <= 256) return plan_dkv_t<T, 256, 128>(p, causal);
+  return KernelPlan{};
+}
+
+template <class T>
+static KernelPlan plan_dq_dt(BwdParams& p, bool causal) {
+  if (p.D <= 64) return plan_dq_t<T, 64>(p, causal);
+  if (p.D <= 128) return plan_dq_t<T, 128>(p, causal);
+  if (p.D <= 256) return plan_dq_t<T, 256>(p, causal);
+  return KernelPlan{};
+}
+
+KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal) {
+  if (dtype == BF16::code) return plan_dkv_dt<BF16>(p, causal);
+  if (dtype == F16::code) return plan_dkv_dt<F16>(p, causal);
+  if (dtype == 0) return plan_bwd_dkv_f32(p, causal);
+  return KernelPlan{};
+}
+
+KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal) {
+  if (dtype == BF16::code) return plan_dq_dt<BF16>(p, causal);
+  if (dtype == F16::code) return plan_dq_dt<F16>(p, causal);
+  if (dtype == 0) return plan_bwd_dq_f32(p, causal);
+  return KernelPlan{};
 }
 
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s) {
-  if (dtype == BF16::code) return launch_bwd_dt<BF16>(p, causal, s);
-  if (dtype == F16::code) return launch_bwd_dt<F16>(p, causal, s);
-  return hipErrorInvalidValue;
+  if (dtype != BF16::code && dtype != F16::code) return hipErrorInvalidValue;
+  BwdParams q = p;
+  const KernelPlan kv = plan_bwd_dkv(dtype, q, causal);
+  const KernelPlan dq = plan_bwd_dq(dtype, q, causal);
+  if (!kv.fn || !dq.fn) return hipErrorInvalidValue;
+  const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (kv.head_dim == 256 ? 2 : 1);
+  const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
+  if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  hipError_t e = run_plan(kv, &q, s);
+  if (e != hipSuccess) return e;
+  return run_plan(dq, &q, s);
 }
 
 }  // namespace sk

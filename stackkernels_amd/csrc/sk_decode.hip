@@ -524,64 +524,97 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecParams p) {
 // kernel with 5 stages of 16 KB (2 workgroups per CU at D = 128, so 128 KB
 // of loads in flight per CU: HBM streaming is latency-bound below that).
 template <class T, int DP, bool PAGED>
-static hipError_t launch_decode_dp(const DecParams& p, hipStream_t s) {
-  const dim3 grid((unsigned)p.num_splits, (unsigned)(p.B * p.Hkv));
+static KernelPlan plan_decode_dp(const DecParams& p) {
   constexpr bool kRing = DP == 64 || DP == 128 || DP == 256;
   constexpr int kStages = DP == 256 ? 2 : 5;
-  if (p.group <= 16)
-    hipLaunchKernelGGL((decode_split_kernel<T, DP, 1, PAGED>), grid, dim3(64), 0, s, p);
-  else if (p.group <= 32) {
+  KernelPlan k;
+  k.grid = dim3((unsigned)p.num_splits, (unsigned)(p.B * p.Hkv));
+  k.elem = T::code;
+  k.head_dim = DP;
+  k.block_n = 32;
+  k.paged = PAGED;
+  k.rope = p.rope.cos != nullptr;
+  int nwh = 0;
+  if (p.group <= 16) {
+    nwh = 1;
+    k.fn = (const void*)decode_split_kernel<T, DP, 1, PAGED>;
+  } else if (p.group <= 32) {
+    nwh = 2;
     if constexpr (kRing)
-      hipLaunchKernelGGL((decode_ring_kernel<T, DP, 2, kStages, PAGED>), grid, dim3(128), 0, s, p);
+      k.fn = (const void*)decode_ring_kernel<T, DP, 2, kStages, PAGED>;
     else
-      hipLaunchKernelGGL((decode_split_kernel<T, DP, 2, PAGED>), grid, dim3(128), 0, s, p);
+      k.fn = (const void*)decode_split_kernel<T, DP, 2, PAGED>;
   } else if (p.group <= 64) {
+    nwh = 4;
     if constexpr (kRing)
-      hipLaunchKernelGGL((decode_ring_kernel<T, DP, 4, kStages, PAGED>), grid, dim3(256), 0, s, p);
+      k.fn = (const void*)decode_ring_kernel<T, DP, 4, kStages, PAGED>;
     else
-      hipLaunchKernelGGL((decode_split_kernel<T, DP, 4, PAGED>), grid, dim3(256), 0, s, p);
+      k.fn = (const void*)decode_split_kernel<T, DP, 4, PAGED>;
   } else {
-    return hipErrorInvalidValue;
+    return KernelPlan{};
   }
-  return hipGetLastError();
+  const bool ring = kRing && nwh > 1;
+  k.kernel = ring ? "decode_ring_kernel" : "decode_split_kernel";
+  k.stages = ring ? kStages : 0;
+  k.block = dim3(64 * nwh);
+  k.block_m = 16 * nwh;
+  return k;
 }
 
 template <class T, bool PAGED>
-static hipError_t launch_decode_tp(const DecParams& p, hipStream_t s) {
+static KernelPlan plan_decode_tp(const DecParams& p) {
   switch (padded_head_dim(p.D)) {
     case 64:
-      return launch_decode_dp<T, 64, PAGED>(p, s);
+      return plan_decode_dp<T, 64, PAGED>(p);
     case 96:
-      return launch_decode_dp<T, 96, PAGED>(p, s);
+      return plan_decode_dp<T, 96, PAGED>(p);
     case 128:
-      return launch_decode_dp<T, 128, PAGED>(p, s);
+      return plan_decode_dp<T, 128, PAGED>(p);
     case 256:
-      return launch_decode_dp<T, 256, PAGED>(p, s);
+      return plan_decode_dp<T, 256, PAGED>(p);
     default:
-      return hipErrorInvalidValue;
+      return KernelPlan{};
   }
 }
 
 template <class T>
-static hipError_t launch_decode_t(const DecParams& p, hipStream_t s) {
-  return p.block_table ? launch_decode_tp<T, true>(p, s) : launch_decode_tp<T, false>(p, s);
+static KernelPlan plan_decode_t(const DecParams& p) {
+  return p.block_table ? plan_decode_tp<T, true>(p) : plan_decode_tp<T, false>(p);
+}
+
+KernelPlan plan_decode_mfma(int dtype, const DecParams& p) {
+  if (dtype == BF16::code) return plan_decode_t<BF16>(p);
+  if (dtype == F16::code) return plan_decode_t<F16>(p);
+  return KernelPlan{};
 }
 
 hipError_t launch_decode_mfma(int dtype, const DecParams& p, hipStream_t s) {
-  if (dtype == BF16::code) return launch_decode_t<BF16>(p, s);
-  if (dtype == F16::code) return launch_decode_t<F16>(p, s);
-  return hipErrorInvalidValue;
+  const KernelPlan k = plan_decode_mfma(dtype, p);
+  if (!k.fn) return hipErrorInvalidValue;
+  return run_plan(k, &p, s);
+}
+
+KernelPlan plan_decode_combine(int dtype, const DecParams& p) {
+  KernelPlan k;
+  if (dtype == BF16::code)
+    k.fn = (const void*)decode_combine_kernel<BF16>;
+  else if (dtype == F16::code)
+    k.fn = (const void*)decode_combine_kernel<F16>;
+  else
+    return k;
+  k.grid = dim3((unsigned)(p.B * p.Hq));
+  k.block = dim3(256);
+  k.kernel = "decode_combine_kernel";
+  k.elem = dtype;
+  k.head_dim = p.dpad;
+  k.block_m = 1;
+  return k;
 }
 
 hipError_t launch_decode_combine(int dtype, const DecParams& p, hipStream_t s) {
-  const dim3 grid((unsigned)(p.B * p.Hq));
-  if (dtype == BF16::code)
-    hipLaunchKernelGGL((decode_combine_kernel<BF16>), grid, dim3(256), 0, s, p);
-  else if (dtype == F16::code)
-    hipLaunchKernelGGL((decode_combine_kernel<F16>), grid, dim3(256), 0, s, p);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const KernelPlan k = plan_decode_combine(dtype, p);
+  if (!k.fn) return hipErrorInvalidValue;
+  return run_plan(k, &p, s);
 }
 
 }  // namespace sk

@@ -317,23 +317,36 @@ __global__ void __launch_bounds__(256) bwd_dkv_f32_kernel(BwdParams p) {
 }
 
 template <int DP>
-static void launch_fwd_f32_dp(const FwdParams& p, bool causal, hipStream_t s) {
-  const dim3 grid((unsigned)(p.n_mblocks * p.B * p.Hq));
-  if (causal)
-    hipLaunchKernelGGL((fwd_f32_kernel<DP, true>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((fwd_f32_kernel<DP, false>), grid, dim3(256), 0, s, p);
+static KernelPlan plan_fwd_f32_dp(const FwdParams& p, bool causal) {
+  KernelPlan k;
+  k.fn = causal ? (const void*)fwd_f32_kernel<DP, true> : (const void*)fwd_f32_kernel<DP, false>;
+  k.grid = dim3((unsigned)(p.n_mblocks * p.B * p.Hq));
+  k.block = dim3(256);
+  k.kernel = "fwd_f32_kernel";
+  k.elem = 0;
+  k.head_dim = DP;
+  k.block_m = kF32Rows;
+  k.block_n = kF32Tile;
+  k.causal = causal;
+  k.paged = p.block_table != nullptr;
+  k.rope = p.rope.cos != nullptr;
+  return k;
+}
+
+KernelPlan plan_fwd_f32(const FwdParams& p, bool causal) {
+  switch (padded_head_dim(p.D)) {
+    case 64: return plan_fwd_f32_dp<64>(p, causal);
+    case 96: return plan_fwd_f32_dp<96>(p, causal);
+    case 128: return plan_fwd_f32_dp<128>(p, causal);
+    case 256: return plan_fwd_f32_dp<256>(p, causal);
+    default: return KernelPlan{};
+  }
 }
 
 hipError_t launch_fwd_f32(const FwdParams& p, bool causal, hipStream_t s) {
-  switch (padded_head_dim(p.D)) {
-    case 64: launch_fwd_f32_dp<64>(p, causal, s); break;
-    case 96: launch_fwd_f32_dp<96>(p, causal, s); break;
-    case 128: launch_fwd_f32_dp<128>(p, causal, s); break;
-    case 256: launch_fwd_f32_dp<256>(p, causal, s); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  const KernelPlan k = plan_fwd_f32(p, causal);
+  if (!k.fn) return hipErrorInvalidValue;
+  return run_plan(k, &p, s);
 }
 
 hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s) {
@@ -351,30 +364,51 @@ hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s) {
 }
 
 template <int DP>
-static void launch_bwd_f32_dp(const BwdParams& p, bool causal, hipStream_t s) {
-  const int mb = (p.Sq + kF32Rows - 1) / kF32Rows;
+static KernelPlan plan_bwd_f32_dp(BwdParams& p, bool causal, bool dq) {
+  p.n_mblocks = (p.Sq + kF32Rows - 1) / kF32Rows;
   const int nb = (p.Sk + kF32Rows - 1) / kF32Rows;
-  BwdParams q = p;
-  q.n_mblocks = mb;
-  const dim3 gq((unsigned)(mb * p.B * p.Hq)), gk((unsigned)(nb * p.B * p.Hkv));
-  if (causal) {
-    hipLaunchKernelGGL((bwd_dq_f32_kernel<DP, true>), gq, dim3(256), 0, s, q);
-    hipLaunchKernelGGL((bwd_dkv_f32_kernel<DP, true>), gk, dim3(256), 0, s, q);
+  KernelPlan k;
+  if (dq) {
+    k.fn = causal ? (const void*)bwd_dq_f32_kernel<DP, true>
+                  : (const void*)bwd_dq_f32_kernel<DP, false>;
+    k.grid = dim3((unsigned)(p.n_mblocks * p.B * p.Hq));
+    k.kernel = "bwd_dq_f32_kernel";
   } else {
-    hipLaunchKernelGGL((bwd_dq_f32_kernel<DP, false>), gq, dim3(256), 0, s, q);
-    hipLaunchKernelGGL((bwd_dkv_f32_kernel<DP, false>), gk, dim3(256), 0, s, q);
+    k.fn = causal ? (const void*)bwd_dkv_f32_kernel<DP, true>
+                  : (const void*)bwd_dkv_f32_kernel<DP, false>;
+    k.grid = dim3((unsigned)(nb * p.B * p.Hkv));
+    k.kernel = "bwd_dkv_f32_kernel";
+  }
+  k.block = dim3(256);
+  k.elem = 0;
+  k.head_dim = DP;
+  k.block_m = kF32Rows;
+  k.block_n = kF32Tile;
+  k.causal = causal;
+  return k;
+}
+
+static KernelPlan plan_bwd_f32(BwdParams& p, bool causal, bool dq) {
+  switch (padded_head_dim(p.D)) {
+    case 64: return plan_bwd_f32_dp<64>(p, causal, dq);
+    case 96: return plan_bwd_f32_dp<96>(p, causal, dq);
+    case 128: return plan_bwd_f32_dp<128>(p, causal, dq);
+    case 256: return plan_bwd_f32_dp<256>(p, causal, dq);
+    default: return KernelPlan{};
   }
 }
 
+KernelPlan plan_bwd_dq_f32(BwdParams& p, bool causal) { return plan_bwd_f32(p, causal, true); }
+KernelPlan plan_bwd_dkv_f32(BwdParams& p, bool causal) { return plan_bwd_f32(p, causal, false); }
+
 hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s) {
-  switch (padded_head_dim(p.D)) {
-    case 64: launch_bwd_f32_dp<64>(p, causal, s); break;
-    case 96: launch_bwd_f32_dp<96>(p, causal, s); break;
-    case 128: launch_bwd_f32_dp<128>(p, causal, s); break;
-    case 256: launch_bwd_f32_dp<256>(p, causal, s); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  BwdParams q = p;
+  const KernelPlan dq = plan_bwd_dq_f32(q, causal);
+  const KernelPlan kv = plan_bwd_dkv_f32(q, causal);
+  if (!dq.fn || !kv.fn) return hipErrorInvalidValue;
+  hipError_t e = run_plan(dq, &q, s);
+  if (e != hipSuccess) return e;
+  return run_plan(kv, &q, s);
 }
 
 }  // namespace sk

@@ -514,38 +514,61 @@ int fwd_rows_per_block(int dtype, int d) {
 }
 
 template <class T, int DP, int BN, int NW, int OCC>
-static hipError_t launch_fwd_t(const FwdParams& p, bool causal, hipStream_t s) {
-  const dim3 grid((unsigned)(p.n_items * p.B * p.Hq));
-  const dim3 block(NW * 64);
+static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
+  KernelPlan k;
   const bool rope = p.rope.cos != nullptr;
   if (causal && !rope)
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, false>), grid, block, 0, s, p);
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, false>;
   else if (!rope)
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, false>), grid, block, 0, s, p);
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, false>;
   else if (causal)
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, true>), grid, block, 0, s, p);
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, true>;
   else
-    hipLaunchKernelGGL((fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, true>), grid, block, 0, s, p);
-  return hipGetLastError();
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, true>;
+  k.grid = dim3((unsigned)(p.n_items * p.B * p.Hq));
+  k.block = dim3(NW * 64);
+  k.kernel = "fwd_mfma_kernel";
+  k.elem = T::code;
+  k.head_dim = DP;
+  k.block_m = 32 * NW;
+  k.block_n = BN;
+  k.stages = 4;
+  k.causal = causal;
+  k.rope = rope;
+  return k;
 }
 
 template <class T>
-static hipError_t launch_fwd_dt(const FwdParams& p, bool causal, hipStream_t s) {
+static KernelPlan plan_fwd_dt(const FwdParams& p, bool causal) {
   switch (fwd_config(p.D).dp) {
     case 64:
-      return launch_fwd_t<T, 64, 64, 8, 1>(p, causal, s);
+      return plan_fwd_t<T, 64, 64, 8, 1>(p, causal);
     case 128:
-      return launch_fwd_t<T, 128, 64, 8, 1>(p, causal, s);
+      return plan_fwd_t<T, 128, 64, 8, 1>(p, causal);
     default:
-      return launch_fwd_t<T, 256, 32, 4, 1>(p, causal, s);
+      return plan_fwd_t<T, 256, 32, 4, 1>(p, causal);
   }
 }
 
+KernelPlan plan_fwd_mfma(int dtype, const FwdParams& p, bool causal) {
+  if (p.D > 256) return KernelPlan{};
+  if (dtype == BF16::code) return plan_fwd_dt<BF16>(p, causal);
+  if (dtype == F16::code) return plan_fwd_dt<F16>(p, causal);
+  return KernelPlan{};
+}
+
 hipError_t launch_fwd_mfma(int dtype, const FwdParams& p, bool causal, hipStream_t s) {
-  if (p.D > 256) return hipErrorInvalidValue;
-  if (dtype == BF16::code) return launch_fwd_dt<BF16>(p, causal, s);
-  if (dtype == F16::code) return launch_fwd_dt<F16>(p, causal, s);
-  return hipErrorInvalidValue;
+  const KernelPlan k = plan_fwd_mfma(dtype, p, causal);
+  if (!k.fn) return hipErrorInvalidValue;
+  return run_plan(k, &p, s);
+}
+
+hipError_t run_plan(const KernelPlan& k, const void* params, hipStream_t s) {
+  if (!k.fn) return hipErrorInvalidValue;
+  if ((uint64_t)k.grid.x * k.grid.y * k.grid.z == 0) return hipSuccess;
+  void* args[] = {const_cast<void*>(params)};
+  const hipError_t e = hipLaunchKernel(k.fn, k.grid, k.block, args, 0, s);
+  return e != hipSuccess ? e : hipGetLastError();
 }
 
 int padded_head_dim(int d) {

@@ -135,6 +135,35 @@ struct CacheParams {
   RopeParams rope;
 };
 
+// What a launcher runs for given parameters: the kernel, its grid and block,
+// and the tile configuration of that instantiation.  Each launcher builds its
+// plan with the plan_* function below and launches exactly that plan, and
+// sk_kernel_config reports the same plan, so the introspection cannot drift
+// from what runs.
+struct KernelPlan {
+  const void* fn = nullptr;  // the __global__ function; null: nothing to launch
+  dim3 grid = dim3(0), block = dim3(0);
+  const char* kernel = "";   // kernel family name
+  int elem = -1;             // element type it is compiled for (SK_F32/F16/BF16)
+  int head_dim = 0;          // padded head dim it is compiled for
+  int block_m = 0;           // query rows per workgroup (decode: query heads)
+  int block_n = 0;           // keys per tile (dK/dV: keys per workgroup)
+  int stages = 0;            // tile ring depth (0: tiles staged in registers)
+  bool causal = false, paged = false, rope = false;
+};
+// Launch plan k with the kernel's single parameter block.
+hipError_t run_plan(const KernelPlan& k, const void* params, hipStream_t s);
+
+KernelPlan plan_fwd_mfma(int dtype, const FwdParams& p, bool causal);
+KernelPlan plan_fwd_f32(const FwdParams& p, bool causal);
+KernelPlan plan_decode_mfma(int dtype, const DecParams& p);
+KernelPlan plan_decode_combine(int dtype, const DecParams& p);
+// The backward plans fill the block counts of p they derive.
+KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal);
+KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal);
+KernelPlan plan_bwd_dkv_f32(BwdParams& p, bool causal);
+KernelPlan plan_bwd_dq_f32(BwdParams& p, bool causal);
+
 // Launchers: return hipSuccess or the launch error.  dtype is SK_F32/F16/BF16.
 hipError_t launch_fwd_mfma(int dtype, const FwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_fwd_f32(const FwdParams& p, bool causal, hipStream_t s);

@@ -34,7 +34,7 @@ def test_header_declares_expected_api():
             "sk_decode_varlen", "sk_kv_cache_update", "sk_decode_paged",
             "sk_kv_cache_update_paged", "sk_attn_fwd_rope", "sk_decode_rope",
             "sk_decode_paged_rope", "sk_kv_cache_update_rope",
-            "sk_kv_cache_update_paged_rope"} <= names
+            "sk_kv_cache_update_paged_rope", "sk_kernel_config"} <= names
 
 
 def test_every_declared_symbol_is_exported(lib):

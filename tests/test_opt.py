@@ -1,0 +1,151 @@
+"""Device profiles and ``pick`` (the reference's ``_opt`` API for the attention
+path): a correct MI355X / gfx950 profile and fingerprint, and ``pick`` /
+``heuristic`` answers that are the library's own launch plans.  No GPU needed:
+``sk_kernel_config`` without a device query makes no HIP call."""
+
+import ctypes
+from types import SimpleNamespace
+
+import pytest
+
+from stackkernels_amd._opt import hardware as hw
+from stackkernels_amd._opt.pick import pick
+
+
+def _rocm_props(**kw):
+    base = dict(name="AMD Instinct MI355X", gcnArchName="gfx950:sramecc+:xnack-",
+                multi_processor_count=256, warp_size=64, total_memory=288 * 10**9,
+                max_threads_per_multi_processor=2048, regs_per_multiprocessor=131072,
+                shared_memory_per_block=160 * 1024, L2_cache_size=4 * 1024 * 1024)
+    base.update(kw)
+    return SimpleNamespace(**base)
+
+
+def test_mi355x_profile_and_fingerprint():
+    p = hw.mi355x_profile()
+    assert p.arch == "gfx950" and p.is_rocm and p.is_cuda
+    assert (p.sm_count, p.warp_size, p.max_smem_per_sm) == (256, 64, 160 * 1024)
+    assert p.peak_bandwidth_gbps == 8000.0 and p.peak_tflops["bf16"] == 2500.0
+    assert p.fingerprint() == f"amd-instinct-mi355x_gfx950_256cu_{288 * 10**9 // 2**20}mb"
+
+
+def test_profile_from_rocm_properties_uses_the_arch_not_the_capability():
+    # torch on ROCm reports (9, 5) for gfx950; gfx90a reports (9, 0), which the
+    # NVIDIA table would read as an H100.
+    # the runtime's generic name and half-CU register count give way to the table
+    p = hw.profile_from_properties(_rocm_props(name="AMD Radeon Graphics",
+                                               regs_per_multiprocessor=65536), (9, 5))
+    assert p.arch == "gfx950" and p.warp_size == 64 and p.sm_count == 256
+    assert p.name == "AMD Instinct MI355X" and p.max_regs_per_sm == 4 * 512 * 64
+    assert p.l2_bytes == 32 * 1024 * 1024
+    assert p.peak_bandwidth_gbps == 8000.0 and p.has_bf16
+    assert "_gfx950_256cu_" in p.fingerprint()
+    q = hw.profile_from_properties(_rocm_props(gcnArchName="gfx90a:xnack-", name="AMD MI250X",
+                                               multi_processor_count=110, warp_size=0), (9, 0))
+    assert q.arch == "gfx90a" and q.warp_size == 64 and q.peak_bandwidth_gbps is None
+    assert "H100" not in q.name
+
+
+def test_profile_from_nvidia_properties_keeps_the_reference_table():
+    props = SimpleNamespace(name="NVIDIA H100 80GB HBM3", multi_processor_count=132,
+                            total_memory=80 * 2**30, max_threads_per_multi_processor=2048)
+    p = hw.profile_from_properties(props, (9, 0))
+    assert p.arch == "" and p.warp_size == 32 and p.peak_bandwidth_gbps == 3350.0
+    assert p.fingerprint() == "nvidia-h100-80gb-hbm3_sm90_132sm_81920mb"
+
+
+def test_cpu_profile_without_gpu(monkeypatch):
+    monkeypatch.setenv("STACKKERNELS_GPU_ARCH", "cpu")
+    hw._DEVICE_PROFILE_CACHE.clear()
+    try:
+        p = hw.get_device_profile()
+        assert p.fingerprint() == "cpu" and not p.is_cuda
+        assert hw.get_hardware_info().has_gpu is False
+        assert hw.get_gpu_arch() == "cpu"
+    finally:
+        hw._DEVICE_PROFILE_CACHE.clear()
+
+
+def test_pick_decode_matches_the_launch_plan():
+    from stackkernels_amd._core.attention.decode import plan
+
+    cfg = pick("flash_decode", (64, 32, 1, 128), dtype="bfloat16", kv_len=32768, num_kv_heads=8)
+    ns, nbytes = plan(__import__("torch").bfloat16, 64, 32, 8, 32768, 128)
+    assert cfg["SPLIT_KV"] == ns > 1  # kv_len is honoured (one split in the reference)
+    assert cfg["workspace_bytes"] == nbytes
+    assert cfg["kernel_variant"] == "decode_split_kernel" and cfg["num_warps"] == 1
+    assert cfg["grid"] == ns * 64 * 8
+    assert cfg["combine"]["grid"] == 64 * 32
+    # MQA C5: the 4-wave LDS-ring kernel
+    c5 = pick("flash_decode", (8, 64, 1, 128), dtype="float16", kv_len=131072, num_kv_heads=1)
+    assert c5["kernel_variant"] == "decode_ring_kernel" and c5["num_warps"] == 4
+    assert c5["num_stages"] == 5
+    # short cache: one split, no combine pass
+    one = pick("flash_decode", (2, 8, 1, 64), kv_len=100, num_kv_heads=2)
+    assert one["SPLIT_KV"] == 1 and "combine" not in one and one["workspace_bytes"] == 0
+    # variants show in the kernel name
+    pg = pick("flash_decode", (2, 8, 1, 64), kv_len=4096, num_kv_heads=2, paged=True, rope=True)
+    assert "paged=1" in pg["kernel"] and "rope=1" in pg["kernel"]
+
+
+def test_pick_forward_and_backward():
+    f = pick("flash_attn", (4, 32, 4096, 128), dtype="bfloat16", is_causal=True)
+    assert (f["BLOCK_M"], f["BLOCK_N"], f["num_warps"], f["num_stages"]) == (256, 64, 8, 4)
+    assert f["paired_causal_blocks"] and f["grid"] == 8 * 4 * 32
+    nc = pick("flash_attention", {"batch": 4, "heads": 32, "seq_q": 4096, "head_dim": 128},
+              dtype="bfloat16")
+    assert not nc["paired_causal_blocks"] and nc["grid"] == 16 * 4 * 32
+    d256 = pick("flash_fwd", (1, 8, 512, 256), dtype="float16")
+    assert (d256["BLOCK_M"], d256["BLOCK_N"], d256["num_warps"]) == (128, 32, 4)
+    f32 = pick("flash_attn", (1, 8, 512, 64), dtype="float32")
+    assert f32["kernel_variant"] == "fwd_f32_kernel"
+    b = pick("flash_bwd", (2, 32, 2048, 128), dtype="bfloat16", kv_len=8192, num_kv_heads=8,
+             is_causal=True)
+    assert b["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_kernel"
+    assert b["grid"] == (8192 // 128) * 2 * 8 and b["dq"]["grid"] == (2048 // 128) * 2 * 32
+    assert b["workspace_bytes"] >= 2 * 2 * 32 * 2048 * 4
+
+
+def test_pick_explain_override_and_errors():
+    cfg, text = pick("flash_decode", (64, 32, 1, 128), dtype="bfloat16", kv_len=32768,
+                     num_kv_heads=8, explain=True)
+    assert "gfx950 table" in text and "decode_split_kernel<BF16, D=128" in text
+    assert f"{cfg['SPLIT_KV']} splits of {cfg['keys_per_split']} keys" in text
+    ov, text = pick("flash_decode", (8, 64, 1, 128), kv_len=131072, num_kv_heads=1,
+                    override={"SPLIT_KV": 16}, explain=True)
+    assert ov == {"SPLIT_KV": 16} and "user_override" in text and "16 splits" in text
+    assert "applied through num_splits" in text
+    _, text = pick("flash_attn", (1, 8, 128, 64), override={"BLOCK_M": 64}, explain=True)
+    assert "returned as given" in text
+    with pytest.raises(NotImplementedError, match="attention path"):
+        pick("rms_norm", (4, 1024))
+    with pytest.raises(ValueError, match="dtype"):
+        pick("flash_attn", (1, 8, 128, 64), dtype="int8")
+    with pytest.raises(NotImplementedError, match="head dim"):
+        pick("flash_attn", (1, 8, 128, 3000))  # head dim > 256 has no kernel
+    with pytest.raises(NotImplementedError):
+        pick("flash_decode", (1, 128, 1, 64), kv_len=64, num_kv_heads=1)  # group of 128
+
+
+def test_heuristics_modules():
+    from stackkernels_amd._opt.heuristics import flash_attn, flash_decode
+
+    d = flash_decode.heuristic((64, 32, 1, 128), dtype="bfloat16", kv_len=32768, num_kv_heads=8)
+    assert d["SPLIT_KV"] > 1
+    f = flash_attn.heuristic((4, 32, 4096, 128), dtype="bfloat16", is_causal=True)
+    assert f["BLOCK_M"] == 256
+
+
+def test_kernel_config_abi_errors():
+    from stackkernels_amd._core.attention import _lib
+
+    lib = _lib.load()
+    cfg = (ctypes.c_int64 * 16)()
+    assert lib.sk_kernel_config(9, 2, 1, 8, 8, 64, 64, 64, 0, 0, 0, 0, cfg, None, 0) == _lib.SK_EINVAL
+    assert "unknown op" in _lib.last_error()
+    assert lib.sk_kernel_config(0, 2, 1, 8, 3, 64, 64, 64, 0, 0, 0, 0, cfg, None, 0) == _lib.SK_EINVAL
+    assert lib.sk_kernel_config(0, 2, 1, 8, 8, 64, 64, 64, 0, 0, 0, 0, None, None, 0) == _lib.SK_EINVAL
+    assert lib.sk_kernel_config(3, 2, 1, 8, 8, 1, 64, 64, 0, 2000, 0, 0, cfg, None, 0) == _lib.SK_EINVAL
+    # no device query: device slots are -1
+    assert lib.sk_kernel_config(0, 2, 1, 8, 8, 64, 64, 64, 0, 0, 0, 0, cfg, None, 0) == _lib.SK_OK
+    assert cfg[10] == cfg[11] == cfg[12] == -1
