@@ -348,8 +348,59 @@ def _register_ops() -> bool:
     return True
 
 
+def _register_decode_ops() -> None:
+    """``torch.ops.stackkernels_amd.decode`` (every flash_decode argument, fake
+    implementation for tracing) and ``torch.ops.stackkernels.flash_decode_op``
+    (the decode counterpart of ``flash_attn_op``), so compiled graphs keep the
+    decode kernel instead of breaking at the library call.  Eager
+    ``flash_decode`` calls the launchers directly."""
+
+    @torch.library.custom_op("stackkernels_amd::decode", mutates_args=())
+    def _decode_op(
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        sm_scale: float,
+        cache_seqlens: torch.Tensor | None,
+        block_table: torch.Tensor | None,
+        rope_cos: torch.Tensor | None,
+        rope_sin: torch.Tensor | None,
+        rope_positions: torch.Tensor | None,
+        start_pos: int,
+    ) -> torch.Tensor:
+        pos = rope_positions if rope_positions is not None else start_pos
+        out = flash_decode(q, k, v, sm_scale=sm_scale, cache_seqlens=cache_seqlens,
+                           block_table=block_table, rope_cos=rope_cos, rope_sin=rope_sin,
+                           start_pos=pos)
+        # (a custom op may not return an input or a view of one)
+        return out.clone() if out.data_ptr() == q.data_ptr() else out
+
+    @_decode_op.register_fake
+    def _decode_fake(q, k, v, sm_scale, cache_seqlens, block_table, rope_cos, rope_sin,
+                     rope_positions, start_pos):
+        return torch.empty_like(q)
+
+    try:
+        torch.ops.stackkernels.flash_decode_op  # noqa: B018
+        return
+    except (AttributeError, RuntimeError):
+        pass
+    lib = torch.library.Library("stackkernels", "FRAGMENT")
+    lib.define("flash_decode_op(Tensor q, Tensor k, Tensor v, float? sm_scale, "
+               "Tensor? cache_seqlens=None) -> Tensor")
+
+    def _flash_decode_op(q, k, v, sm_scale, cache_seqlens=None):
+        scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else sm_scale
+        return torch.ops.stackkernels_amd.decode(q, k, v, scale, cache_seqlens, None, None, None,
+                                                 None, 0)
+
+    lib.impl("flash_decode_op", _flash_decode_op, "CompositeImplicitAutograd")
+    _LIBS.append(lib)
+
+
 _LIBS: list = []
 _CUSTOM_OP_REGISTERED = _register_ops()
+_register_decode_ops()
 
 
 __all__ = [

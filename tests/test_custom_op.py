@@ -99,3 +99,52 @@ def test_fake_shapes():
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
         o2 = torch.ops.stackkernels.flash_attn_op(q, k, k, True, None)
         assert o2.shape == q.shape
+
+
+# ------------------------------------------------------------ decode custom op
+
+def _decode_inputs(seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(2, 8, 1, 64, generator=g)
+    k = torch.randn(2, 2, 40, 64, generator=g)
+    v = torch.randn(2, 2, 40, 64, generator=g)
+    return q, k, v
+
+
+def test_flash_decode_op_matches_flash_decode():
+    from stackkernels_amd.torch import flash_decode
+
+    q, k, v = _decode_inputs()
+    lens = torch.tensor([40, 7])
+    torch.testing.assert_close(torch.ops.stackkernels.flash_decode_op(q, k, v, None),
+                               flash_decode(q, k, v), rtol=0, atol=0)
+    torch.testing.assert_close(torch.ops.stackkernels.flash_decode_op(q, k, v, 0.2, lens),
+                               flash_decode(q, k, v, sm_scale=0.2, cache_seqlens=lens),
+                               rtol=0, atol=0)
+
+
+def test_flash_decode_op_compiled_fullgraph():
+    from stackkernels_amd.torch import flash_decode
+
+    q, k, v = _decode_inputs(1)
+    lens = torch.tensor([33, 40])
+    fn = torch.compile(lambda a, b, c, n: torch.ops.stackkernels.flash_decode_op(a, b, c, 0.1, n),
+                       backend="aot_eager", fullgraph=True)
+    torch.testing.assert_close(fn(q, k, v, lens),
+                               flash_decode(q, k, v, sm_scale=0.1, cache_seqlens=lens),
+                               rtol=0, atol=0)
+
+
+def test_opcheck_decode_op():
+    from stackkernels_amd._reference.torch.rope import precompute_freqs
+
+    op = torch.ops.stackkernels_amd.decode.default
+    q, k, v = _decode_inputs(2)
+    lens = torch.tensor([40, 12])
+    cos, sin = precompute_freqs(64, 64)
+    torch.library.opcheck(op, (q, k, v, 0.125, lens, None, cos, sin, None, 5))
+    torch.library.opcheck(op, (q, k, v, 0.125, None, None, None, None, None, 0))
+    pool_k = torch.randn(4, 2, 32, 64)
+    pool_v = torch.randn(4, 2, 32, 64)
+    table = torch.tensor([[0, 1], [3, 2]])
+    torch.library.opcheck(op, (q, pool_k, pool_v, 0.125, lens, table, cos, sin, lens - 1, 0))

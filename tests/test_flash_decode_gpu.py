@@ -118,3 +118,17 @@ def test_config5_full_size_mqa_decode(device):
     v = (torch.rand(8, 1, 131072, 128, generator=g) * 2 - 1).half().to(device)
     out = flash_decode(q, k, v)
     assert_close_maxabs(out.float(), _ref_decode_fp32(q, k, v, 1), 2e-2, "O")
+
+
+def test_flash_decode_op_compiled_matches_eager():
+    """The decode custom op (``stackkernels::flash_decode_op``) in a compiled
+    graph runs the same kernels as eager ``flash_decode``: identical bits."""
+    q, k, v = make_qkv(4, 32, 8, 1, 4096, 128, torch.bfloat16, seed=3)
+    lens = torch.tensor([4096, 100, 1, 2500], dtype=torch.int32, device="cuda")
+    fn = torch.compile(lambda a, b, c, n: torch.ops.stackkernels.flash_decode_op(a, b, c, None, n),
+                       backend="aot_eager", fullgraph=True)
+    out = fn(q, k, v, lens)
+    ref = flash_decode(q, k, v, cache_seqlens=lens)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert native_loaded()
