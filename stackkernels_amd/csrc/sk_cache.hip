@@ -5,10 +5,10 @@
 // slot_indices) (docs/user_guide/dropout_cache_sampling.md:66-72; stub
 // modules src/stackkernels/torch/cache.py, src/stackkernels/_core/cache/kv_update.py).
 //
-// One thread moves one UNIT-byte chunk of one row of K and the same chunk of
-// V: consecutive threads walk a row's chunks, so every wave's loads and
-// stores are contiguous runs.  The slot of a token is read once per chunk
-// (it is the same for every chunk of a row, so those reads hit the cache).
+// One thread moves one UNIT-byte chunk of a new token's K row and the same
+// chunk of V, for up to four KV heads: consecutive threads walk a row's
+// chunks, so every wave's loads and stores are contiguous runs, and the
+// token's slot is read once per four heads.
 // A slot outside [0, S) skips the token, which lets callers pad ragged
 // batches with -1.  Plain byte copies: the cache holds exactly the input's
 // bits.
@@ -44,42 +44,48 @@ struct CopyUnit<2> {
   using type = uint16_t;
 };
 
+// Thread i of grid row y copies UNIT-byte chunk c of new token t of batch
+// row b, (b, t, c) = split(i), for the KV heads [kHeadsPerThread * y,
+// kHeadsPerThread * (y + 1)): the token's slot is read once for all of them.
+constexpr int kHeadsPerThread = 4;
+
 template <int UNIT>
 __global__ void __launch_bounds__(256) kv_cache_update_kernel(CacheParams p) {
   using U = typename CopyUnit<UNIT>::type;
   const int chunks = p.row_bytes / UNIT;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t rows = (int64_t)p.B * p.Hkv * p.T;
-  if (i >= rows * chunks) return;
-  const int64_t r = i / chunks;
-  const int c = (int)(i - r * chunks);
-  const int t = (int)(r % p.T);
-  const int64_t bh = r / p.T;
-  const int h = (int)(bh % p.Hkv);
-  const int b = (int)(bh / p.Hkv);
-  const int64_t slot = p.slots[(int64_t)b * p.T + t];
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < B * T * chunks (checked on the host)
+  if (i >= p.B * p.T * chunks) return;
+  const int bt = i / chunks;
+  const int c = i - bt * chunks;
+  const int b = bt / p.T;
+  const int t = bt - b * p.T;
+  const int64_t slot = p.slots[bt];
   if (slot < 0 || slot >= p.S) return;
   // Contiguous: row slot of batch row b's cache.  Paged: in-page row of a page.
   const int64_t unit = p.page_size > 0 ? slot / p.page_size : b;
   const int64_t row = p.page_size > 0 ? slot % p.page_size : slot;
   const int64_t e = p.esize;
-  const char* ks = (const char*)p.k + (b * p.k_sb + h * p.k_sh + t * p.k_ss) * e + (int64_t)c * UNIT;
-  const char* vs = (const char*)p.v + (b * p.v_sb + h * p.v_sh + t * p.v_ss) * e + (int64_t)c * UNIT;
-  char* kd = (char*)p.kc + (unit * p.kc_sb + h * p.kc_sh + row * p.kc_ss) * e + (int64_t)c * UNIT;
-  char* vd = (char*)p.vc + (unit * p.vc_sb + h * p.vc_sh + row * p.vc_ss) * e + (int64_t)c * UNIT;
-  const U kx = *reinterpret_cast<const U*>(ks);
-  const U vx = *reinterpret_cast<const U*>(vs);
-  *reinterpret_cast<U*>(kd) = kx;
-  *reinterpret_cast<U*>(vd) = vx;
+  const int h0 = blockIdx.y * kHeadsPerThread;
+#pragma unroll
+  for (int j = 0; j < kHeadsPerThread; ++j) {
+    const int h = h0 + j;
+    if (h >= p.Hkv) break;
+    const char* ks = (const char*)p.k + (b * p.k_sb + h * p.k_sh + t * p.k_ss) * e + (int64_t)c * UNIT;
+    const char* vs = (const char*)p.v + (b * p.v_sb + h * p.v_sh + t * p.v_ss) * e + (int64_t)c * UNIT;
+    char* kd = (char*)p.kc + (unit * p.kc_sb + h * p.kc_sh + row * p.kc_ss) * e + (int64_t)c * UNIT;
+    char* vd = (char*)p.vc + (unit * p.vc_sb + h * p.vc_sh + row * p.vc_ss) * e + (int64_t)c * UNIT;
+    const U kx = *reinterpret_cast<const U*>(ks);
+    const U vx = *reinterpret_cast<const U*>(vs);
+    *reinterpret_cast<U*>(kd) = kx;
+    *reinterpret_cast<U*>(vd) = vx;
+  }
 }
 
 // Rotating append.  Thread i of grid row y handles 16-byte chunk c of new
 // token t of batch row b, (b, t, c) = split(i), for the KV heads
-// [kRopeHeads * y, kRopeHeads * (y + 1)): the slot, the position and the
-// table entries are loaded once for all of them.  T: BF16 / F16 (8 elements
-// per chunk) or float (4).
-constexpr int kRopeHeads = 4;
-
+// [kHeadsPerThread * y, kHeadsPerThread * (y + 1)): the slot, the position
+// and the table entries are loaded once for all of them.  T: BF16 / F16 (8
+// elements per chunk) or float (4).
 template <class T>
 __global__ void __launch_bounds__(256) kv_cache_update_rope_kernel(CacheParams p) {
   constexpr bool kF32 = __is_same(T, float);
@@ -103,9 +109,9 @@ __global__ void __launch_bounds__(256) kv_cache_update_rope_kernel(CacheParams p
   const int rrow = rope_row(p.rope, b, t);
   float cs[EPC], sn[EPC];
   if (rrow >= 0) rope_coeffs<EPC>(p.rope, rrow, d0, cs, sn);
-  const int h0 = blockIdx.y * kRopeHeads;
+  const int h0 = blockIdx.y * kHeadsPerThread;
 #pragma unroll
-  for (int j = 0; j < kRopeHeads; ++j) {
+  for (int j = 0; j < kHeadsPerThread; ++j) {
     const int h = h0 + j;
     if (h >= p.Hkv) break;
     const E* ks = (const E*)p.k + b * p.k_sb + h * p.k_sh + t * p.k_ss;
@@ -158,7 +164,7 @@ hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s) {
     const int64_t threads = (int64_t)p.B * p.T * (p.D / epc);
     if (threads == 0) return hipSuccess;
     if (threads > 0x7fffffffLL - 255) return hipErrorInvalidConfiguration;
-    const int64_t head_groups = (p.Hkv + kRopeHeads - 1) / kRopeHeads;
+    const int64_t head_groups = (p.Hkv + kHeadsPerThread - 1) / kHeadsPerThread;
     if (head_groups > 65535) return hipErrorInvalidConfiguration;
     const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)head_groups);
     switch (p.dtype) {
@@ -169,11 +175,12 @@ hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s) {
     return hipGetLastError();
   }
   if (unit < 2) return hipErrorInvalidValue;
-  const int64_t threads = (int64_t)p.B * p.Hkv * p.T * (p.row_bytes / unit);
+  const int64_t threads = (int64_t)p.B * p.T * (p.row_bytes / unit);
   if (threads == 0) return hipSuccess;
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)blocks);
+  if (threads > 0x7fffffffLL - 255) return hipErrorInvalidConfiguration;
+  const int64_t head_groups = (p.Hkv + kHeadsPerThread - 1) / kHeadsPerThread;
+  if (head_groups > 65535) return hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)head_groups);
   switch (unit) {
     case 16: hipLaunchKernelGGL(kv_cache_update_kernel<16>, grid, dim3(256), 0, s, p); break;
     case 8: hipLaunchKernelGGL(kv_cache_update_kernel<8>, grid, dim3(256), 0, s, p); break;
