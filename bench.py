@@ -69,10 +69,10 @@ HBM_TRAFFIC_BYTES = {
     "decode": 8_612_428_279,
     "decode_mqa": 572_983_785,
     "decode_varlen": 4_305_177_417,
-    "kv_update": 67_274_953,
+    "kv_update": 67_245_869,
     "decode_paged": 4_305_404_288,
-    "decode_rope": 8_612_555_565,
-    "kv_update_rope": 75_530_834,
+    "decode_rope": 8_612_496_813,
+    "kv_update_rope": 75_531_648,
 }
 
 
