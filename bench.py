@@ -26,6 +26,12 @@ Workloads (inputs synthetic, seeded, generated on the device):
 * ``decode_rope`` -- C4 decode with the RoPE rotation of q fused into the decode
                     kernel (fp32 (Sk, D) tables, every row's query at position
                     Sk - 1).  Bytes of ``decode`` + the table rows read.
+* ``decode_step`` -- one serving decode step on the C4 cache, captured once as a HIP graph
+                    and replayed: append one token per row at its cache length
+                    (keys rotated) + decode over the grown cache (q rotated); per-row
+                    lengths U[1, Sk - 1] (seed 3), fp32 tables.  Bytes of
+                    ``decode_varlen`` over the grown rows + the append + table rows;
+                    ``details`` also gives the eager (un-captured) step time.
 * ``kv_update_rope`` -- the cache append with the new keys rotated on the way in:
                     128 tokens per row appended at seeded per-row positions
                     p_b .. p_b + 127 (slots = positions), fp32 tables.  Bytes of
@@ -108,6 +114,10 @@ WORKLOADS = {
     "decode_rope": dict(name="C4 flash_decode bf16 GQA, RoPE of q fused (fp32 tables, position "
                              "Sk-1)", B=64, Hq=32, Hkv=8, Sq=1, Sk=32768, D=128, causal=False,
                         dtype="bf16", kind="decode_rope"),
+    "decode_step": dict(name="serving decode step, C4 cache, per-row lengths U[1, Sk-1]: append "
+                             "(keys rotated) + decode (q rotated), replayed as a HIP graph", B=64,
+                        Hq=32, Hkv=8, Sq=1, Sk=32768, D=128, causal=False, dtype="bf16",
+                        kind="decode_step"),
     "kv_update_rope": dict(name="kv_cache_update bf16, RoPE of the new keys fused, C4 cache, 128 "
                                 "new tokens per row at seeded per-row positions", B=64, Hq=32,
                            Hkv=8, Sq=128, Sk=32768, D=128, causal=False, dtype="bf16",
@@ -157,8 +167,21 @@ def rope_tables(w: dict, dev):
     return precompute_freqs(w["D"], w["Sk"], device=dev)
 
 
+def step_lengths(w: dict):
+    """Cache lengths before the decode_step append: varlen_lengths capped at Sk - 1."""
+    return varlen_lengths(w).clamp(max=w["Sk"] - 1)
+
+
 def work_units(w: dict) -> tuple[float, str]:
     """Algorithmic work of one step: (FLOP or bytes, unit of the rate)."""
+    if w["kind"] == "decode_step":
+        lens = step_lengths(w).long()
+        esz, D, Hkv = 2, w["D"], w["Hkv"]
+        kv = 2 * int((lens + 1).sum()) * Hkv * D * esz    # keys each row sees after the append
+        qo = 2 * w["B"] * w["Hq"] * D * esz
+        app = 4 * w["B"] * Hkv * D * esz + w["B"] * 8      # new k, v read; cache rows written; slots
+        tab = int(lens.unique().numel()) * 2 * D * 4       # (cos, sin) rows
+        return float(kv + qo + app + tab), "GB/s"
     if w["kind"] == "decode_rope":
         base, unit = work_units(dict(w, kind="decode"))
         return base + 2 * w["D"] * 4, unit  # one (cos, sin) row pair: every query at Sk - 1
@@ -246,6 +269,35 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
                                              *sts, cos.data_ptr(), sin.data_ptr(), _lib.SK_F32,
                                              Sk, D, starts_dev.data_ptr(), 0, stream)
             _lib.check(rc, "sk_kv_cache_update_rope")
+        return launch
+    if w["kind"] == "decode_step":
+        ns = ctypes.c_int(0)
+        nb = ctypes.c_size_t(0)
+        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+                   "plan")
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+        q, k, v = inputs[0]
+        o = torch.empty_like(q)
+        g = torch.Generator(device=dev).manual_seed(7)
+        kn = torch.randn(B, Hkv, 1, D, generator=g, device=dev, dtype=q.dtype)
+        vn = torch.randn(B, Hkv, 1, D, generator=g, device=dev, dtype=q.dtype)
+        lens = step_lengths(w).to(dev)
+        lens1 = (lens + 1).contiguous()
+        slots = lens.to(torch.int64).contiguous()
+        cos, sin = rope_tables(w, dev)
+        rope = (cos.data_ptr(), sin.data_ptr(), _lib.SK_F32, Sk, D, lens.data_ptr(), 0)
+        sts = [_lib.strides3(t) for t in (q, k, v, o)]
+        sta = [_lib.strides3(t) for t in (kn, vn, k, v)]
+
+        def launch(i):
+            rc = lib.sk_kv_cache_update_rope(code, kn.data_ptr(), vn.data_ptr(), k.data_ptr(),
+                                             v.data_ptr(), slots.data_ptr(), B, Hkv, 1, Sk, D,
+                                             *sta, *rope, stream)
+            _lib.check(rc, "sk_kv_cache_update_rope")
+            rc = lib.sk_decode_rope(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), ns.value, B, Hq, Hkv, Sk, D, *sts,
+                                    lens1.data_ptr(), *rope, scale, stream)
+            _lib.check(rc, "sk_decode_rope")
         return launch
     if w["kind"] == "decode_rope":
         ns = ctypes.c_int(0)
@@ -418,6 +470,7 @@ def run_gpu(w: dict, steps: int, warmup: int):
     sets = 2 if w["name"].startswith("C5") else 1
     inputs = _make_inputs(w, torch, dev, sets)
     details: dict = {}
+    eager_fn = None
     do = None
     if w["kind"] == "fwdbwd":
         g = torch.Generator(device=dev).manual_seed(1)
@@ -460,6 +513,37 @@ def run_gpu(w: dict, steps: int, warmup: int):
         def step(i):
             q, k, v = inputs[0]
             flash_decode(q, k, v, rope_cos=cos, rope_sin=sin, start_pos=w["Sk"] - 1)
+    elif w["kind"] == "decode_step":
+        from stackkernels_amd.torch.attention import flash_decode as api_decode
+        from stackkernels_amd.torch.cache import kv_cache_update
+
+        q, kc, vc = inputs[0]
+        g = torch.Generator(device=dev).manual_seed(7)
+        kn = torch.randn(w["B"], w["Hkv"], 1, w["D"], generator=g, device=dev, dtype=q.dtype)
+        vn = torch.randn(w["B"], w["Hkv"], 1, w["D"], generator=g, device=dev, dtype=q.dtype)
+        lens = step_lengths(w).to(dev)
+        cos, sin = rope_tables(w, dev)
+        details["num_splits"] = plan(q.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        details["mean_length"] = round(float(lens.float().mean()) + 1, 1)
+
+        def eager(i):
+            kv_cache_update(kn, vn, kc, vc, lens.to(torch.int64).view(-1, 1), rope_cos=cos,
+                            rope_sin=sin, start_pos=lens)
+            return api_decode(q, kc, vc, cache_seqlens=lens + 1, rope_cos=cos, rope_sin=sin,
+                              start_pos=lens)
+
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            eager(0)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            eager(0)
+        eager_fn = eager
+
+        def step(i):
+            graph.replay()
     elif w["kind"] == "kv_update_rope":
         from stackkernels_amd.torch.cache import kv_cache_update
 
@@ -495,6 +579,8 @@ def run_gpu(w: dict, steps: int, warmup: int):
     _warm_device(torch, dev)
     ms_step, _ = _time_loop(step, steps, warmup, torch, stream)
     _, per = _time_loop(launch, steps, warmup, torch, stream, per_step=True)
+    if eager_fn is not None:  # the same step without the graph (public API calls)
+        details["eager_ms_per_step"] = round(_time_loop(eager_fn, steps, warmup, torch, stream)[0], 5)
     details["launch_ms_median"] = round(per[len(per) // 2], 5)
     details["launch_ms_min"] = round(per[0], 5)
     mean = sum(per) / len(per)
@@ -545,6 +631,21 @@ def _cpu_baseline_next_rows(w: dict, budget_s: float):
         fn = lambda: flash_decode(q, k, v, rope_cos=cos, rope_sin=sin,  # noqa: E731
                                   start_pos=n - 1)
         what = f"flash_decode reference path with RoPE of q on batch row 0 ({n} keys)"
+    elif w["kind"] == "decode_step":
+        n = int(step_lengths(w)[0])
+        q = torch.randn(1, Hq, 1, D, generator=g).bfloat16()
+        kc = torch.randn(1, Hkv, n + 1, D, generator=g).bfloat16()
+        vc = torch.randn(1, Hkv, n + 1, D, generator=g).bfloat16()
+        kn = torch.randn(1, Hkv, 1, D, generator=g).bfloat16()
+        vn = torch.randn(1, Hkv, 1, D, generator=g).bfloat16()
+        cos, sin = rope_tables(w, "cpu")
+        units_one = 2 * (n + 1) * Hkv * D * 2 + 2 * Hq * D * 2 + 4 * Hkv * D * 2 + 8 + 2 * D * 4
+
+        def fn():
+            kv_cache_update(kn, vn, kc, vc, torch.tensor([[n]]), rope_cos=cos, rope_sin=sin,
+                            start_pos=n)
+            flash_decode(q, kc, vc, rope_cos=cos, rope_sin=sin, start_pos=n)
+        what = f"append + decode reference path with RoPE on batch row 0 (length {n} + 1)"
     elif w["kind"] == "kv_update_rope":
         T = w["Sq"]
         kn = torch.randn(1, Hkv, T, D, generator=g).bfloat16()
@@ -595,7 +696,7 @@ def run_cpu_baseline(w: dict, budget_s: float):
     from stackkernels_amd._reference.torch.attention import attention_reference
 
     if w["kind"] in ("decode_varlen", "kv_update", "decode_paged", "decode_rope",
-                     "kv_update_rope"):
+                     "kv_update_rope", "decode_step"):
         return _cpu_baseline_next_rows(w, budget_s)
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
@@ -651,7 +752,9 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
               "decode_paged": "decode_split_kernel (paged) + decode_combine_kernel",
               "kv_update": "kv_cache_update_kernel",
               "decode_rope": "decode_split_kernel (q rotated on load) + decode_combine_kernel",
-              "kv_update_rope": "kv_cache_update_rope_kernel"}[w["kind"]]
+              "kv_update_rope": "kv_cache_update_rope_kernel",
+              "decode_step": "kv_cache_update_rope_kernel + decode_split_kernel (q rotated) + "
+                             "decode_combine_kernel"}[w["kind"]]
     if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
         kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
     res = {
