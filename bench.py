@@ -79,6 +79,7 @@ HBM_TRAFFIC_BYTES = {
     "decode_paged": 4_305_404_288,
     "decode_rope": 8_612_496_813,
     "kv_update_rope": 75_531_648,
+    "decode_step": 4_306_762_304,
 }
 
 
