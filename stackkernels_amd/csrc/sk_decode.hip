@@ -43,20 +43,41 @@ struct TileRows {
   const uint16_t* v;
   bool ok;
 };
+// The same, for a tile whose block-table entry the caller has read.
 template <bool PAGED>
-__device__ __forceinline__ TileRows tile_rows(const DecParams& p, const uint16_t* kbase,
-                                              const uint16_t* vbase, int b, int hkv, int n0) {
+__device__ __forceinline__ TileRows tile_rows_in(const DecParams& p, const uint16_t* kbase,
+                                                 const uint16_t* vbase, int hkv, int n0,
+                                                 int page_entry) {
   if (!PAGED) return {kbase + (int64_t)n0 * p.k_ss, vbase + (int64_t)n0 * p.v_ss, true};
   // (readfirstlane: the table entry is the same for every lane, and the
   // DMA resource built from it must sit in scalar registers.)
-  const int page =
-      __builtin_amdgcn_readfirstlane(p.block_table[(int64_t)b * p.max_pages + n0 / p.page_size]);
+  const int page = __builtin_amdgcn_readfirstlane(page_entry);
   const bool ok = page >= 0 && page < p.num_pages;
   const int64_t pg = ok ? page : 0;
   const int64_t off = n0 % p.page_size;
   return {(const uint16_t*)p.k + pg * p.k_sb + (int64_t)hkv * p.k_sh + off * p.k_ss,
           (const uint16_t*)p.v + pg * p.v_sb + (int64_t)hkv * p.v_sh + off * p.v_ss, ok};
 }
+
+template <bool PAGED>
+__device__ __forceinline__ TileRows tile_rows(const DecParams& p, const uint16_t* kbase,
+                                              const uint16_t* vbase, int b, int hkv, int n0) {
+  return tile_rows_in<PAGED>(
+      p, kbase, vbase, hkv, n0,
+      PAGED ? p.block_table[(int64_t)b * p.max_pages + n0 / p.page_size] : 0);
+}
+
+// Block-table entries of one batch row read by vector loads (counted by
+// vmcnt, like the tile loads), so a kernel can fetch a tile's page a tile
+// ahead of use without a scalar-load wait inside the tile loop.
+struct PageTable {
+  buf_rsrc rsrc;
+  int first_key, page_size;
+  __device__ __forceinline__ int entry(int n0) const {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(
+        rsrc, (uint32_t)(((n0 - first_key) / page_size) * 4), 0, 0);
+  }
+};
 
 // Q^T operand: lane holds q[hq][32*s + 8*g .. +7] (zeros past D and for
 // lanes without a head), rotated when the call carries RoPE tables and
@@ -126,10 +147,22 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   u32x4 qreg[KD];
   load_q<T>(p, b, hq, head_ok, g, qreg);
 
+  // Paged: the page of tile t + 2 is read (vector load) while tile t runs,
+  // and used when tile t + 2's loads are issued, one iteration later.
+  PageTable ptab{};
+  if constexpr (PAGED) {
+    const int first = k_lo / p.page_size * p.page_size;
+    ptab.rsrc = make_rsrc(p.block_table + (int64_t)b * p.max_pages + first / p.page_size,
+                          max(0, p.max_pages - first / p.page_size) * 4);
+    ptab.first_key = first;
+    ptab.page_size = p.page_size;
+  }
+  auto page_of = [&](int t) { return PAGED ? ptab.entry(k_lo + t * BN) : 0; };
+
   u32x4 kreg[LOADS], vreg[LOADS];
-  auto load_tile = [&](int t) {
+  auto load_tile = [&](int t, int page_entry) {
     const int n0 = k_lo + t * BN;
-    const TileRows tr = tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0);
+    const TileRows tr = tile_rows_in<PAGED>(p, kbase, vbase, hkv, n0, page_entry);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int c = tid + i * NT;
@@ -166,11 +199,17 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   const int k_off = c16 * Tile::kStride + 8 * g;
   const int v_off = (4 * g + c16 / 4) * Tile::kStride + 4 * (c16 & 3);
 
-  if (n_tiles > 0) load_tile(0);
+  int pg_cur = 0, pg_nxt = 0;  // block-table entries of tiles t and t + 1 (paged)
+  if (n_tiles > 0) {
+    pg_cur = page_of(0);
+    if (n_tiles > 1) pg_nxt = page_of(1);
+    load_tile(0, pg_cur);
+  }
   for (int t = 0; t < n_tiles; ++t) {
     store_tile();
     __syncthreads();
-    if (t + 1 < n_tiles) load_tile(t + 1);
+    const int pg_far = (PAGED && t + 2 < n_tiles) ? page_of(t + 2) : 0;
+    if (t + 1 < n_tiles) load_tile(t + 1, pg_nxt);
     const int n0 = k_lo + t * BN;
 
     f32x4 sacc[2];
@@ -183,7 +222,13 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
         sacc[kb] = mfma16<T>(a, qreg[s], sacc[kb]);
       }
     }
-    const bool tile_ok = !PAGED || tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0).ok;
+    bool tile_ok = true;
+    if constexpr (PAGED) {
+      const int page = __builtin_amdgcn_readfirstlane(pg_cur);
+      tile_ok = page >= 0 && page < p.num_pages;
+      pg_cur = pg_nxt;
+      pg_nxt = pg_far;
+    }
     if (!tile_ok || n0 + BN > k_hi) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -322,9 +367,14 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
     koff[j] = kc * 8 < p.D ? (uint32_t)((r * p.k_ss + kc * 8) * 2) : kBufferOob;
     voff[j] = vc * 8 < p.D ? (uint32_t)((r * p.v_ss + vc * 8) * 2) : kBufferOob;
   }
+  // Paged: bit t % 32 of page_ok records whether tile t's page lies in the
+  // pool, set when the tile is issued (STAGES - 1 tiles ahead), so the tile
+  // loop does not read the block table again.
+  uint32_t page_ok = 0;
   auto issue_tile = [&](int t) {
     const int n0 = k_lo + t * BN;
     const TileRows tr = tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0);
+    if (PAGED) page_ok = (page_ok & ~(1u << (t & 31))) | ((uint32_t)tr.ok << (t & 31));
     const int rows = tr.ok ? min(BN, k_hi - n0) : 0;
     // (The paged row pointers come from a table load; readfirstlane states
     // what is true -- they are wave-uniform -- so the DMA resources stay
@@ -384,7 +434,7 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
         sacc[kb] = mfma16<T>(a, qreg[s], sacc[kb]);
       }
     }
-    const bool tile_ok = !PAGED || tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0).ok;
+    const bool tile_ok = !PAGED || ((page_ok >> (t & 31)) & 1u);
     if (!tile_ok || n0 + BN > k_hi) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
