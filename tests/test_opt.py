@@ -149,3 +149,29 @@ def test_kernel_config_abi_errors():
     # no device query: device slots are -1
     assert lib.sk_kernel_config(0, 2, 1, 8, 8, 64, 64, 64, 0, 0, 0, 0, cfg, None, 0) == _lib.SK_OK
     assert cfg[10] == cfg[11] == cfg[12] == -1
+
+
+def test_memory_layout_and_workspace():
+    import torch
+
+    from stackkernels_amd._opt.memory import layout, workspace
+
+    q = torch.zeros(2, 8, 16, 80)
+    k = torch.zeros(2, 2, 32, 80)
+    assert layout.validate_attention_layout(q, k, k) == (2, 8, 2, 16, 32, 80)
+    with pytest.raises(ValueError, match="divisible"):
+        layout.validate_attention_layout(torch.zeros(2, 3, 16, 80), k, k)
+    assert [layout.get_padded_head_dim(d) for d in (16, 64, 80, 96, 128, 200)] == \
+        [64, 64, 96, 96, 128, 256]
+    with pytest.raises(ValueError):
+        layout.get_padded_head_dim(300)
+    lse = workspace.allocate_lse_buffer(2, 8, 16, "cpu")
+    assert lse.shape == (2, 8, 16) and lse.dtype == torch.float32
+    po, pl = workspace.allocate_split_kv_buffers(2, 8, 4, 128, "cpu")
+    assert po.shape == (2, 8, 4, 128) and pl.shape == (2, 8, 4)
+    ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu")
+    assert ns == 8 and ws.numel() == 64 * 32 * 8 * (128 + 1) * 4
+    ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu", num_splits=4)
+    assert ns == 4 and ws.numel() == 64 * 32 * 4 * (128 + 1) * 4
+    bw = workspace.bwd_workspace(torch.bfloat16, 2, 32, 8, 2048, 8192, 128, True, "cpu")
+    assert bw.numel() >= 2 * 2 * 32 * 2048 * 4
