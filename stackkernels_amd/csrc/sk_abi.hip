@@ -434,6 +434,7 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
   p.scale_log2 = p.scale * 1.4426950408889634f;
   p.q_sign = sm_scale < 0.f ? 0x80008000u : 0u;
   p.seqlens = seqlens;
+  p.longest_first = seqlens != nullptr && B <= 256;
   p.block_table = pc.block_table;
   p.page_size = pc.page_size, p.max_pages = pc.max_pages, p.num_pages = pc.num_pages;
   p.rope = rope;

@@ -79,6 +79,35 @@ struct PageTable {
   }
 };
 
+// Batch row with the r-th longest cache length (ties by row index), for
+// workgroup row r of the grid.  Workgroups are dispatched in grid order, so
+// handing rows out longest first lets the short rows fill in behind the long
+// ones (list scheduling, longest first) instead of leaving a few long rows to
+// run alone at the end.  Lane i ranks row c + i of each 64-row chunk against
+// every row, reading the lengths of the other rows with readlane; one ballot
+// per chunk finds the row of rank r.  O(B^2 / 64) steps per workgroup, which
+// is why the host enables it for B <= 256 only.
+__device__ __forceinline__ int row_of_rank(const DecParams& p, int r) {
+  const int lane = threadIdx.x & 63;
+  auto len = [&](int i) { return min(max(p.seqlens[i], 0), p.Sk); };
+  for (int c = 0; c < p.B; c += 64) {
+    const int i = c + lane;
+    const int li = i < p.B ? len(i) : -1;
+    int rank = 0;
+    for (int c2 = 0; c2 < p.B; c2 += 64) {
+      const int lj_v = c2 + lane < p.B ? len(c2 + lane) : -1;
+      const int n = min(64, p.B - c2);
+      for (int j = 0; j < n; ++j) {
+        const int lj = __builtin_amdgcn_readlane(lj_v, j);
+        rank += (lj > li) || (lj == li && c2 + j < i);
+      }
+    }
+    const uint64_t hit = __ballot(i < p.B && rank == r);
+    if (hit) return c + (int)__builtin_ctzll(hit);
+  }
+  return r;  // every r < B has a row
+}
+
 // Q^T operand: lane holds q[hq][32*s + 8*g .. +7] (zeros past D and for
 // lanes without a head), rotated when the call carries RoPE tables and
 // sign-flipped when sm_scale < 0 (the rotation is linear, so the order of the
@@ -124,7 +153,7 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
 
   const int split = blockIdx.x;
   const int bk = blockIdx.y;
-  const int b = bk / p.Hkv;
+  const int b = p.longest_first ? row_of_rank(p, bk / p.Hkv) : bk / p.Hkv;
   const int hkv = bk % p.Hkv;
   // Keys this row sees: all S_k, or its cache length.  With per-row lengths
   // the row's keys are spread over all its splits (32-key multiples), so a
@@ -332,7 +361,7 @@ __global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
 
   const int split = blockIdx.x;
   const int bk = blockIdx.y;
-  const int b = bk / p.Hkv;
+  const int b = p.longest_first ? row_of_rank(p, bk / p.Hkv) : bk / p.Hkv;
   const int hkv = bk % p.Hkv;
   // Keys this row sees: all S_k, or its cache length.  With per-row lengths
   // the row's keys are spread over all its splits (32-key multiples), so a

@@ -73,6 +73,9 @@ struct DecParams {
   uint32_t q_sign;
   // Null, or per-batch-row key counts: row b sees keys [0, clamp(seqlens[b], 0, Sk)).
   const int* seqlens;
+  // With seqlens: 1 hands batch rows to workgroups longest first (the
+  // kernels rank the lengths themselves; the host sets it for B <= 256).
+  int longest_first;
   // Null (k/v are (B, Hkv, Sk, D)), or a paged cache: k/v are pools of
   // num_pages pages (k_sb / v_sb is the page stride) of page_size keys, and
   // key n of row b is in-page row n % page_size of page

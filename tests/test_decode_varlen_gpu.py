@@ -93,6 +93,22 @@ def test_decode_varlen_split_counts(device, dtype, splits):
     assert_close_maxabs(out, ref, TOL[dtype], "O")
 
 
+@pytest.mark.parametrize("b", [65, 130, 256, 300])
+@pytest.mark.parametrize("group", [4, 64])
+def test_decode_varlen_many_rows(device, b, group):
+    """Many batch rows with repeated lengths: rows are handed to workgroups
+    longest first (ranked in the kernel, ties by row) up to B = 256, in grid
+    order above; every row must land in its own output slot either way."""
+    sk = 320
+    q, k, v = make_qkv(b, group, 1, 1, sk, 64, torch.bfloat16, seed=b + group)
+    g = torch.Generator().manual_seed(b)
+    lens = torch.randint(0, sk + 40, (b,), generator=g, dtype=torch.int32)
+    lens[::7] = 100  # ties
+    out = flash_decode(q, k, v, cache_seqlens=lens.to(q.device))
+    ref = orc.decode_varlen(np64(q), np64(k), np64(v), lens.numpy())
+    assert_close_maxabs(out, ref, TOL[torch.bfloat16], "O")
+
+
 def test_decode_varlen_full_lengths_equal_decode(device):
     q, k, v = make_qkv(3, 16, 4, 1, 1234, 128, torch.bfloat16, seed=3)
     full = torch.full((3,), 1234, dtype=torch.int32, device=q.device)
