@@ -74,12 +74,12 @@ HBM_TRAFFIC_BYTES = {
     "fwdbwd": 788_786_752,
     "decode": 8_612_428_279,
     "decode_mqa": 572_983_785,
-    "decode_varlen": 4_305_177_417,
+    "decode_varlen": 4_305_234_221,
     "kv_update": 67_245_869,
-    "decode_paged": 4_305_404_288,
+    "decode_paged": 4_305_401_453,
     "decode_rope": 8_612_496_813,
     "kv_update_rope": 75_531_648,
-    "decode_step": 4_306_762_304,
+    "decode_step": 4_306_767_682,
 }
 
 
