@@ -680,7 +680,10 @@ int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, 
   int64_t splits = 1, kps = 0, paired = 0;
   size_t ws = 0;
   if (op == SK_OP_FWD || (decode && dtype == SK_F32)) {
-    if (op == SK_OP_DECODE_COMBINE) return SK_OK;  // fp32 decode has no combine pass
+    if (op == SK_OP_DECODE_COMBINE) {  // fp32 decode has no combine pass
+      cfg[SK_CFG_SPLITS] = 1;
+      return SK_OK;
+    }
     sk::FwdParams p{};
     if ((rc = fwd_shape(dtype, B, Hq, Hkv, decode ? 1 : Sq, Sk, D, decode ? 0 : is_causal, &p)))
       return rc;
