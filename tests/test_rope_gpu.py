@@ -208,3 +208,23 @@ def test_forward_rope_paired_causal_blocks():
         base = flash_attention(qr, k, v, True)
     torch.cuda.synchronize()
     assert torch.equal(out, base)
+
+
+def test_forward_rope_c2_shape_equals_forward_on_rotated_q():
+    """C2 (bf16 causal MHA, B=4, H=32, S=4096, D=128): the fused rotation of q
+    in the forward gives the bits of the plain forward on the oracle-rotated q,
+    at per-row start positions."""
+    b, h, s, d = 4, 32, 4096, 128
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(31)
+    q = torch.randn(b, h, s, d, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(b, h, s, d, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(b, h, s, d, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = _tables(d, 3 * s)
+    starts = torch.tensor([0, 1, 4096, 8191 - s + 1], dtype=torch.int32)
+    with torch.no_grad():
+        out = flash_attention(q, k, v, True, rope_cos=cos, rope_sin=sin, start_pos=starts.cuda())
+        qr = _rotated(q, cos, sin, orc.rope_positions(starts.numpy(), b, s))
+        base = flash_attention(qr, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
