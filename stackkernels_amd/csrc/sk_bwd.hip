@@ -50,6 +50,8 @@
 // D = 256); 32-key K/V tiles stream through the ring; S^T = K Q^T and
 // dP^T = V dO^T give one query per lane, and dQ^T += K^T dS^T reads K^T
 // transposed from the ring.
+#include <mutex>
+
 #include "sk_common.h"
 #include "sk_kernels.h"
 
@@ -818,6 +820,40 @@ KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal) {
   return KernelPlan{};
 }
 
+// Side stream of each device for the dQ kernel, created on first use with
+// the device of the caller's stream current (default priority).
+static constexpr int kMaxDevices = 64;
+static std::mutex g_side_mu;
+static hipStream_t g_side[kMaxDevices];
+
+static hipStream_t side_stream(hipStream_t s) {
+  hipDevice_t dev = -1;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  if (g_side[dev]) return g_side[dev];
+  // Creating a stream is not a stream operation, but a caller capturing a
+  // graph gets the one-stream order until a side stream exists.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+    return nullptr;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  hipStream_t side = nullptr;
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+  const hipError_t e = hipStreamCreateWithFlags(&side, hipStreamNonBlocking);
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return nullptr;
+  g_side[dev] = side;
+  return side;
+}
+
+// dK/dV and dQ only read what the preprocess pass and the caller wrote, and
+// write disjoint outputs.  When the dK/dV grid runs more than one round of
+// workgroups, dQ runs on the device's side stream, forked from the caller's
+// stream after the preprocess pass and joined back with events: the last,
+// partly filled round of each kernel then overlaps the other kernel's work.
+// Calls from several host threads share the side stream; each call's events
+// order its own kernels.
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s) {
   if (dtype != BF16::code && dtype != F16::code) return hipErrorInvalidValue;
   BwdParams q = p;
@@ -827,9 +863,24 @@ hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream
   const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (kv.head_dim == 256 ? 2 : 1);
   const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
   if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  hipError_t e = run_plan(kv, &q, s);
-  if (e != hipSuccess) return e;
-  return run_plan(dq, &q, s);
+  hipStream_t side = g_kv > 256 && g_q > 0 ? side_stream(s) : nullptr;
+  if (!side) {
+    hipError_t e = run_plan(kv, &q, s);
+    if (e != hipSuccess) return e;
+    return run_plan(dq, &q, s);
+  }
+  hipEvent_t fork = nullptr, join = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&fork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&join, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(fork, s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(side, fork, 0);
+  if (e == hipSuccess) e = run_plan(dq, &q, side);
+  if (e == hipSuccess) e = hipEventRecord(join, side);
+  if (e == hipSuccess) e = run_plan(kv, &q, s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(s, join, 0);
+  if (fork) (void)hipEventDestroy(fork);
+  if (join) (void)hipEventDestroy(join);
+  return e;
 }
 
 }  // namespace sk
