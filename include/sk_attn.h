@@ -3,8 +3,12 @@
  *
  * Plain C: pointers, sizes and ints only.  No allocation happens inside the
  * library: every output, the backward scratch and the decode split buffer
- * are device memory that the caller owns and passes in.  All launches go on
- * the HIP stream the caller passes (NULL = the null stream); no call
+ * are device memory that the caller owns and passes in.  All work is ordered
+ * on the HIP stream the caller passes (NULL = the null stream): it starts
+ * after the work queued there before the call and ends before the work
+ * queued after it.  Every kernel goes on that stream except the backward's
+ * dQ kernel, which sk_attn_bwd may fork onto a per-device side stream of the
+ * library (created on first use) and join back with events.  No call
  * synchronises the host.  Calls are re-entrant and thread-safe.
  *
  * Tensor layout is (B, H, S, D) with D contiguous ("BHSD").  Where a call
@@ -91,7 +95,11 @@ SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int 
  * (B,Hkv,Sk,D); lse (B,Hq,Sq) fp32 as written by sk_attn_fwd.  dk and dv are
  * summed over the query heads that share a KV head.  Rows with lse = -inf
  * contribute nothing.  workspace: >= sk_attn_bwd_workspace() bytes, any
- * contents (the call initialises what it uses).
+ * contents (the call initialises what it uses).  When the dK/dV grid runs
+ * more than one round of workgroups (more than 256 workgroups), the dQ kernel
+ * runs on the library's side stream of the device, forked from `stream`
+ * after the preprocess pass and joined back into it; under graph capture the
+ * fork and the join are recorded as graph edges.
  */
 SK_API int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
                 const void* o, const float* lse, void* dq, void* dk, void* dv,
