@@ -7,9 +7,12 @@
  * on the HIP stream the caller passes (NULL = the null stream): it starts
  * after the work queued there before the call and ends before the work
  * queued after it.  Every kernel goes on that stream except the backward's
- * dQ kernel, which sk_attn_bwd may fork onto a per-device side stream of the
- * library (created on first use) and join back with events.  No call
- * synchronises the host.  Calls are re-entrant and thread-safe.
+ * dQ kernel, which sk_attn_bwd may fork onto a side stream that the library
+ * keeps for each caller stream (created on the first call on that stream
+ * that is not under graph capture) and join back with events.  No call
+ * synchronises the host.  Calls are re-entrant and thread-safe: calls on
+ * different streams share no stream, so one thread's graph capture never
+ * picks up another caller's work.
  *
  * Tensor layout is (B, H, S, D) with D contiguous ("BHSD").  Where a call
  * takes strides they are ELEMENT strides, given as int64_t[3] = {b, h, s};
@@ -97,9 +100,11 @@ SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int 
  * contribute nothing.  workspace: >= sk_attn_bwd_workspace() bytes, any
  * contents (the call initialises what it uses).  When the dK/dV grid runs
  * more than one round of workgroups (more than 256 workgroups), the dQ kernel
- * runs on the library's side stream of the device, forked from `stream`
- * after the preprocess pass and joined back into it; under graph capture the
- * fork and the join are recorded as graph edges.
+ * runs on the library's side stream for `stream`, forked from `stream` after
+ * the preprocess pass and joined back into it (also when a launch fails);
+ * under graph capture the fork and the join are recorded as graph edges.  A
+ * call under capture on a stream that has never run an eager backward keeps
+ * the one-stream order.
  */
 SK_API int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
                 const void* o, const float* lse, void* dq, void* dk, void* dv,

@@ -820,40 +820,71 @@ KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal) {
   return KernelPlan{};
 }
 
-// Side stream of each device for the dQ kernel, created on first use with
-// the device of the caller's stream current (default priority).
-static constexpr int kMaxDevices = 64;
-static std::mutex g_side_mu;
-static hipStream_t g_side[kMaxDevices];
+// Side streams for the dQ kernel, one per (device, caller stream), each with
+// its own fork and join events, created on first use with the caller's device
+// current (default priority) and kept until the process ends.  Keying by the
+// caller's stream keeps callers apart: a backward launched on one stream
+// never puts work on a side stream that another stream's call (possibly under
+// graph capture, possibly on another thread) has pulled into its capture.
+// Calls on one caller stream are already ordered by that stream; sharing its
+// side stream and events among them is safe, because a wait on an event
+// sees its latest record, which is at or after the calling thread's own.
+namespace {
+struct SideEntry {
+  int dev = -1;
+  hipStream_t caller = nullptr;
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxSides = 128;
+std::mutex g_side_mu;
+SideEntry g_side[kMaxSides];
+int g_n_side = 0;
+}  // namespace
 
-static hipStream_t side_stream(hipStream_t s) {
+// The side entry of caller stream s, or null (no fork: the one-stream order)
+// when none exists and none can be made now: s is capturing (creating
+// streams and events is not a stream operation, so a call under capture gets
+// the one-stream order until an eager call on the same stream has made the
+// entry), the table is full, or a HIP call fails.
+static const SideEntry* side_entry(hipStream_t s) {
   hipDevice_t dev = -1;
-  if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0) return nullptr;
   std::lock_guard<std::mutex> lock(g_side_mu);
-  if (g_side[dev]) return g_side[dev];
-  // Creating a stream is not a stream operation, but a caller capturing a
-  // graph gets the one-stream order until a side stream exists.
+  for (int i = 0; i < g_n_side; ++i)
+    if (g_side[i].dev == dev && g_side[i].caller == s) return &g_side[i];
+  if (g_n_side == kMaxSides) return nullptr;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
     return nullptr;
   int cur = -1;
   if (hipGetDevice(&cur) != hipSuccess) return nullptr;
-  hipStream_t side = nullptr;
   if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
-  const hipError_t e = hipStreamCreateWithFlags(&side, hipStreamNonBlocking);
+  SideEntry e;
+  e.dev = dev;
+  e.caller = s;
+  hipError_t err = hipStreamCreateWithFlags(&e.side, hipStreamNonBlocking);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&e.fork, hipEventDisableTiming);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&e.join, hipEventDisableTiming);
+  if (err != hipSuccess) {
+    if (e.join) (void)hipEventDestroy(e.join);
+    if (e.fork) (void)hipEventDestroy(e.fork);
+    if (e.side) (void)hipStreamDestroy(e.side);
+  }
   if (cur != dev) (void)hipSetDevice(cur);
-  if (e != hipSuccess) return nullptr;
-  g_side[dev] = side;
-  return side;
+  if (err != hipSuccess) return nullptr;
+  g_side[g_n_side] = e;
+  return &g_side[g_n_side++];
 }
 
 // dK/dV and dQ only read what the preprocess pass and the caller wrote, and
 // write disjoint outputs.  When the dK/dV grid runs more than one round of
-// workgroups, dQ runs on the device's side stream, forked from the caller's
-// stream after the preprocess pass and joined back with events: the last,
-// partly filled round of each kernel then overlaps the other kernel's work.
-// Calls from several host threads share the side stream; each call's events
-// order its own kernels.
+// workgroups, dQ runs on the caller stream's side stream, forked from the
+// caller's stream after the preprocess pass and joined back with events: the
+// last, partly filled round of each kernel then overlaps the other kernel's
+// work.  Once dQ is queued on the side stream, the caller's stream always
+// waits for it, also when the dK/dV launch fails, so nothing queued after the
+// call can reuse its buffers early and a capture stays joined.
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s) {
   if (dtype != BF16::code && dtype != F16::code) return hipErrorInvalidValue;
   BwdParams q = p;
@@ -863,24 +894,23 @@ hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream
   const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (kv.head_dim == 256 ? 2 : 1);
   const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
   if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  hipStream_t side = g_kv > 256 && g_q > 0 ? side_stream(s) : nullptr;
-  if (!side) {
+  const SideEntry* se = g_kv > 256 && g_q > 0 ? side_entry(s) : nullptr;
+  if (!se) {
     hipError_t e = run_plan(kv, &q, s);
     if (e != hipSuccess) return e;
     return run_plan(dq, &q, s);
   }
-  hipEvent_t fork = nullptr, join = nullptr;
-  hipError_t e = hipEventCreateWithFlags(&fork, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&join, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventRecord(fork, s);
-  if (e == hipSuccess) e = hipStreamWaitEvent(side, fork, 0);
-  if (e == hipSuccess) e = run_plan(dq, &q, side);
-  if (e == hipSuccess) e = hipEventRecord(join, side);
-  if (e == hipSuccess) e = run_plan(kv, &q, s);
-  if (e == hipSuccess) e = hipStreamWaitEvent(s, join, 0);
-  if (fork) (void)hipEventDestroy(fork);
-  if (join) (void)hipEventDestroy(join);
-  return e;
+  hipError_t e = hipEventRecord(se->fork, s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(se->side, se->fork, 0);
+  if (e != hipSuccess) return e;
+  // From here on the side stream depends on s (under capture it has joined
+  // s's capture), so it is joined back whatever fails.
+  const hipError_t e_dq = run_plan(dq, &q, se->side);
+  const hipError_t e_kv = e_dq == hipSuccess ? run_plan(kv, &q, s) : hipSuccess;
+  hipError_t e_join = hipEventRecord(se->join, se->side);
+  if (e_join == hipSuccess) e_join = hipStreamWaitEvent(s, se->join, 0);
+  if (e_dq != hipSuccess) return e_dq;
+  return e_kv != hipSuccess ? e_kv : e_join;
 }
 
 }  // namespace sk

@@ -293,10 +293,12 @@ def _register_ops() -> bool:
         out, lse = _attn_fwd_impl(q, k, v, is_causal, sm_scale)
         return out, lse
 
+    # The fakes return contiguous tensors, as the implementations do (both
+    # paths make their inputs contiguous first), whatever the inputs' strides.
     @_attn_fwd_op.register_fake
     def _attn_fwd_fake(q, k, v, is_causal, sm_scale):
         B, Hq, Sq, _ = q.shape
-        return torch.empty_like(q), q.new_empty((B, Hq, Sq), dtype=torch.float32)
+        return q.new_empty(q.shape), q.new_empty((B, Hq, Sq), dtype=torch.float32)
 
     @torch.library.custom_op("stackkernels_amd::attn_bwd", mutates_args=())
     def _attn_bwd_op(
@@ -314,7 +316,7 @@ def _register_ops() -> bool:
 
     @_attn_bwd_op.register_fake
     def _attn_bwd_fake(do, q, k, v, out, lse, is_causal, sm_scale):
-        return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
 
     def _setup_context(ctx, inputs, output):
         q, k, v, is_causal, sm_scale = inputs
@@ -378,7 +380,7 @@ def _register_decode_ops() -> None:
     @_decode_op.register_fake
     def _decode_fake(q, k, v, sm_scale, cache_seqlens, block_table, rope_cos, rope_sin,
                      rope_positions, start_pos):
-        return torch.empty_like(q)
+        return q.new_empty(q.shape)
 
     try:
         torch.ops.stackkernels.flash_decode_op  # noqa: B018

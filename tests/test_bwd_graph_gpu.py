@@ -2,8 +2,8 @@
 HIP graph capture.
 
 When the dK/dV grid runs more than one round of workgroups, ``sk_attn_bwd``
-forks the dQ kernel onto a per-device side stream after the preprocess pass
-and joins it back into the caller's stream with events.  The kernels use no
+forks the dQ kernel onto the side stream the library keeps for the caller's
+stream, after the preprocess pass, and joins it back with events.  The kernels use no
 atomics, so the result does not depend on how the two overlap: every replay
 of a captured backward (fork and join become graph edges) must equal, bit for
 bit, the eager call on the same inputs, and the eager call must match the
@@ -54,15 +54,16 @@ def test_backward_graph_replays_match_eager(dtype):
     q, k, v, do = _inputs(dtype, 1)
     out, lse = flash_attn_fwd(q, k, v, True)
 
-    # eager call first: loads the library and creates the side stream, so the
-    # capture records the fork and the join as graph edges
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
+    # eager call first, on the stream the capture will use: loads the library
+    # and creates that stream's side stream, so the capture records the fork
+    # and the join as graph edges
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
         flash_attn_bwd(do, q, k, v, out, lse, True)
-    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.current_stream().wait_stream(cap)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=cap):
         grads = flash_attn_bwd(do, q, k, v, out, lse, True)
 
     for step in range(3):
@@ -75,4 +76,69 @@ def test_backward_graph_replays_match_eager(dtype):
         graph.replay()
         torch.cuda.synchronize()
         for name, got, ref in zip(("dQ", "dK", "dV"), grads, want):
+            assert torch.equal(got, ref), f"replay {step}: {name} differs from the eager call"
+
+
+def test_capture_beside_eager_thread():
+    """One thread captures a forked backward while another runs forked
+    backwards eagerly on its own stream: neither picks up the other's work
+    (each caller stream has its own side stream).  The captured graph's
+    replays and every eager result equal a plain eager call bit for bit."""
+    import threading
+
+    dtype = torch.bfloat16
+    q, k, v, do = _inputs(dtype, 2)
+    out, lse = flash_attn_fwd(q, k, v, True)
+    want = flash_attn_bwd(do, q, k, v, out, lse, True)
+    torch.cuda.synchronize()
+
+    cap = torch.cuda.Stream()
+    eag = torch.cuda.Stream()
+    for st in (cap, eag):  # make both streams' side streams before the capture
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            flash_attn_bwd(do, q, k, v, out, lse, True)
+        torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    captured = {}
+    eager_results = []
+    errors = []
+    started = threading.Event()
+
+    def capture():
+        try:
+            with torch.cuda.graph(graph, stream=cap, capture_error_mode="thread_local"):
+                started.set()
+                captured["grads"] = flash_attn_bwd(do, q, k, v, out, lse, True)
+        except Exception as e:  # noqa: BLE001 -- reported by the main thread
+            errors.append(e)
+            started.set()
+
+    def eager():
+        try:
+            started.wait(timeout=30)
+            with torch.cuda.stream(eag):
+                for _ in range(4):
+                    eager_results.append(flash_attn_bwd(do, q, k, v, out, lse, True))
+            eag.synchronize()
+        except Exception as e:  # noqa: BLE001
+            errors.append(e)
+
+    threads = [threading.Thread(target=capture), threading.Thread(target=eager)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert len(eager_results) == 4
+    torch.cuda.synchronize()
+    for i, res in enumerate(eager_results):
+        for name, got, ref in zip(("dQ", "dK", "dV"), res, want):
+            assert torch.equal(got, ref), f"eager call {i} beside the capture: {name} differs"
+    for step in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("dQ", "dK", "dV"), captured["grads"], want):
             assert torch.equal(got, ref), f"replay {step}: {name} differs from the eager call"

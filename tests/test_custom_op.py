@@ -148,3 +148,42 @@ def test_opcheck_decode_op():
     pool_v = torch.randn(4, 2, 32, 64)
     table = torch.tensor([[0, 1], [3, 2]])
     torch.library.opcheck(op, (q, pool_k, pool_v, 0.125, lens, table, cos, sin, lens - 1, 0))
+
+
+def test_fakes_are_contiguous_for_strided_inputs():
+    """The implementations return contiguous tensors whatever the inputs'
+    strides, so the fakes must too (a stride mismatch breaks inductor)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(2, 7, 4, 32).transpose(1, 2)   # BSHD view of (2, 4, 7, 32)
+        k = torch.empty(2, 9, 2, 32).transpose(1, 2)
+        out, lse = torch.ops.stackkernels_amd.attn_fwd(q, k, k, True, 0.2)
+        assert out.is_contiguous() and lse.is_contiguous()
+        dq, dk, dv = torch.ops.stackkernels_amd.attn_bwd(q, q, k, k, out, lse, True, 0.2)
+        assert dq.is_contiguous() and dk.is_contiguous() and dv.is_contiguous()
+        qd = torch.empty(2, 1, 4, 32).transpose(1, 2)
+        od = torch.ops.stackkernels_amd.decode(qd, k, k, 0.2, None, None, None, None, None, 0)
+        assert od.is_contiguous()
+
+
+def test_flash_attn_op_inductor_transposed_inputs():
+    """torch.compile(backend='inductor', fullgraph=True), forward and backward,
+    on BSHD inputs viewed as BHSD (transposed strides)."""
+    torch.manual_seed(5)
+    qb = torch.randn(2, 16, 4, 32)   # (B, S, H, D)
+    kb = torch.randn(2, 24, 2, 32)
+    vb = torch.randn(2, 24, 2, 32)
+    do = torch.randn(2, 4, 16, 32)
+
+    def run(fn):
+        q, k, v = (t.clone().requires_grad_(True) for t in (qb, kb, vb))
+        out = fn(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+        out.backward(do)
+        return out.detach(), q.grad, k.grad, v.grad
+
+    op = lambda a, b, c: torch.ops.stackkernels.flash_attn_op(a, b, c, True, None)  # noqa: E731
+    got = run(torch.compile(op, backend="inductor", fullgraph=True))
+    want = run(op)
+    for a, b in zip(got, want):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
