@@ -29,6 +29,7 @@ from stackkernels_amd._core.attention._common import (
     stream_of,
 )
 from stackkernels_amd._core.attention.layout import validate_attention_layout
+from stackkernels_amd._core.attention.workspace import decode_workspace
 
 
 def plan(dtype: torch.dtype, b: int, hq: int, hkv: int, sk: int, d: int) -> tuple[int, int]:
@@ -71,16 +72,8 @@ def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None 
     qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k, v))
     lib = _lib.load()
     code = _lib.dtype_code(q.dtype)
-    if num_splits is None:
-        ns, nbytes = plan(q.dtype, b, hq, hkv, sk, d)
-    else:
-        ns = int(num_splits)
-        nb = ctypes.c_size_t(0)
-        _lib.check(lib.sk_decode_workspace(code, b, hq, hkv, sk, dk, ns, ctypes.byref(nb)),
-                   "flash_decode")
-        nbytes = nb.value
+    ws, ns = decode_workspace(q.dtype, b, hq, hkv, sk, dk, dev, num_splits)
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
-    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         if rope is not None:
             rc = lib.sk_decode_rope(
@@ -158,16 +151,8 @@ def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
     lib = _lib.load()
     code = _lib.dtype_code(q.dtype)
     sk = max_pages * page_size
-    if num_splits is None:
-        ns, nbytes = plan(q.dtype, b, hq, hkv, sk, d)
-    else:
-        ns = int(num_splits)
-        nb = ctypes.c_size_t(0)
-        _lib.check(lib.sk_decode_workspace(code, b, hq, hkv, sk, dk, ns, ctypes.byref(nb)),
-                   "flash_decode")
-        nbytes = nb.value
+    ws, ns = decode_workspace(q.dtype, b, hq, hkv, sk, dk, dev, num_splits)
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
-    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     paged_args = (code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(),
                   ws.data_ptr(), ws.numel(), ns, b, hq, hkv, num_pages, page_size, max_pages, dk,
                   _lib.strides3(qk), _lib.strides3(kk), _lib.strides3(vk), _lib.strides3(out),

@@ -7,8 +7,6 @@ Same contract as the reference's ``flash_attn_bwd``
 
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from stackkernels_amd._core.attention import _lib
@@ -20,6 +18,7 @@ from stackkernels_amd._core.attention._common import (
     stream_of,
 )
 from stackkernels_amd._core.attention.layout import validate_attention_layout
+from stackkernels_amd._core.attention.workspace import bwd_workspace
 
 
 def _contig(t: torch.Tensor) -> torch.Tensor:
@@ -40,10 +39,7 @@ def flash_attn_bwd(do, q, k, v, out, lse, is_causal: bool = False, sm_scale: flo
     dvv = torch.empty((b, hkv, sk, dk_), dtype=q.dtype, device=dev)
     lib = _lib.load()
     code = _lib.dtype_code(q.dtype)
-    nbytes = ctypes.c_size_t(0)
-    _lib.check(lib.sk_attn_bwd_workspace(code, b, hq, hkv, sq, sk, dk_, int(bool(is_causal)),
-                                         ctypes.byref(nbytes)), "flash_attn_bwd")
-    ws = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=dev)
+    ws = bwd_workspace(q.dtype, b, hq, hkv, sq, sk, dk_, is_causal, dev)
     with torch.cuda.device(dev):
         rc = lib.sk_attn_bwd(
             code, do_.data_ptr(), q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o_.data_ptr(),

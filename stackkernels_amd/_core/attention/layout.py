@@ -3,7 +3,9 @@
 ``validate_attention_layout`` keeps the reference's checks and ``ValueError``
 messages (``src/stackkernels/_opt/memory/layout.py:7-41``).
 ``padded_head_dim`` is this build's own rule: the gfx950 kernels are compiled
-for head dims padded to 64, 96, 128 or 256.
+for head dims padded to 64, 96, 128 or 256.  ``get_padded_head_dim`` is the
+reference's name for it (``layout.py:44-56``, where the answer is the Triton
+tile width); here it raises ``ValueError`` above 256, where no kernel exists.
 """
 
 from __future__ import annotations
@@ -40,3 +42,11 @@ def padded_head_dim(d: int) -> int:
 
 
 MAX_HEAD_DIM = 256
+
+
+def get_padded_head_dim(D: int) -> int:
+    """Head dim the kernels run ``D`` at (64, 96, 128 or 256); ValueError above 256."""
+    p = padded_head_dim(int(D))
+    if p == 0:
+        raise ValueError(f"head dim {D} > {MAX_HEAD_DIM} has no kernel")
+    return p

@@ -1,0 +1,50 @@
+"""Scratch buffers the C ABI takes, sized by the library and allocated by torch.
+
+The reference allocates its scratch in the launchers
+(``src/stackkernels/_opt/memory/workspace.py:6-46``: LSE, delta and the
+split-KV partials as separate float32 tensors).  Here the library sizes one
+byte buffer per call (``sk_attn_bwd_workspace``, ``sk_decode_plan`` /
+``sk_decode_workspace``) and never allocates; these helpers take that buffer
+from torch's caching allocator.  The launchers use them, and callers that bind
+the library directly can too.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from stackkernels_amd._core.attention import _lib
+
+
+def bwd_workspace(dtype: torch.dtype, B: int, Hq: int, Hkv: int, Sq: int, Sk: int, D: int,
+                  is_causal: bool, device) -> torch.Tensor:
+    """uint8 scratch for ``sk_attn_bwd`` (D: the kernel head dim; at least 16 bytes)."""
+    nb = ctypes.c_size_t(0)
+    _lib.check(_lib.load().sk_attn_bwd_workspace(_lib.dtype_code(dtype), B, Hq, Hkv, Sq, Sk, D,
+                                                 int(bool(is_causal)), ctypes.byref(nb)),
+               "flash_attn_bwd")
+    return torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device)
+
+
+def decode_workspace(dtype: torch.dtype, B: int, Hq: int, Hkv: int, Sk: int, D: int, device,
+                     num_splits: int | None = None) -> tuple[torch.Tensor, int]:
+    """(uint8 scratch, split count) for ``sk_decode*`` (D: the kernel head dim):
+    the gfx950 table's split count when ``num_splits`` is None, else the
+    given one."""
+    lib = _lib.load()
+    code = _lib.dtype_code(dtype)
+    nb = ctypes.c_size_t(0)
+    if num_splits is None:
+        ns = ctypes.c_int(0)
+        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+                   "flash_decode plan")
+        num_splits = ns.value
+    else:
+        _lib.check(lib.sk_decode_workspace(code, B, Hq, Hkv, Sk, D, int(num_splits),
+                                           ctypes.byref(nb)), "flash_decode")
+    return torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device), int(num_splits)
+
+
+__all__ = ["bwd_workspace", "decode_workspace"]

@@ -1,6 +1,6 @@
 """Device profiles and ``pick`` (the reference's ``_opt`` API for the attention
-path): a correct MI355X / gfx950 profile and fingerprint, and ``pick`` /
-``heuristic`` answers that are the library's own launch plans.  No GPU needed:
+path): a correct MI355X / gfx950 profile and fingerprint, and ``pick``
+answers that are the library's own launch plans.  No GPU needed:
 ``sk_kernel_config`` without a device query makes no HIP call."""
 
 import ctypes
@@ -46,24 +46,40 @@ def test_profile_from_rocm_properties_uses_the_arch_not_the_capability():
     assert "H100" not in q.name
 
 
-def test_profile_from_nvidia_properties_keeps_the_reference_table():
+def test_profile_from_other_gpu_properties():
+    # not a gfx950: the runtime's figures only, no peaks; the reference's
+    # fingerprint format with capability and SM count
     props = SimpleNamespace(name="NVIDIA H100 80GB HBM3", multi_processor_count=132,
                             total_memory=80 * 2**30, max_threads_per_multi_processor=2048)
     p = hw.profile_from_properties(props, (9, 0))
-    assert p.arch == "" and p.warp_size == 32 and p.peak_bandwidth_gbps == 3350.0
+    assert p.arch == "" and p.warp_size == 32 and p.peak_bandwidth_gbps is None
     assert p.fingerprint() == "nvidia-h100-80gb-hbm3_sm90_132sm_81920mb"
 
 
-def test_cpu_profile_without_gpu(monkeypatch):
-    monkeypatch.setenv("STACKKERNELS_GPU_ARCH", "cpu")
-    hw._DEVICE_PROFILE_CACHE.clear()
-    try:
-        p = hw.get_device_profile()
-        assert p.fingerprint() == "cpu" and not p.is_cuda
-        assert hw.get_hardware_info().has_gpu is False
-        assert hw.get_gpu_arch() == "cpu"
-    finally:
-        hw._DEVICE_PROFILE_CACHE.clear()
+def test_partitioned_gfx950_keeps_runtime_cus():
+    p = hw.profile_from_properties(_rocm_props(multi_processor_count=32, total_memory=36 * 10**9),
+                                   (9, 5))
+    assert p.name == "AMD Instinct MI355X" and p.sm_count == 32
+    assert p.fingerprint() == f"amd-instinct-mi355x_gfx950_32cu_{36 * 10**9 // 2**20}mb"
+
+
+def test_fingerprint_format_of_reference_profiles():
+    # the reference's fixture shapes (tests/fixtures/profiles.py): sm format, and "cpu"
+    t4 = hw.DeviceProfile(name="Tesla T4", compute_capability=(7, 5), sm_count=40, warp_size=32,
+                          max_regs_per_sm=65536, max_regs_per_thread=255, max_threads_per_sm=1024,
+                          max_smem_per_block=49152, max_smem_per_sm=65536, l2_bytes=4 << 20,
+                          total_memory_bytes=16 * 2**30)
+    fp = t4.fingerprint()
+    assert "tesla-t4" in fp and "sm75" in fp and "40sm" in fp
+    assert hw.host_profile().fingerprint() == "cpu"
+
+
+def test_get_device_profile_cpu_arguments():
+    import torch
+
+    for dev in ("cpu", torch.device("cpu")):
+        p = hw.get_device_profile(dev)
+        assert p.compute_capability == (0, 0) and not p.is_cuda and p.fingerprint() == "cpu"
 
 
 def test_pick_decode_matches_the_launch_plan():
@@ -127,15 +143,6 @@ def test_pick_explain_override_and_errors():
         pick("flash_decode", (1, 128, 1, 64), kv_len=64, num_kv_heads=1)  # group of 128
 
 
-def test_heuristics_modules():
-    from stackkernels_amd._opt.heuristics import flash_attn, flash_decode
-
-    d = flash_decode.heuristic((64, 32, 1, 128), dtype="bfloat16", kv_len=32768, num_kv_heads=8)
-    assert d["SPLIT_KV"] > 1
-    f = flash_attn.heuristic((4, 32, 4096, 128), dtype="bfloat16", is_causal=True)
-    assert f["BLOCK_M"] == 256
-
-
 def test_kernel_config_abi_errors():
     from stackkernels_amd._core.attention import _lib
 
@@ -151,10 +158,10 @@ def test_kernel_config_abi_errors():
     assert cfg[10] == cfg[11] == cfg[12] == -1
 
 
-def test_memory_layout_and_workspace():
+def test_layout_and_workspace():
     import torch
 
-    from stackkernels_amd._opt.memory import layout, workspace
+    from stackkernels_amd._core.attention import layout, workspace
 
     q = torch.zeros(2, 8, 16, 80)
     k = torch.zeros(2, 2, 32, 80)
@@ -165,10 +172,6 @@ def test_memory_layout_and_workspace():
         [64, 64, 96, 96, 128, 256]
     with pytest.raises(ValueError):
         layout.get_padded_head_dim(300)
-    lse = workspace.allocate_lse_buffer(2, 8, 16, "cpu")
-    assert lse.shape == (2, 8, 16) and lse.dtype == torch.float32
-    po, pl = workspace.allocate_split_kv_buffers(2, 8, 4, 128, "cpu")
-    assert po.shape == (2, 8, 4, 128) and pl.shape == (2, 8, 4)
     ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu")
     assert ns == 8 and ws.numel() == 64 * 32 * 8 * (128 + 1) * 4
     ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu", num_splits=4)

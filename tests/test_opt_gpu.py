@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 
 
 def test_device_profile_is_mi355x():
-    hw._DEVICE_PROFILE_CACHE.clear()
+    hw._PROFILES.clear()
     p = hw.get_device_profile()
     print(p)
     assert p.arch == "gfx950" and p.warp_size == 64 and p.sm_count == 256
@@ -21,7 +21,6 @@ def test_device_profile_is_mi355x():
     assert p.name == "AMD Instinct MI355X"
     assert p.fingerprint().startswith("amd-instinct-mi355x_gfx950_256cu_")
     assert hw.get_gpu_arch() == "gfx950"
-    assert hw.get_hardware_info().arch == "gfx950"
 
 
 @pytest.mark.parametrize("op,shape,kw,lds,per_cu", [
