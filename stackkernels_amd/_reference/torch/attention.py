@@ -28,7 +28,7 @@ import torch
 
 def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
     """(B, H_kv, S, D) -> (B, H_kv * n_rep, S, D); query head h reads KV head h // n_rep."""
-    return x if n_rep == 1 else x.repeat_interleave(n_rep, dim=1)
+    return x if n_rep == 1 else torch.repeat_interleave(x, repeats=n_rep, dim=1)
 
 
 def attention_reference(
@@ -45,19 +45,27 @@ def attention_reference(
     assert h_q % h_kv == 0, f"Query heads {h_q} must be divisible by KV heads {h_kv}"
     scale = 1.0 / math.sqrt(d) if sm_scale is None else sm_scale
 
+    # The reference's op sequence, op for op (same torch calls on the same
+    # operands), so a CPU caller gets the reference's results bit for bit.
+    # On a GPU the transposed key operand is made contiguous first: batched
+    # products with a transposed right operand have faulted on this
+    # platform's GPUs, and a device result is compared within tolerance only.
     group = h_q // h_kv
     qf = q.float()
     kf = repeat_kv(k, group).float()
     vf = repeat_kv(v, group).float()
-    scores = (qf @ kf.transpose(-2, -1).contiguous()) * scale
+    kt = kf.transpose(-2, -1)
+    if kt.device.type != "cpu":
+        kt = kt.contiguous()
+    scores = torch.matmul(qf, kt) * scale
     if is_causal:
-        rows = torch.arange(s_q, device=q.device)[:, None]
-        cols = torch.arange(s_k, device=q.device)[None, :]
-        hidden = cols > rows + (s_k - s_q)
-        scores = scores.masked_fill(hidden, float("-inf"))
+        rows = torch.arange(s_q, device=q.device).unsqueeze(1)
+        cols = torch.arange(s_k, device=k.device).unsqueeze(0)
+        hidden = cols > (rows + (s_k - s_q))
+        scores = scores.masked_fill(hidden.unsqueeze(0).unsqueeze(0), float("-inf"))
     lse = torch.logsumexp(scores, dim=-1)
     probs = torch.nan_to_num(torch.softmax(scores, dim=-1), nan=0.0)
-    out = (probs @ vf).to(q.dtype)
+    out = torch.matmul(probs, vf).to(q.dtype)
     return out, lse
 
 
