@@ -4,12 +4,14 @@ ragged S_q / S_k on both sides of every tile size, head dims that are any
 multiple of 8 up to 256, both masks, every dtype, scales of both signs).
 Tolerances: max-abs 1e-4 (fp32), 2e-2 (fp16/bf16) on O, 1e-3 on LSE, as
 everywhere.  The gradients of these shapes (GQA groups up to 8 summed into dK
-and dV, head dims up to 256, scale 0.3) reach magnitudes of 10-25, where a
-bf16 value's own rounding step is 0.06-0.13; their bound is therefore
-max(2e-2, 1e-2 * max|reference|), about two bf16 rounding steps of the
-largest gradient (the fixed 2e-2 is the bound for the configured shapes,
-whose gradients stay near 1).  The sizes are drawn small enough for the
-float64 oracle to finish in well under a second each.
+and dV, head dims up to 256, scales up to 1) reach magnitudes of 10-30, where
+one bf16 rounding step of the value is already 0.06-0.13, so a fixed 2e-2
+cannot hold for them; each gradient element is held instead to the error of
+the repo's fp32 reference path (autograd, gradients returned in the input
+type) plus twice the unit roundoff times the magnitude the kernel's bf16/fp16
+roundings of P, dS and the stored O can move it by (``tests/_bwd_bound.py``,
+validated on the CPU by ``tests/test_bwd_bound.py``).  The sizes are drawn
+small enough for the float64 oracle to finish in well under a second each.
 """
 
 import random
@@ -23,8 +25,10 @@ from stackkernels_amd._core.attention.flash_bwd import flash_attn_bwd
 from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
 from stackkernels_amd.torch import flash_decode
 
+from _bwd_bound import check_backward, rounding_mass
 from _gpu_util import TOL, assert_close_maxabs, assert_lse_close, make_qkv, native_loaded, np64
 from oracle import attention_oracle as orc
+from stackkernels_amd._reference.torch.attention import attention_reference
 
 pytestmark = pytest.mark.gpu
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
@@ -72,10 +76,17 @@ def test_backward_random(seed):
     g = torch.randn(out.shape, generator=torch.Generator().manual_seed(seed)).to(dtype).cuda()
     dq, dk, dv = flash_attn_bwd(g, q, k, v, out, lse, is_causal=s["causal"], sm_scale=scale)
     torch.cuda.synchronize()
-    rq, rk, rv = orc.attention_backward(np64(q), np64(k), np64(v), np64(g), s["causal"], scale)
-    for name, got, ref in (("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
-        tol = max(TOL[dtype], 1e-2 * float(np.abs(ref).max(initial=0.0)))
-        assert_close_maxabs(got, ref, tol, f"{name} {s}")
+    exact = orc.attention_backward(np64(q), np64(k), np64(v), np64(g), s["causal"], scale)
+    dt = "bf16" if dtype == torch.bfloat16 else "f16"
+    mass = rounding_mass(np64(q), np64(k), np64(v), np64(g), s["causal"], scale, dt)
+    qr, kr, vr = (t.detach().cpu().float().requires_grad_(True) for t in (q, k, v))
+    ref, _ = attention_reference(qr, kr, vr, is_causal=s["causal"], sm_scale=scale)
+    ref.backward(g.cpu().float())
+    path = [np64(t.grad.to(dtype)) for t in (qr, kr, vr)]
+    for i, (name, got) in enumerate((("dQ", dq), ("dK", dk), ("dV", dv))):
+        used = check_backward(np64(got), path[i], exact[i], mass[i], dt, f"{name} {s}")
+        print(f"{name}: max-abs {float(np.abs(np64(got) - exact[i]).max(initial=0)):.3e}, "
+              f"rounding allowance used {used:.2f}")
 
 
 @pytest.mark.parametrize("seed", range(16))
