@@ -11,9 +11,10 @@
 //   then all V stages), written by buffer_load ... lds (direct to LDS, no
 //   register staging).  Each wave issues whole 1 KiB segments; rows past S_k
 //   and head-dim padding come back as zeros from the buffer range check.
-//   One barrier per tile; K runs three tiles and V two tiles ahead of the
-//   math.  The tile loop is unrolled by the ring depth, so every LDS
-//   address is a lane-constant register plus a compile-time offset.
+//   One barrier per two tiles, each issuing the next two K and V tiles into
+//   the stages the two previous tiles freed, so every load has two tiles'
+//   time to land.  The tile loop is unrolled by the ring depth, so every
+//   LDS address is a lane-constant register plus a compile-time offset.
 // * One tile body per tile and wave: the score MFMAs of tile t+1, then the
 //   O MFMAs of tile t, with the softmax of tile t (scale/exp2, row sum,
 //   pack) and the row maximum of tile t+1 spread evenly between all of
@@ -52,6 +53,11 @@
 #include "sk_common.h"
 #include "sk_kernels.h"
 #include "sk_rope.h"
+
+// Tiles between two workgroup barriers of the forward's tile loop (1 or 2).
+#ifndef SK_FWD_SYNC_TILES
+#define SK_FWD_SYNC_TILES 2
+#endif
 
 namespace sk {
 
@@ -107,6 +113,8 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   static_assert(3 * KT + (BN - 8) * RB < 65536, "stage offsets must fit the ds immediate");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGES * KT];
+  constexpr int kSync = SK_FWD_SYNC_TILES;  // tiles per workgroup barrier
+  static_assert(kSync == 1 || kSync == 2, "one barrier per tile or per two tiles");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -233,9 +241,13 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   float l_run = 0.f;
 
   const bool wave_has_rows = mw < p.Sq;
-  auto active = [&](int t) {
-    return t < n_tiles && wave_has_rows && (!CAUSAL || t * BN <= mw + 31 + diag);
-  };
+  // Tiles [0, vis_tiles) hold keys this wave can see.
+  int vis_tiles = wave_has_rows ? n_tiles : 0;
+  if (CAUSAL) {
+    const int last_key = mw + 31 + diag;  // last key the wave's last row sees
+    vis_tiles = last_key < 0 ? 0 : min(vis_tiles, last_key / BN + 1);
+  }
+  auto active = [&](int t) { return t < vis_tiles; };
   // Group g landed for this wave (vmcnt, with group g + 1 possibly still in
   // flight), then for all (barrier); the barrier also retires every wave's
   // reads of the stages the next issue refills.
@@ -405,37 +417,71 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
     return xhalf_max(mx);
   };
 
-  // Pipeline.  Barrier t makes group t (K(t+1), V(t)) visible to every wave
-  // and retires every wave's reads of tile t-1's body, which read K(t) and
-  // V(t-1); group t+2 (K(t+3), V(t+2)) is then issued into the stages K(t-1)
-  // and V(t-2) used, so each load has two tiles' time to land.  Stage indices
-  // are tile % 4 and the loop is unrolled by 4, so they are compile-time
-  // constants.  Even tiles' scores live in s0, odd in s1.  A wave that sees
-  // tile t always computes S(t+1) in its body; on its last visible tile that
-  // result (from a stale or empty stage) is never read.
+  // Pipeline.  Stage indices are tile % 4 and the loop is unrolled by 4, so
+  // they are compile-time constants.  Even tiles' scores live in s0, odd in
+  // s1.  A wave that sees tile t always computes S(t+1) in its body; on its
+  // last visible tile that result (from a stale stage) is never read.
+  //
+  // kSync == 2 (one barrier per two tiles): barrier k (k even) makes K(k+1),
+  // K(k+2), V(k), V(k+1) visible to every wave (issued at barrier k-2, so all
+  // of this wave's loads are waited for) and retires every wave's reads of
+  // bodies k-2 and k-1 (K(k-1), K(k), V(k-2), V(k-1)); K(k+3), K(k+4),
+  // V(k+2), V(k+3) then go into exactly those stages.  Bodies k and k+1 run
+  // between barriers, and every load still has two tiles' time to land.
+  //
+  // kSync == 1 (one barrier per tile): barrier t makes group t (K(t+1), V(t))
+  // visible and retires body t-1's reads (K(t), V(t-1)); group t+2 (K(t+3),
+  // V(t+2)) is then issued into the stages K(t-1) and V(t-2) used.
   f32x16 s0[KB], s1[KB];
   auto masked = [&](int t) {
     const int n0 = t * BN;
     return n0 + BN > p.Sk || (CAUSAL && (n0 + BN - 1 > mw + diag));
   };
-  auto barrier_issue = [&](int k, int u_k) {  // barrier k; u_k = k % 4
-    sync_group(k);
-    if (k + 2 < n_tiles) {
-      issue_k((u_k + 3) % STAGES);
-      issue_v((u_k + 2) % STAGES);
+  auto barrier_issue = [&](int k, int u_k) {  // before body k; u_k = k % 4
+    if constexpr (kSync == 2) {
+      if (u_k & 1) {
+        // No barrier.  The visible-tile count goes through an empty asm so
+        // the compiler cannot tell that a skipped body k-1 implies a skipped
+        // body k and thread the two bodies' control flow together (which
+        // raises register pressure past the budget).
+        asm volatile("" : "+s"(vis_tiles));
+        __builtin_amdgcn_sched_barrier(0);
+        return;
+      }
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (k + 3 < n_tiles) issue_k((u_k + 3) % STAGES);
+      if (k + 4 < n_tiles) issue_k(u_k);
+      if (k + 2 < n_tiles) issue_v((u_k + 2) % STAGES);
+      if (k + 3 < n_tiles) issue_v((u_k + 3) % STAGES);
+    } else {
+      sync_group(k);
+      if (k + 2 < n_tiles) {
+        issue_k((u_k + 3) % STAGES);
+        issue_v((u_k + 2) % STAGES);
+      }
     }
   };
   float neg_m = 0.f;
   if (n_tiles > 0) {
-    issue_k(0);
-    issue_k(1);
-    issue_v(0);  // group 0
-    if (n_tiles > 1) {
+    if constexpr (kSync == 2) {
+      issue_k(0);
+      issue_k(1);
+      issue_v(0);
       issue_k(2);
-      issue_v(1);  // group 1
-      wait_vmcnt<2 * 2 * LK>();
+      issue_v(1);
+      wait_vmcnt<4 * LK>();  // K(0)
     } else {
-      wait_vmcnt<2 * LK>();
+      issue_k(0);
+      issue_k(1);
+      issue_v(0);  // group 0
+      if (n_tiles > 1) {
+        issue_k(2);
+        issue_v(1);  // group 1
+        wait_vmcnt<2 * 2 * LK>();
+      } else {
+        wait_vmcnt<2 * LK>();
+      }
     }
     __syncthreads();  // K(0)
     gemm0(0, s0);
