@@ -41,7 +41,7 @@ extern "C" {
 #define SK_API
 #endif
 
-#define SK_ABI_VERSION 5
+#define SK_ABI_VERSION 6
 
 /* Element type codes. */
 #define SK_F32 0
@@ -141,6 +141,28 @@ SK_API int sk_decode(int dtype, const void* q, const void* k, const void* v, voi
               const int64_t* q_strides, const int64_t* k_strides,
               const int64_t* v_strides, const int64_t* o_strides,
               float sm_scale, void* stream);
+
+/*
+ * sk_decode without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The split
+ * partials go to a static scratch array the library holds on each GPU it runs
+ * on, SK_NOALLOC_SCRATCH_BYTES per GPU until the process ends; the call itself
+ * allocates nothing.  num_splits 0 takes the gfx950 table's split count,
+ * lowered until the partials fit; an explicit split count whose partials do
+ * not fit (B * Hq * num_splits * (padded D + 1) * 4 bytes) is rejected with
+ * SK_EWORKSPACE.  fp32 runs unsplit with its B * Hq LSE values in the scratch.
+ * Every call on one GPU shares that GPU's scratch, which keeps the last call's
+ * contents: calls that overlap on one GPU (concurrent streams, threads) race
+ * and must be ordered by the caller.  Results equal sk_decode's for the same
+ * split count.
+ */
+#define SK_NOALLOC_SCRATCH_BYTES (32u << 20)
+SK_API int sk_decode_noalloc(int dtype, const void* q, const void* k, const void* v, void* o,
+                      int num_splits, int B, int Hq, int Hkv, int Sk, int D,
+                      const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides,
+                      float sm_scale, void* stream);
 
 /* Scratch bytes sk_decode needs for an explicit split count. */
 SK_API int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,

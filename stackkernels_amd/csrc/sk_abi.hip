@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "sk_attn.h"
 #include "sk_kernels.h"
@@ -461,6 +462,83 @@ int sk_decode(int dtype, const void* q, const void* k, const void* v, void* o, v
   return decode_impl(dtype, q, k, v, o, workspace, workspace_bytes, num_splits, B, Hq, Hkv, Sk, D,
                      q_strides, k_strides, v_strides, o_strides, nullptr, PagedCache{},
                      sk::RopeParams{}, sm_scale, stream);
+}
+
+}  // extern "C"
+
+// Library-held scratch of sk_decode_noalloc: SK_NOALLOC_SCRATCH_BYTES of
+// device memory, one copy on every GPU the library runs on, held until the
+// process ends.  On the host the array's name is a stand-in, not a device
+// address, so host code never passes it to a kernel or a copy: each device's
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current, and kept in g_scratch_ptr.  Every sk_decode_noalloc call on
+// a GPU shares that GPU's copy; nothing in it must start at zero (each split
+// writes its whole partial before the combine reads it), but calls that
+// overlap on one GPU race.
+static __device__ __align__(256) uint8_t scratch[SK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of the scratch copy on the device of stream s.
+int scratch_address(hipStream_t s, void** out) {
+  hipDevice_t dev = -1;
+  hipError_t e = hipStreamGetDevice(s, &dev);
+  if (e != hipSuccess) return hip_fail(e, "sk_decode_noalloc: device of the stream");
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(SK_EINVAL, "sk_decode_noalloc: device %d outside [0, %d)", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return hip_fail(e, "sk_decode_noalloc: hipGetDevice");
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return hip_fail(e, "sk_decode_noalloc: hipSetDevice");
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return hip_fail(e, "sk_decode_noalloc: hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(SK_EINVAL, "sk_decode_noalloc: no scratch address on device %d", dev);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sk_decode_noalloc(int dtype, const void* q, const void* k, const void* v, void* o,
+                      int num_splits, int B, int Hq, int Hkv, int Sk, int D,
+                      const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                      void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
+  if (rc) return rc;
+  constexpr size_t kBytes = SK_NOALLOC_SCRATCH_BYTES;
+  if (num_splits == 0 && dtype != SK_F32 && (int64_t)B * Hq > 0) {
+    // the table's split count, lowered until the partials fit the scratch
+    const size_t per_split = (size_t)B * Hq * (sk::padded_head_dim(D) + 1) * sizeof(float);
+    const int64_t fit = std::max<int64_t>(1, (int64_t)(kBytes / per_split));
+    num_splits = (int)std::min<int64_t>(plan_splits(B, Hq, Hkv, Sk, D), fit);
+  }
+  int splits = 0, kps = 0;
+  if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &splits, &kps))) return rc;
+  const size_t need = decode_ws_bytes(dtype, B, Hq, D, splits);
+  if (need > kBytes)
+    return fail(SK_EWORKSPACE,
+                "sk_decode_noalloc: %d split(s) need %zu bytes of scratch, more than the "
+                "library's %zu-byte static scratch (pass fewer splits, or use sk_decode)",
+                splits, need, kBytes);
+  void* ws = nullptr;
+  if (need > 0 && (rc = scratch_address((hipStream_t)stream, &ws))) return rc;
+  return decode_impl(dtype, q, k, v, o, ws, kBytes, splits, B, Hq, Hkv, Sk, D, q_strides,
+                     k_strides, v_strides, o_strides, nullptr, PagedCache{}, sk::RopeParams{},
+                     sm_scale, stream);
 }
 
 }  // extern "C"

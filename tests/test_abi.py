@@ -215,3 +215,21 @@ def test_rope_argument_errors(lib):
                                         st, st, st, st, 16, 16, *rope(**kw), 0.125, None)
 
     assert pdec() == _lib.SK_EINVAL and "multiple of 32" in _lib.last_error()
+
+
+def test_decode_noalloc_rejects_oversized_splits(lib):
+    """An explicit split count whose partials exceed the static scratch is
+    rejected before anything runs (no device call on this path)."""
+    from stackkernels_amd._core.attention import _lib
+
+    st = _st(1024, 128, 128)
+    # 64 x 64 heads x 64 splits x (128 + 1) x 4 bytes = 135 MB > 32 MiB
+    rc = lib.sk_decode_noalloc(2, 16, 16, 16, 16, 64, 64, 64, 8, 32768, 128, st, st, st, st, 0.1,
+                               None)
+    assert rc == _lib.SK_EWORKSPACE
+    assert "static scratch" in _lib.last_error()
+    rc = lib.sk_decode_noalloc(2, 16, 16, 16, 16, 2000, 1, 8, 2, 100, 128, st, st, st, st, 0.1,
+                               None)
+    assert rc == _lib.SK_EINVAL
+    rc = lib.sk_decode_noalloc(2, 16, 16, 16, 16, 0, 1, 6, 4, 100, 128, st, st, st, st, 0.1, None)
+    assert rc == _lib.SK_EINVAL and "divisible" in _lib.last_error()
