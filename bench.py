@@ -68,12 +68,20 @@ if ROOT not in sys.path:
 METRIC = "attn fwd/bwd TFLOP/s (% bf16 MFMA peak); flash_decode KV GB/s (% HBM peak)"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+PEAK_NOTE = {
+    "mfma": "MI355X published dense bf16/fp16 MFMA peak, 2500 TFLOP/s (256 CUs x 2.4 GHz x "
+            "4096 FLOP/clk = 2516.6 would give a fraction 0.66% lower)",
+    "hbm": "MI355X published HBM3E peak, 8000 GB/s",
+}
 
 # HBM bytes per step of each workload's kernels, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, then WRITE_SIZE; profiles/hbm_traffic_counters.md), each scaled by
 # what the same counter reads for a 1 GiB device copy (FETCH_SIZE x 2,
 # WRITE_SIZE x 1).  Counter runs cannot share a process with the timed loops,
-# so these are recorded figures of the current kernels, not live ones.
+# so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
+# kernel sources (kernel_sources_digest) the counters were measured on; when
+# the sources differ, the line reports traffic null rather than a stale figure.
+TRAFFIC_SOURCES_SHA256 = "recorded-before-digests"
 HBM_TRAFFIC_BYTES = {
     "fwd": 786_890_745,
     "fwdbwd": 788_786_752,
@@ -86,6 +94,31 @@ HBM_TRAFFIC_BYTES = {
     "kv_update_rope": 75_531_648,
     "decode_step": 4_306_767_682,
 }
+
+
+def kernel_sources_digest() -> str:
+    """SHA-256 over the HIP kernel sources and headers (sorted by name)."""
+    import hashlib
+
+    csrc = os.path.join(ROOT, "stackkernels_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()
+
+
+def recorded_traffic(key: str):
+    """(HBM bytes per step, note) for workload key: the counter figure if it was
+    measured on the current kernel sources, else (None, why)."""
+    if kernel_sources_digest() != TRAFFIC_SOURCES_SHA256:
+        return None, ("recorded counters predate the current kernel sources; re-run the "
+                      "FETCH_SIZE / WRITE_SIZE passes")
+    val = HBM_TRAFFIC_BYTES.get(key)
+    return val, ("rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated, measured on kernel sources "
+                 f"sha256 {TRAFFIC_SOURCES_SHA256[:16]}" if val else "not measured")
 
 
 def causal_pairs(sq: int, sk: int, causal: bool) -> int:
@@ -777,6 +810,7 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
               "kv_update_rope": "kv_cache_update_rope_kernel",
               "decode_step": "kv_cache_update_rope_kernel + decode_split_kernel (q rotated) + "
                              "decode_combine_kernel"}[w["kind"]]
+    traffic, traffic_note = recorded_traffic(key)
     if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
         kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
     res = {
@@ -792,8 +826,10 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
             "peak": peak,
             "unit": unit,
             "frac": round(achieved / peak, 4),
-            "traffic": HBM_TRAFFIC_BYTES.get(key),
-            "traffic_unit": "bytes per step (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
+            "peak_basis": PEAK_NOTE[bound],
+            "traffic": traffic,
+            "traffic_unit": "HBM bytes per step",
+            "traffic_note": traffic_note,
             "work_per_launch": units,
         },
         "details": details,
