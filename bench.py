@@ -811,8 +811,6 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
               "decode_step": "kv_cache_update_rope_kernel + decode_split_kernel (q rotated) + "
                              "decode_combine_kernel"}[w["kind"]]
     traffic, traffic_note = recorded_traffic(key)
-    if w["kind"] == "decode" and w["Hq"] // w["Hkv"] > 16:
-        kernel = "decode_ring_kernel + decode_combine_kernel"  # the launcher's pick for big groups
     res = {
         "workload": key,
         "config": {k_: w[k_] for k_ in ("name", "B", "Hq", "Hkv", "Sq", "Sk", "D", "causal", "dtype")},

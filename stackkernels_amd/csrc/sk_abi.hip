@@ -65,34 +65,25 @@ int check_ptr(const char* name, const void* p) {
 }
 
 // gfx950 decode split table.  A split is one workgroup per (batch, KV head);
-// the table sizes the split count to the workgroups the chip holds at once:
-// * groups of up to 16 heads: one-wave workgroups, 18 KB of LDS each, eight
-//   per CU; aim for about two rounds of them;
-// * 32- and 64-head groups (D of 64, 128 or 256): the 2- / 4-wave LDS-ring
-//   kernel, whose 5 x 16 KB stages (2 x 32 KB at D = 256) leave room for
-//   160 KB / ring bytes workgroups per CU; aim for exactly one round, so the
-//   ring stays full for the whole call and no split waits for a second
-//   round (a 64-head group writes 32 KB of partials per split, so fewer,
-//   longer splits also keep that traffic small);
-// * other head dims with large groups: the register-staged kernel.
+// the table sizes the split count to the workgroups the chip holds at once,
+// counted as eight waves per CU (16 query heads per wave: 1, 2 or 4 waves per
+// workgroup):
+// * groups of up to 16 heads (one-wave workgroups): about two rounds.  One
+//   round (C4: 4 splits) is 1.6% faster on uniform cache lengths but 6.5%
+//   slower with per-row lengths and paged pools, which take the same plan;
+// * 32- and 64-head groups: exactly one round, so no split waits for a second
+//   round; a 64-head group writes 32 KB of partials per split, so fewer,
+//   longer splits also keep that traffic small (C5: 64 splits; 32 and 128
+//   splits measured 15% and 10% slower).
 // Every split keeps at least 256 keys (8 tiles) and the count is capped at
 // 1024 (the combine kernel's LDS weight array).
 int plan_splits(int B, int Hq, int Hkv, int Sk, int D) {
+  (void)D;
   if (Sk <= 0 || B <= 0 || Hkv <= 0) return 1;
   const int group = Hq / Hkv;
-  const int dpad = sk::padded_head_dim(D);
   const int waves = group <= 16 ? 1 : group <= 32 ? 2 : 4;
-  int64_t slots;
-  int rounds;
-  if (group > 16 && (dpad == 64 || dpad == 128 || dpad == 256)) {
-    const int ring = (dpad == 256 ? 2 : 5) * 2 * 32 * dpad * 2;
-    const int per_cu = std::min(160 * 1024 / ring, 16 / waves);
-    slots = 256LL * per_cu;
-    rounds = 1;
-  } else {
-    slots = 256LL * 8 / waves;
-    rounds = 2;
-  }
+  const int64_t slots = 256LL * 8 / waves;
+  const int rounds = group <= 16 ? 2 : 1;
   const int64_t units = (int64_t)B * Hkv;
   int64_t splits = (rounds * slots + units - 1) / units;
   splits = std::min<int64_t>(splits, std::max(1, Sk / 256));

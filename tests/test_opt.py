@@ -92,10 +92,10 @@ def test_pick_decode_matches_the_launch_plan():
     assert cfg["kernel_variant"] == "decode_split_kernel" and cfg["num_warps"] == 1
     assert cfg["grid"] == ns * 64 * 8
     assert cfg["combine"]["grid"] == 64 * 32
-    # MQA C5: the 4-wave LDS-ring kernel
+    # MQA C5: four waves per workgroup share each tile; one round of 64 splits
     c5 = pick("flash_decode", (8, 64, 1, 128), dtype="float16", kv_len=131072, num_kv_heads=1)
-    assert c5["kernel_variant"] == "decode_ring_kernel" and c5["num_warps"] == 4
-    assert c5["num_stages"] == 5
+    assert c5["kernel_variant"] == "decode_split_kernel" and c5["num_warps"] == 4
+    assert c5["SPLIT_KV"] == 64 and c5["grid"] == 64 * 8
     # short cache: one split, no combine pass
     one = pick("flash_decode", (2, 8, 1, 64), kv_len=100, num_kv_heads=2)
     assert one["SPLIT_KV"] == 1 and "combine" not in one and one["workspace_bytes"] == 0

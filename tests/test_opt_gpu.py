@@ -1,8 +1,8 @@
 """On the MI355X: the device profile reads gfx950 correctly, and the
 occupancy the HIP runtime reports for the kernels ``pick`` names equals what
 the gfx950 table was sized for (one forward / dK/dV workgroup per CU, two dQ
-workgroups per CU at D <= 128, eight one-wave decode workgroups, two 4-wave
-MQA ring workgroups)."""
+workgroups per CU at D <= 128, eight one-wave decode workgroups, three 4-wave
+MQA decode workgroups)."""
 
 import pytest
 
@@ -29,7 +29,7 @@ def test_device_profile_is_mi355x():
     ("flash_decode", (64, 32, 1, 128), dict(dtype="bfloat16", kv_len=32768, num_kv_heads=8),
      None, 8),
     ("flash_decode", (8, 64, 1, 128), dict(dtype="float16", kv_len=131072, num_kv_heads=1),
-     81920, 2),
+     18432, 3),
 ])
 def test_reported_occupancy_matches_the_table(op, shape, kw, lds, per_cu):
     cfg, text = pick(op, shape, explain=True, **kw)
