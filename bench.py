@@ -164,6 +164,9 @@ WORKLOADS = {
 }
 
 
+NUM_SPLITS = 0  # --num-splits: decode split count override (0: the gfx950 table's)
+
+
 def varlen_lengths(w: dict):
     """Seeded per-row cache lengths of the decode_varlen workload, uniform in [1, Sk]."""
     import torch
@@ -409,6 +412,10 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
         nb = ctypes.c_size_t(0)
         _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
                    "plan")
+        if NUM_SPLITS:
+            ns.value = NUM_SPLITS
+            _lib.check(lib.sk_decode_workspace(code, B, Hq, Hkv, Sk, D, NUM_SPLITS,
+                                               ctypes.byref(nb)), "workspace")
         ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
         o = torch.empty_like(q0)
         st = [(_lib.strides3(q), _lib.strides3(k), _lib.strides3(v)) for q, k, v in inputs]
@@ -532,11 +539,12 @@ def run_gpu(w: dict, steps: int, warmup: int):
 
     if w["kind"] == "decode":
         q0 = inputs[0][0]
-        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        details["num_splits"] = (NUM_SPLITS or
+                                 plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0])
 
         def step(i):
             q, k, v = inputs[i % sets]
-            flash_decode(q, k, v)
+            flash_decode(q, k, v, num_splits=NUM_SPLITS or None)
     elif w["kind"] == "decode_varlen":
         q0 = inputs[0][0]
         details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
@@ -866,7 +874,12 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload (0 disables)")
+    ap.add_argument("--num-splits", type=int, default=0,
+                    help="decode / decode_mqa: run this split count instead of the table's "
+                         "(tile-table study; 0 = the table)")
     args = ap.parse_args()
+    global NUM_SPLITS
+    NUM_SPLITS = args.num_splits
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path is "
               "built and measured on a single MI355X in this build.", file=sys.stderr)

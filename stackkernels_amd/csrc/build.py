@@ -8,6 +8,7 @@ streams.  Usage: ``python -m stackkernels_amd.csrc.build`` or ``build()``.
 
 from __future__ import annotations
 
+import hashlib
 import os
 import re
 import shutil
@@ -54,7 +55,7 @@ def _hipcc() -> str:
 # Kernels that stream tiles with buffer_load ... lds and count their own loads
 # with s_waitcnt vmcnt.  A register spill would add scratch loads to that
 # count, so the waits would no longer cover the tiles: such a build is refused.
-RING_KERNELS = ("fwd_mfma_kernel", "bwd_dkv_kernel", "bwd_dq_kernel")
+RING_KERNELS = ("fwd_mfma_kernel", "bwd_dkv_kernel", "bwd_dq_kernel", "decode_ring_kernel")
 
 
 def _check_no_scratch(src: str, remarks: str) -> None:
@@ -74,17 +75,22 @@ def lib_path() -> str:
     return os.path.join(HERE, LIB_NAME)
 
 
-def build(verbose: bool = False, jobs: int = 5) -> str:
-    """Compile every HIP source for gfx950 and link ``libsk_attn.so`` next to them."""
+def build(verbose: bool = False, jobs: int = 5, defines: tuple = (), out: str | None = None) -> str:
+    """Compile every HIP source for gfx950 and link ``libsk_attn.so`` next to them.
+
+    ``defines`` (``NAME=VALUE`` strings) and ``out`` build a candidate library of
+    a tile study elsewhere (e.g. ``SK_FWD_SYNC_TILES=1``, ``SK_FWD_D128_TILE=32,4,2``);
+    load one with ``SK_ATTN_LIB=<path>``."""
     hipcc = _hipcc()
-    out_dir = os.path.join(HERE, "_build")
+    tag = hashlib.sha1(" ".join(defines).encode()).hexdigest()[:10] if defines else ""
+    out_dir = os.path.join(HERE, "_build" + (f"_{tag}" if tag else ""))
     os.makedirs(out_dir, exist_ok=True)
     objs = []
 
     def compile_one(src: str) -> str:
         obj = os.path.join(out_dir, src.replace(".hip", ".o"))
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{HERE}", "-c", os.path.join(HERE, src), "-o", obj,
-               "-Rpass-analysis=kernel-resource-usage"]
+        cmd = [hipcc, *HIPCC_FLAGS, *(f"-D{d}" for d in defines), f"-I{INCLUDE}", f"-I{HERE}", "-c",
+               os.path.join(HERE, src), "-o", obj, "-Rpass-analysis=kernel-resource-usage"]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
@@ -96,7 +102,8 @@ def build(verbose: bool = False, jobs: int = 5) -> str:
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(compile_one, SOURCES))
     tlib = _torch_lib_dir()
-    tmp = lib_path() + ".tmp"
+    target = out or lib_path()
+    tmp = target + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
            f"-L{tlib}", "-lamdhip64", f"-Wl,-rpath,{tlib}", "-Wl,--no-undefined"]
     if verbose:
@@ -104,9 +111,19 @@ def build(verbose: bool = False, jobs: int = 5) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, lib_path())
-    return lib_path()
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    import argparse
+
+    ap = argparse.ArgumentParser(description="build libsk_attn.so for gfx950")
+    ap.add_argument("-v", action="store_true", help="print the compile commands")
+    ap.add_argument("-D", dest="defines", action="append", default=[],
+                    help="NAME=VALUE macro for a tile-study candidate build (needs -o)")
+    ap.add_argument("-o", dest="out", default=None, help="output path (default: in place)")
+    a = ap.parse_args()
+    if a.defines and not a.out:
+        ap.error("a candidate build (-D) needs -o: the in-place library is the table's")
+    print(build(verbose=a.v, defines=tuple(a.defines), out=a.out))

@@ -544,13 +544,23 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
 // One workgroup per CU.  BN = 64 keeps two 32x32 score blocks per wave per
 // tile (two independent MFMA chains) while the score, operand and O
 // registers fit the 256-register budget of two waves per SIMD.
+// The D <= 128 row can be rebuilt as a candidate of the tile study (keys per
+// tile, waves, workgroups per CU): -DSK_FWD_D128_TILE=32,4,2 (4 waves, two
+// workgroups per CU) or 32,8,1; the table's entry is 64,8,1.
+#ifndef SK_FWD_D128_TILE
+#define SK_FWD_D128_TILE 64, 8, 1
+#endif
 struct FwdConfig {
   int dp, bn, nw, occ;
 };
+struct FwdTile {
+  int bn, nw, occ;
+};
+constexpr FwdTile kFwdD128{SK_FWD_D128_TILE};
 
 static FwdConfig fwd_config(int d) {
   if (d <= 64) return {64, 64, 8, 1};
-  if (d <= 128) return {128, 64, 8, 1};
+  if (d <= 128) return {128, kFwdD128.bn, kFwdD128.nw, kFwdD128.occ};
   return {256, 32, 4, 1};
 }
 
@@ -590,7 +600,7 @@ static KernelPlan plan_fwd_dt(const FwdParams& p, bool causal) {
     case 64:
       return plan_fwd_t<T, 64, 64, 8, 1>(p, causal);
     case 128:
-      return plan_fwd_t<T, 128, 64, 8, 1>(p, causal);
+      return plan_fwd_t<T, 128, kFwdD128.bn, kFwdD128.nw, kFwdD128.occ>(p, causal);
     default:
       return plan_fwd_t<T, 256, 32, 4, 1>(p, causal);
   }
