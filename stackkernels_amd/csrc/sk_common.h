@@ -19,6 +19,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// On a lambda whose callers pass it register arrays by reference: inlining
+// keeps those arrays in registers.
+#define SK_INLINE __attribute__((always_inline))
+
 namespace sk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
