@@ -1060,11 +1060,21 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
 //          D <= 128.
 // dQ kernel table by padded head dim: key tile, workgroups per CU, and
 // whether a wave interleaves its own softmax with the next tile's MFMAs.
+// SK_BWD_DQ_TILE (key tile, workgroups per CU, interleave) overrides the
+// D <= 128 row for candidate builds.
+#ifndef SK_BWD_DQ_TILE
+#define SK_BWD_DQ_TILE 32, 2, false
+#endif
+struct DqTile {
+  int bn, occ;
+  bool pipe;
+};
+constexpr DqTile kDqSmall{SK_BWD_DQ_TILE};
 template <int DP>
 struct DqConfig {
-  static constexpr int kBn = 32;
-  static constexpr int kOcc = 2;
-  static constexpr bool kPipe = false;
+  static constexpr int kBn = kDqSmall.bn;
+  static constexpr int kOcc = kDqSmall.occ;
+  static constexpr bool kPipe = kDqSmall.pipe;
 };
 template <>
 struct DqConfig<256> {

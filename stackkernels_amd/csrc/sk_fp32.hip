@@ -137,33 +137,52 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
 //   delta[r]    = sum_d dO[r,d] * O[r,d]          (reference flash_bwd.py:15-55)
 //   lse_log2[r] = lse[r] * log2(e), or +inf where lse = -inf so that
 //                 exp2(s - lse_log2) is exactly 0 on rows that see no key.
+// Sixteen lanes per row, each reading 16-byte chunks of dO and O (D is a
+// multiple of 8 and rows start 16-byte aligned), so a wave's loads cover
+// four whole rows; the lanes' partial sums meet in a butterfly.
 template <class T>
-__device__ __forceinline__ float ld_elem(const void* p, int64_t i);
+__device__ __forceinline__ float dot_chunk(u32x4 a, u32x4 b, float x);
 template <>
-__device__ __forceinline__ float ld_elem<float>(const void* p, int64_t i) {
-  return ((const float*)p)[i];
+__device__ __forceinline__ float dot_chunk<float>(u32x4 a, u32x4 b, float x) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x = fmaf(__uint_as_float(a[e]), __uint_as_float(b[e]), x);
+  return x;
 }
-template <>
-__device__ __forceinline__ float ld_elem<BF16>(const void* p, int64_t i) {
-  return to_f32<BF16>(((const uint16_t*)p)[i]);
-}
-template <>
-__device__ __forceinline__ float ld_elem<F16>(const void* p, int64_t i) {
-  return to_f32<F16>(((const uint16_t*)p)[i]);
+template <class T>
+__device__ __forceinline__ float dot_chunk(u32x4 a, u32x4 b, float x) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x = fmaf(to_f32<T>((uint16_t)(a[e] & 0xffffu)), to_f32<T>((uint16_t)(b[e] & 0xffffu)), x);
+    x = fmaf(to_f32<T>((uint16_t)(a[e] >> 16)), to_f32<T>((uint16_t)(b[e] >> 16)), x);
+  }
+  return x;
 }
 
 template <class T>
+constexpr int kElemBytes = 2;
+template <>
+constexpr int kElemBytes<float> = 4;
+
+template <class T>
 __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
+  constexpr int kRowLanes = 16;
+  constexpr int esize = kElemBytes<T>;
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  const int64_t r = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
-  const int part = threadIdx.x & 3;
+  const int64_t r = (int64_t)blockIdx.x * (256 / kRowLanes) + (threadIdx.x / kRowLanes);
+  const int j = threadIdx.x % kRowLanes;
   float x = 0.f;
   if (r < rows) {
-    const int64_t base = r * p.D;
-    for (int d = part; d < p.D; d += 4) x = fmaf(ld_elem<T>(p.dout, base + d), ld_elem<T>(p.o, base + d), x);
+    const int64_t base = r * p.D * esize;
+    const uint8_t* g = (const uint8_t*)p.dout + base;
+    const uint8_t* o = (const uint8_t*)p.o + base;
+    const int chunks = p.D * esize / 16;
+    for (int c = j; c < chunks; c += kRowLanes)
+      x = dot_chunk<T>(*reinterpret_cast<const u32x4*>(g + 16 * c),
+                       *reinterpret_cast<const u32x4*>(o + 16 * c), x);
   }
-  x = quad_sum(x);
-  if (r < rows && part == 0) {
+#pragma unroll
+  for (int m = kRowLanes / 2; m > 0; m >>= 1) x += __shfl_xor(x, m);
+  if (r < rows && j == 0) {
     p.delta[r] = x;
     const float l = p.lse[r];
     p.lse_log2[r] = l == kNegInf ? __builtin_inff() : l * kLog2e;
@@ -351,7 +370,7 @@ hipError_t launch_fwd_f32(const FwdParams& p, bool causal, hipStream_t s) {
 
 hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  const dim3 grid((unsigned)((rows + 63) / 64));
+  const dim3 grid((unsigned)((rows + 15) / 16));
   if (dtype == 0)
     hipLaunchKernelGGL((bwd_prep_kernel<float>), grid, dim3(256), 0, s, p);
   else if (dtype == BF16::code)
