@@ -54,6 +54,13 @@
 
 #include "sk_common.h"
 
+// dQ schedule 2: row-operand and transposed-operand read leads (MFMA slots).
+#ifndef SK_DQ_KL
+#define SK_DQ_KL 3
+#endif
+#ifndef SK_DQ_XL
+#define SK_DQ_XL 4
+#endif
 // dK/dV ring depth at D = 128: 6 (pipelined schedule) or 4.
 #ifndef SK_BWD_DKV_STAGES
 #define SK_BWD_DKV_STAGES 6
@@ -764,7 +771,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
-template <class T, int DP, int BN, int NW, int STAGES, int OCC, bool PIPE, bool CAUSAL>
+template <class T, int DP, int BN, int NW, int STAGES, int OCC, int MODE, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
   using L = BwdTile<DP, BN>;  // K and V tiles
   constexpr int BM = 32 * NW;
@@ -995,7 +1002,110 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
   // (past its rows' diagonal or past S_k) are masked, not skipped: their dS
   // is exactly zero.  Waves with no rows (past S_q) compute unused values.
   f32x16 s0[KB], p0[KB], s1[KB], p1[KB];
-  if constexpr (PIPE) {
+  if constexpr (MODE == 2) {
+    // S^T one tile ahead, dP^T in step: step t runs the dP^T MFMAs of tile t
+    // with P(t) = exp2(S^T(t)...) between them, then the S^T MFMAs of tile
+    // t+1 with dS(t) = P(t) (dP(t) - delta) between them, then dQ^T += K^T
+    // dS^T of tile t, its transposed K reads XL slots ahead.  Three score
+    // tiles are live (S^T of t and t+1, dP^T of t) instead of four.
+    static_assert(KB == 1, "one 32-key block per tile");
+    constexpr int NP = KD;           // dP^T MFMAs (slots 0 .. NP-1)
+    constexpr int NSN = KD;          // S^T MFMAs of the next tile
+    constexpr int NQ = DB * KN;      // dQ^T MFMAs
+    constexpr int KL = SK_DQ_KL, XL = SK_DQ_XL;
+    constexpr int NE = KN * 8;       // elements per lane and tile
+    // element x: FMA at pa(x), exp2 at pa(x) + 1; dS at pb(x); pack of
+    // elements 8g..8g+7 one slot after the last of them
+    auto pa = [](int x) { return (x * NP) / NE; };
+    auto pb = [](int x) { return NP + 1 + (x * (NSN + DB - 5)) / NE; };
+    auto pk_slot = [&](int g) { return pb(8 * g + 7) + 1; };
+    static_assert(NE == 16 && KN == 2, "two packed k-steps per tile");
+    // P(t) overwrites S^T(t) and dS(t) overwrites dP^T(t) in place.
+    // su = t % STAGES, a compile-time constant in the unrolled loop, so every
+    // LDS address is a lane-constant register plus an immediate.
+    auto body = [&](int su, f32x16& cs, f32x16& ns, bool next) SK_INLINE {
+      const uint8_t* st = smem + su * kStageBytes;
+      const uint8_t* sn = smem + ((su + 1) & (STAGES - 1)) * kStageBytes;
+      f32x16 dp = f32x16{};
+      u32x4 a[NP + NSN];
+      u32x4 kt[NQ];
+      auto addr = [&](int i) {
+        return i < NP ? st + L::kTileBytes + k_lds[i] : sn + k_lds[i - NP];
+      };
+      auto read_kt = [&](int m) {
+        const int s2 = m / DB, c = m % DB;
+        kt[m] = lds_tr_pair(st + 16 * s2 * RB + kt_lo[c], st + 16 * s2 * RB + kt_hi[c]);
+      };
+#pragma unroll
+      for (int i = 0; i < KL; ++i) a[i] = lds_b128(addr(i));
+      ns = f32x16{};
+#pragma unroll
+      for (int i = 0; i < NP + NSN + NQ; ++i) {
+        if (i + KL < NP + NSN && (next || i + KL < NP)) a[i + KL] = lds_b128(addr(i + KL));
+#pragma unroll
+        for (int m = 0; m < NQ; ++m)
+          if (NP + NSN + m - XL == i) read_kt(m);
+        if (i < NP) {
+          dp = mfma32<T>(a[i], greg[i], dp);
+        } else if (i < NP + NSN) {
+          if (next) ns = mfma32<T>(a[i], qreg[i - NP], ns);
+        } else {
+          const int m = i - NP - NSN, s2 = m / DB, c = m % DB;
+          dqacc[c] = mfma32<T>(kt[m], dsk[s2], dqacc[c]);
+        }
+#pragma unroll
+        for (int x = 0; x < NE; ++x) {
+          if (pa(x) == i) cs[x] = fmaf(cs[x], c_log2, -lse2);
+          if (pa(x) + 1 == i) cs[x] = fast_exp2(cs[x]);
+          if (pb(x) == i) dp[x] = cs[x] * (dp[x] - dl);
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+          if (pk_slot(g) == i)
+            dsk[g] = u32x4{pack2<T>(dp[8 * g], dp[8 * g + 1]), pack2<T>(dp[8 * g + 2], dp[8 * g + 3]),
+                           pack2<T>(dp[8 * g + 4], dp[8 * g + 5]), pack2<T>(dp[8 * g + 6], dp[8 * g + 7])};
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    static_assert(pb(7) + 1 < NP + NSN && pb(15) + 1 < NP + NSN + DB,
+                  "dS^T packed before its dQ^T MFMAs");
+    if (n_tiles > 0) {
+      sync_tile(0, PD);
+      s0[0] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KD; ++s) s0[0] = mfma32<T>(lds_b128(stage(0) + k_lds[s]), qreg[s], s0[0]);
+    }
+    // Tiles with a successor run in a loop unrolled by the ring depth; the
+    // last tile (no S^T ahead) runs once after it, its stage and score
+    // registers chosen at run time.
+    auto iteration = [&](int t, int su, f32x16 (&cs)[KB], f32x16 (&ns)[KB]) SK_INLINE {
+      premask(t, cs);
+      sync_tile(t + 1, PD - 1);
+      if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
+      body(su, cs[0], ns[0], true);
+    };
+    const int n_main = n_tiles - 1;
+    for (int t0 = 0; t0 < n_main; t0 += STAGES) {
+#pragma unroll
+      for (int u = 0; u < STAGES; ++u) {
+        if (t0 + u >= n_main) break;
+        if (u & 1)
+          iteration(t0 + u, u, s1, s0);
+        else
+          iteration(t0 + u, u, s0, s1);
+      }
+    }
+    if (n_main >= 0) {
+      auto last = [&](f32x16 (&cs)[KB], f32x16 (&ns)[KB]) SK_INLINE {
+        premask(n_main, cs);
+        body(n_main & (STAGES - 1), cs[0], ns[0], false);
+      };
+      if (n_main & 1)
+        last(s1, s0);
+      else
+        last(s0, s1);
+    }
+  } else if constexpr (MODE == 1) {
     // Fixed register roles: even tiles in s0/p0, odd tiles in s1/p1.
     if (n_tiles > 0) {
       sync_tile(0, PD);
@@ -1054,33 +1164,35 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
 //   dK/dV: 8 waves, one workgroup per CU, 128 keys per workgroup, 32-query
 //          tiles (at D = 256 the output head dim is split over two
 //          workgroups); LDS ring 4 x (Q + dO + stats) + P exchange
-//          = 72 / 104 / 152 KiB.
+//          = 72 / 104 / 152 KiB, at D = 128 6 x (Q + dO + stats) + P
+//          exchange = 140 KiB.
 //   dQ:    4 waves, 128 query rows per workgroup, 32-key tiles; ring
 //          4 x (K + V) = 32 / 64 / 128 KiB, so two workgroups fit a CU at
 //          D <= 128.
-// dQ kernel table by padded head dim: key tile, workgroups per CU, and
-// whether a wave interleaves its own softmax with the next tile's MFMAs.
-// SK_BWD_DQ_TILE (key tile, workgroups per CU, interleave) overrides the
-// D <= 128 row for candidate builds.
+// dQ kernel table by padded head dim: key tile, workgroups per CU, and the
+// schedule of a wave's MFMA and VALU work.
+// SK_BWD_DQ_TILE (key tile, workgroups per CU, schedule) overrides the
+// D <= 128 row for candidate builds.  Schedules: 0 tiles in order (the other
+// wave of the SIMD overlaps the VALU work), 1 S^T and dP^T one tile ahead,
+// 2 S^T one tile ahead and dP^T in step.
 #ifndef SK_BWD_DQ_TILE
-#define SK_BWD_DQ_TILE 32, 2, false
+#define SK_BWD_DQ_TILE 32, 2, 2
 #endif
 struct DqTile {
-  int bn, occ;
-  bool pipe;
+  int bn, occ, mode;
 };
 constexpr DqTile kDqSmall{SK_BWD_DQ_TILE};
 template <int DP>
 struct DqConfig {
   static constexpr int kBn = kDqSmall.bn;
   static constexpr int kOcc = kDqSmall.occ;
-  static constexpr bool kPipe = kDqSmall.pipe;
+  static constexpr int kMode = kDqSmall.mode;
 };
 template <>
 struct DqConfig<256> {
   static constexpr int kBn = 32;
   static constexpr int kOcc = 1;
-  static constexpr bool kPipe = false;
+  static constexpr int kMode = 0;
 };
 
 template <class T, int DP, int DO>
@@ -1115,8 +1227,8 @@ static KernelPlan plan_dq_t(BwdParams& p, bool causal) {
   using QC = DqConfig<DP>;
   p.n_mblocks = (p.Sq + 32 * NW - 1) / (32 * NW);
   KernelPlan k;
-  k.fn = causal ? (const void*)bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, true>
-                : (const void*)bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kPipe, false>;
+  k.fn = causal ? (const void*)bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kMode, true>
+                : (const void*)bwd_dq_kernel<T, DP, QC::kBn, NW, STAGES, QC::kOcc, QC::kMode, false>;
   k.grid = dim3((unsigned)((int64_t)p.n_mblocks * p.B * p.Hq));
   k.block = dim3(NW * 64);
   k.kernel = "bwd_dq_kernel";
