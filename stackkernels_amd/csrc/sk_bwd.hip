@@ -61,6 +61,15 @@
 #ifndef SK_DQ_XL
 #define SK_DQ_XL 4
 #endif
+// dK/dV pipelined schedule: statistics broadcast by DPP (1) or read per lane (0).
+#ifndef SK_BWD_STAT_DPP
+#define SK_BWD_STAT_DPP 0
+#endif
+// dK/dV pipelined schedule: first row operands of a step read before its
+// barrier (1) or after it (0).
+#ifndef SK_BWD_DKV_PRELOAD
+#define SK_BWD_DKV_PRELOAD 1
+#endif
 // dK/dV ring depth at D = 128: 6 (pipelined schedule) or 4.
 #ifndef SK_BWD_DKV_STAGES
 #define SK_BWD_DKV_STAGES 6
@@ -294,6 +303,12 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // key group's P blocks (block kb at +kb*kPBlock; 16-byte chunk k of every
   // lane at +1024*k).
   const int stat_lds = kSReg + wave * 256 + 16 * hl;
+  // The same statistics one float per lane: lane L holds query row
+  // 8*((L%16)/4) + L%4 + 4*hl, so within each 16-lane row of the wave lane r
+  // holds the row of result register r, and a DPP row broadcast of lane r
+  // hands every lane its register-r statistic.
+  const int stat_lds1 = kSReg + wave * 256 + 4 * (8 * ((lane & 15) >> 2) + (lane & 3) + 4 * hl);
+  auto ldf1 = [&](int addr) { return *reinterpret_cast<const float*>(smem + addr); };
   const int p_lds = kPReg + KB * kg * kPBlock + lane * 16;
   const float c_log2 = p.abs_scale_log2;
 
@@ -462,6 +477,19 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   constexpr int XL = 4;                // transposed-operand read lead
   constexpr int SL = 2;                // statistics / P read lead
   constexpr int F0 = NS >= 8 ? 1 : 0;  // first softmax / dS slot
+  // Statistics by one 4-byte read per lane and DPP row broadcasts (else four
+  // 16-byte reads per lane).
+  constexpr bool kStatDpp = SK_BWD_STAT_DPP;
+  // Preloaded step start: barrier j waits for tile j+2, so at the end of
+  // step j a wave already reads the first KLP row operands of step j+1 (role
+  // 0: Q(j+2), role 1: dO(j+1)) and its MFMAs start right after the next
+  // barrier; the DMA of tile j+4 is issued at slot kIssSlot, after the
+  // step's first MFMAs, instead of right after the barrier.
+  constexpr bool kPre = SK_BWD_DKV_PRELOAD;
+  constexpr int KLP = (KL + KB - 1) / KB;  // row operands read before slot 0
+  constexpr int kIssSlot = 2;
+  constexpr int kPreSlot = NS + 1;
+  u32x4 pre[KLP];
   // Pair t in consumption order: (s2, kb, g) with t = 4 (s2 KB + kb) + g % 4
   // and g the pair of elements 2g, 2g+1 of key block kb (g / 4 = s2).  Group
   // u = t / 4 feeds accumulate slot NS + u DB; pair t starts (FMA) at slot
@@ -483,13 +511,18 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       "every pair is packed before its accumulate slot");
   auto pair_t = [](int kb, int g) { return 4 * ((g >> 2) * KB + kb) + (g & 3); };
   auto begin_v2 = [&](int j) {
-    wait_tiles<kLoads, 2>(min(2, max(0, n_it - j - 2)));  // tile j+1 landed
-    __syncthreads();
-    if (j + 4 < n_it) issue((j + 4) % STAGES);
+    if constexpr (kPre) {
+      wait_tiles<kLoads, 1>(min(1, max(0, n_it - j - 3)));  // tile j+2 landed
+      __syncthreads();
+    } else {
+      wait_tiles<kLoads, 2>(min(2, max(0, n_it - j - 2)));  // tile j+1 landed
+      __syncthreads();
+      if (j + 4 < n_it) issue((j + 4) % STAGES);
+    }
   };
   // Role 0, tile j in stage st, tile j+1 in stage st1, P buffer pbi; sc holds
   // S(j), nx receives S(j+1).
-  auto body0 = [&](int st, int st1, int pbi, f32x16 (&sc)[KB], f32x16 (&nx)[KB]) SK_INLINE {
+  auto body0 = [&](int j, int st, int st1, int pbi, f32x16 (&sc)[KB], f32x16 (&nx)[KB]) SK_INLINE {
     if (CAUSAL) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
@@ -505,9 +538,21 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     // (key block 0) that uses them
     f32x4 lv[4];
     auto lv_slot = [&](int q) { return pf(pair_t(0, 2 * q)) - SL; };
+    float lx = 0.f;
+    if constexpr (kStatDpp) {
+      lx = ldf1(stat_lds1 + st * kStatStage);
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (lv_slot(q) < 0) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
+      for (int q = 0; q < 4; ++q)
+        if (lv_slot(q) < 0) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
+    }
+    // statistic of result register r
+    auto lse_r = [&](int r) {
+      if constexpr (kStatDpp)
+        return row_bcast(lx, r);
+      else
+        return lv[r / 4][r % 4];
+    };
     u32x4 aq[KD];
     u32x4 xt[NX];
     float pe[KB][16];
@@ -521,7 +566,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     auto xt_slot = [&](int x) { return NS + (x / DB) * DB * KB + x % DB - XL; };
 #pragma unroll
     for (int s = 0; s < KD; ++s)
-      if (s * KB - KL < 0) aq[s] = ld128(row_lds[s] + st1 * QT);
+      if (s * KB - KL < 0) aq[s] = kPre ? pre[s] : ld128(row_lds[s] + st1 * QT);
 #pragma unroll
     for (int x = 0; x < NX; ++x)
       if (xt_slot(x) < 0) read_xt(x);
@@ -532,12 +577,17 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 #pragma unroll
       for (int s = 0; s < KD; ++s)
         if (s * KB - KL == i && i >= 0) aq[s] = ld128(row_lds[s] + st1 * QT);
+      if (kPre && i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
+      if (kPre && i == kPreSlot) {
+#pragma unroll
+        for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + ((st1 + 1) % STAGES) * QT);
+      }
 #pragma unroll
       for (int x = 0; x < NX; ++x)
         if (xt_slot(x) == i) read_xt(x);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (lv_slot(q) == i) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
+        if (!kStatDpp && lv_slot(q) == i) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
       if (i < NS) {
         const int s = i / KB, kb = i % KB;
         nx[kb] = mfma32<T>(aq[s], kv[kb][s], nx[kb]);
@@ -553,8 +603,8 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
           const int f = pf(pair_t(kb, g));
           float* e = pe[kb];
           if (f == i) {
-            e[2 * g] = fmaf(sc[kb][2 * g], c_log2, -lv[g / 2][2 * (g & 1)]);
-            e[2 * g + 1] = fmaf(sc[kb][2 * g + 1], c_log2, -lv[g / 2][2 * (g & 1) + 1]);
+            e[2 * g] = fmaf(sc[kb][2 * g], c_log2, -lse_r(2 * g));
+            e[2 * g + 1] = fmaf(sc[kb][2 * g + 1], c_log2, -lse_r(2 * g + 1));
           }
           if (f + 1 == i) {
             e[2 * g] = fast_exp2(e[2 * g]);
@@ -577,13 +627,24 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   };
   // Role 1: tile j in stage st (dO(j) rows: dP(j) into dn), tile j-1 in
   // stage stp (Q(j-1)^T, delta(j-1)), P(j-1) in buffer pbp; dpv holds dP(j-1).
-  auto body1 = [&](int st, int stp, int pbp, const f32x16 (&dpv)[KB], f32x16 (&dn)[KB]) SK_INLINE {
+  auto body1 = [&](int j, int st, int stp, int pbp, const f32x16 (&dpv)[KB], f32x16 (&dn)[KB]) SK_INLINE {
     const uint8_t* pb = smem + p_lds + pbp * 4 * kPBlock;
     f32x4 pr[KB][4], dv[4];
     auto pr_slot = [&](int kb, int q) { return pf(pair_t(kb, 2 * q)) + 1 - SL; };
+    float dx = 0.f;
+    if constexpr (kStatDpp) {
+      dx = ldf1(stat_lds1 + stp * kStatStage);
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (pr_slot(0, q) < 0) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+      for (int q = 0; q < 4; ++q)
+        if (pr_slot(0, q) < 0) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+    }
+    auto delta_r = [&](int r) {
+      if constexpr (kStatDpp)
+        return row_bcast(dx, r);
+      else
+        return dv[r / 4][r % 4];
+    };
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -601,7 +662,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     auto xq_slot = [&](int x) { return NS + (x / DB) * DB * KB + x % DB - XL; };
 #pragma unroll
     for (int s = 0; s < KD; ++s)
-      if (s * KB - KL < 0) ad[s] = ld128(row_lds[s] + st * QT);
+      if (s * KB - KL < 0) ad[s] = kPre ? pre[s] : ld128(row_lds[s] + st * QT);
 #pragma unroll
     for (int x = 0; x < NX; ++x)
       if (xq_slot(x) < 0) read_xq(x);
@@ -612,12 +673,17 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 #pragma unroll
       for (int s = 0; s < KD; ++s)
         if (s * KB - KL == i && i >= 0) ad[s] = ld128(row_lds[s] + st * QT);
+      if (kPre && i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
+      if (kPre && i == kPreSlot) {
+#pragma unroll
+        for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + ((st + 1) % STAGES) * QT);
+      }
 #pragma unroll
       for (int x = 0; x < NX; ++x)
         if (xq_slot(x) == i) read_xq(x);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (pr_slot(0, q) == i) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+        if (!kStatDpp && pr_slot(0, q) == i) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -640,7 +706,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
               const int x = 2 * g + e;
-              de[kb][x] = pr[kb][x >> 2][x & 3] * (dpv[kb][x] - dv[x >> 2][x & 3]);
+              de[kb][x] = pr[kb][x >> 2][x & 3] * (dpv[kb][x] - delta_r(x));
             }
           }
           if (f + 1 == i) dsk[kb][g >> 2][g & 3] = pack2<T>(de[kb][2 * g], de[kb][2 * g + 1]);
@@ -658,25 +724,36 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       if (t < n_it) issue(t);
     begin_v2(0);
     score_all(0, sv[0]);
-    if (role == 0) body0(0, 1, 0, sv[0], sv[1]);
+    if constexpr (kPre) {
+      // first row operands of the next body: role 0's S(1) reads Q(1), role
+      // 1's dP(1) reads dO(1), both in stage 1
+#pragma unroll
+      for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + QT);
+    }
+    if (role == 0)
+      body0(0, 0, 1, 0, sv[0], sv[1]);
+    else if (kPre && 4 < n_it)
+      issue(4);
     for (int j0 = 1; j0 < n_it; j0 += STAGES) {
 #pragma unroll
       for (int u = 0; u < STAGES; ++u) {
         const int j = j0 + u;
         if (j >= n_it) break;
         begin_v2(j);
-        role_body((1 + u) % STAGES, (1 + u) & 1);  // j % 6, j & 1
+        role_body(j, (1 + u) % STAGES, (1 + u) & 1);  // j % 6, j & 1
       }
     }
     __syncthreads();  // role 0's P of the last tile
   };
   auto run_v2_roles = [&]() {
     if (role == 0) {
-      run_v2([&](int st, int par) SK_INLINE { body0(st, (st + 1) % STAGES, par, sv[par], sv[par ^ 1]); });
+      run_v2([&](int j, int st, int par) SK_INLINE {
+        body0(j, st, (st + 1) % STAGES, par, sv[par], sv[par ^ 1]);
+      });
       return;
     }
-    run_v2([&](int st, int par) SK_INLINE {
-      body1(st, (st + STAGES - 1) % STAGES, par ^ 1, sv[par ^ 1], sv[par]);
+    run_v2([&](int j, int st, int par) SK_INLINE {
+      body1(j, st, (st + STAGES - 1) % STAGES, par ^ 1, sv[par ^ 1], sv[par]);
     });
     // dS and dK^T of the last tile (stage chosen at run time; the dP
     // register set by a branch, so both sets stay in registers)
