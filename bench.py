@@ -81,18 +81,18 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "recorded-before-digests"
+TRAFFIC_SOURCES_SHA256 = "2a751ccd9ec2ea3b8c2b9fb647a8196754b3866b6f2207a13f2ff8ad44639fae"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 786_890_745,
-    "fwdbwd": 788_786_752,
-    "decode": 8_612_428_279,
-    "decode_mqa": 572_983_785,
-    "decode_varlen": 4_305_234_221,
-    "kv_update": 67_245_869,
-    "decode_paged": 4_305_401_453,
-    "decode_rope": 8_612_496_813,
-    "kv_update_rope": 75_531_648,
-    "decode_step": 4_306_767_682,
+    "fwd": 806_547_836,
+    "fwdbwd": 732_043_130,
+    "decode": 8_612_473_654,
+    "decode_mqa": 573_007_088,
+    "decode_varlen": 4_305_218_706,
+    "kv_update": 67_240_131,
+    "decode_paged": 4_305_360_118,
+    "decode_rope": 8_612_484_944,
+    "kv_update_rope": 75_523_403,
+    "decode_step": 4_306_745_635,
 }
 
 
@@ -863,14 +863,38 @@ def copy_calibration(steps: int, warmup: int) -> dict:
             "GB/s": round(2 * n / mean / 1e6, 1)}
 
 
+def gemm_calibration(steps: int, warmup: int, n: int = 8192) -> dict:
+    """Time a plain bf16 ``torch.matmul`` of two n x n matrices (the vendor GEMM).
+
+    Its rate, with the clock and MFMA busy fraction its counters give, is the
+    MFMA throughput this part sustains under its power limit, the reference
+    point beside the published peak for the attention kernels' fractions."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn(n, n, generator=g, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, generator=g, device=dev, dtype=torch.bfloat16)
+    c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    _, per = _time_loop(lambda i: torch.matmul(a, b, out=c), steps, warmup, torch, stream,
+                        per_step=True)
+    mean = sum(per) / len(per)
+    flop = 2 * n ** 3
+    return {"workload": "gemm", "n": n, "flop": flop, "ms_mean": round(mean, 5),
+            "TFLOP/s": round(flop / mean / 1e9, 1),
+            "frac_of_published_peak": round(flop / mean / 1e9 / PEAK_BF16_TFLOPS, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["copy"], default="fwd",
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["copy", "gemm"], default="fwd",
                     help="headline workload (default fwd = C2); 'copy' times a plain 1 GiB "
-                         "device copy, the calibration kernel for the HBM-traffic counters")
+                         "device copy, the calibration kernel for the HBM-traffic counters; "
+                         "'gemm' times a bf16 8192^3 torch.matmul, the sustained-MFMA reference")
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload (0 disables)")
@@ -891,6 +915,9 @@ def main() -> int:
         return 2
     if args.workload == "copy":
         print(json.dumps(copy_calibration(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.workload == "gemm":
+        print(json.dumps(gemm_calibration(args.steps, args.warmup)), flush=True)
         return 0
     head = measure(args.workload, args.steps, args.warmup, args.cpu_seconds)
     extra = []
