@@ -456,10 +456,11 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // dS(j-1) = P(j-1) (dP(j-1) - delta(j-1)), then dK^T += Q(j-1)^T dS(j-1).
   // Each wave thus keeps its own MFMA and VALU work interleaved (a wave
   // overlaps MFMA and VALU only with its own instructions).  Barrier j makes
-  // tile j+1 (the furthest-ahead tile read: S(j+1)) and role 0's P(j-1)
-  // visible, and retires every read of tile j-2 (role 1 reads Q(j-2) in
-  // step j-1); tile j+4 then goes into tile j-2's stage, so every load has
-  // three steps to land.
+  // role 0's P(j-1) visible, retires every read of tile j-2 (role 1 reads
+  // Q(j-2) in step j-1), and makes tile j+2 visible (the furthest-ahead tile
+  // read in step j: the preload of S(j+2)'s first operands; tile j+1 without
+  // the preload); tile j+4 then goes into tile j-2's stage, so every load
+  // has two steps to land (three without the preload).
   //
   // A step is a list of MFMA slots, each closed by a scheduling barrier:
   // NS score slots (k-step s, key block kb; one read of each A operand for

@@ -55,7 +55,12 @@ def test_kernel_sources_digest_covers_every_kernel_source(tmp_path, monkeypatch)
             (csrc / name).write_bytes(open(os.path.join(src, name), "rb").read())
     monkeypatch.setattr(bench, "ROOT", str(tmp_path))
     assert bench.kernel_sources_digest() == d0
-    (csrc / "sk_bwd.hip").write_bytes((csrc / "sk_bwd.hip").read_bytes() + b"\n")
+    # comments, blank lines and indentation do not count ...
+    src = (csrc / "sk_bwd.hip").read_bytes()
+    (csrc / "sk_bwd.hip").write_bytes(b"// a note\n/* and\n another */\n\n" + src.replace(b"\n", b"\n  "))
+    assert bench.kernel_sources_digest() == d0
+    # ... code does
+    (csrc / "sk_bwd.hip").write_bytes(src + b"\nstatic int sk_digest_probe;\n")
     assert bench.kernel_sources_digest() != d0
 
 
