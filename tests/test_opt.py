@@ -119,6 +119,13 @@ def test_pick_forward_and_backward():
              is_causal=True)
     assert b["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_kernel"
     assert b["grid"] == (8192 // 128) * 2 * 8 and b["dq"]["grid"] == (2048 // 128) * 2 * 32
+    # dK/dV: the 6-deep pipelined ring at D = 128, the 4-deep one elsewhere;
+    # 8 waves (two roles x four 32-key groups) in both
+    assert (b["num_stages"], b["num_warps"]) == (6, 8)
+    for d in (64, 256):
+        o = pick("flash_bwd", (2, 8, 512, d), dtype="bfloat16", kv_len=1024, num_kv_heads=2)
+        assert (o["num_stages"], o["num_warps"]) == (4, 8)
+    assert (b["dq"]["num_stages"], b["dq"]["num_warps"], b["dq"]["BLOCK_N"]) == (4, 4, 32)
     assert b["workspace_bytes"] >= 2 * 2 * 32 * 2048 * 4
 
 
