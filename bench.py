@@ -70,7 +70,9 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 PEAK_NOTE = {
     "mfma": "MI355X published dense bf16/fp16 MFMA peak, 2500 TFLOP/s (256 CUs x 2.4 GHz x "
-            "4096 FLOP/clk = 2516.6 would give a fraction 0.66% lower)",
+            "4096 FLOP/clk = 2516.6 would give a fraction 0.66% lower); the part is power-limited "
+            "below it: the vendor's bf16 GEMM sustains about 1307 TFLOP/s at 70% MFMA busy and "
+            "1.69 GHz (bench.py --workload gemm)",
     "hbm": "MI355X published HBM3E peak, 8000 GB/s",
 }
 
