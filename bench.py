@@ -38,7 +38,9 @@ Workloads (inputs synthetic, seeded, generated on the device):
                     ``kv_update`` + the distinct table rows read.
 
 ``python bench.py`` runs ``fwd`` as the headline (``value``) and, unless
-``--no-extra``, the others as entries of ``extra``.  Each line carries a
+``--no-extra``, the others as entries of ``extra``, followed by the
+``gemm`` reference: a bf16 8192^3 ``torch.matmul`` (the vendor GEMM), the
+dense MFMA rate this part sustains under its power limit.  Each line carries a
 ``roofline`` object for the dominant kernel (algorithmic work per launch over
 the average launch time measured with HIP events on the launch stream) and a
 ``cpu_baseline`` measured on this host with the PyTorch reference path
@@ -941,6 +943,9 @@ def main() -> int:
             except (RuntimeError, NotImplementedError) as e:
                 extra.append({"workload": key, "error": str(e)[:300]})
                 print(f"# {key}: failed: {e}", file=sys.stderr, flush=True)
+        # the sustained-MFMA reference of this part, beside the attention rates
+        extra.append(gemm_calibration(args.steps, args.warmup))
+        print(f"# gemm: {extra[-1]['TFLOP/s']} TFLOP/s", file=sys.stderr, flush=True)
     w = WORKLOADS[args.workload]
     line = {
         "metric": METRIC,
