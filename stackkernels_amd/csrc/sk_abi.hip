@@ -163,16 +163,20 @@ const char* sk_last_error(void) { return g_err; }
 
 // Sizes and work split of the forward: query blocks per (b, h) and, under
 // the causal mask, whether blocks j and n_mblocks-1-j are paired in one
-// workgroup (when that still leaves at least two workgroups per CU).
+// workgroup (when that still leaves SK_FWD_PAIR_MIN paired workgroups, two
+// per CU; a tile-study build can raise it to keep every block on its own).
+#ifndef SK_FWD_PAIR_MIN
+#define SK_FWD_PAIR_MIN 512
+#endif
 static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
                      sk::FwdParams* p) {
   p->B = B, p->Hq = Hq, p->Hkv = Hkv, p->Sq = Sq, p->Sk = Sk, p->D = D, p->group = Hq / Hkv;
-  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D);
+  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D, (int64_t)B * Hq, Sq, is_causal != 0);
   p->n_mblocks = (Sq + rows - 1) / rows;
   if ((int64_t)p->n_mblocks * B * Hq > 0x7fffffffLL)
     return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p->n_mblocks * B * Hq);
   p->pair_items = dtype != SK_F32 && is_causal && p->n_mblocks >= 2 &&
-                  (int64_t)((p->n_mblocks + 1) / 2) * B * Hq >= 512;
+                  (int64_t)((p->n_mblocks + 1) / 2) * B * Hq >= SK_FWD_PAIR_MIN;
   p->n_items = p->pair_items ? (p->n_mblocks + 1) / 2 : p->n_mblocks;
   return SK_OK;
 }

@@ -6,15 +6,19 @@
 //
 // * A workgroup of NW waves owns BM = 32*NW query rows of one (batch, query
 //   head); each wave owns 32 of them, with its Q rows held in registers.
-//   At D <= 128 a workgroup is 8 waves (two per SIMD) and fills a CU alone.
+//   At D <= 128 a workgroup is 8 waves (two per SIMD) and fills a CU alone,
+//   or, for short work, 4 waves with two workgroups per CU (the tile table
+//   at the end of this file).
 // * K/V tiles of BN keys stream through two 4-deep LDS rings (all K stages,
 //   then all V stages), written by buffer_load ... lds (direct to LDS, no
 //   register staging).  Each wave issues whole 1 KiB segments; rows past S_k
 //   and head-dim padding come back as zeros from the buffer range check.
 //   One barrier per two tiles, each issuing the next two K and V tiles into
 //   the stages the two previous tiles freed, so every load has two tiles'
-//   time to land.  The tile loop is unrolled by the ring depth, so every
-//   LDS address is a lane-constant register plus a compile-time offset.
+//   time to land.  (The two-workgroup entry has 2-deep rings: one barrier
+//   per tile, issuing the next K and V tiles, which get one tile's time.)
+//   The tile loop is unrolled by the ring depth, so every LDS address is a
+//   lane-constant register plus a compile-time offset.
 // * One tile body per tile and wave: the score MFMAs of tile t+1, then the
 //   O MFMAs of tile t, with the softmax of tile t (scale/exp2, row sum,
 //   pack) and the row maximum of tile t+1 spread evenly between all of
@@ -109,11 +113,13 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   constexpr int RB = L::kRowBytes;
   constexpr int kVReg = STAGES * KT;  // LDS: all K stages, then all V stages
   static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
-  static_assert(STAGES == 4, "the unrolled tile loop assumes a 4-deep ring");
+  static_assert(STAGES == 4 || STAGES == 2, "a 4-deep ring (two groups ahead) or 2-deep (one ahead)");
   static_assert(3 * KT + (BN - 8) * RB < 65536, "stage offsets must fit the ds immediate");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGES * KT];
-  constexpr int kSync = SK_FWD_SYNC_TILES;  // tiles per workgroup barrier
+  // Tiles per workgroup barrier.  The 2-deep ring (two workgroups per CU)
+  // synchronises every tile and keeps one load group in flight.
+  constexpr int kSync = STAGES == 2 ? 1 : SK_FWD_SYNC_TILES;
   static_assert(kSync == 1 || kSync == 2, "one barrier per tile or per two tiles");
 
   const int tid = threadIdx.x;
@@ -252,10 +258,10 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   // flight), then for all (barrier); the barrier also retires every wave's
   // reads of the stages the next issue refills.
   auto sync_group = [&](int g) {
-    if (g + 1 < n_tiles)
+    if (STAGES == 4 && g + 1 < n_tiles)
       wait_vmcnt<2 * LK>();
     else
-      wait_vmcnt<0>();
+      wait_vmcnt<0>();  // 2-deep ring: group g is the only one in flight
     __syncthreads();
   };
 
@@ -454,11 +460,20 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
       if (k + 4 < n_tiles) issue_k(u_k);
       if (k + 2 < n_tiles) issue_v((u_k + 2) % STAGES);
       if (k + 3 < n_tiles) issue_v((u_k + 3) % STAGES);
-    } else {
+    } else if constexpr (STAGES == 4) {
       sync_group(k);
       if (k + 2 < n_tiles) {
         issue_k((u_k + 3) % STAGES);
         issue_v((u_k + 2) % STAGES);
+      }
+    } else {
+      // 2-deep: barrier k retires body k-1's reads (K(k), V(k-1)); group
+      // k+1 (K(k+2), V(k+1)) goes into exactly those stages and has body
+      // k's time to land.
+      sync_group(k);
+      if (k + 1 < n_tiles) {
+        issue_k((u_k + 2) % STAGES);
+        issue_v((u_k + 1) % STAGES);
       }
     }
   };
@@ -471,6 +486,11 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
       issue_k(2);
       issue_v(1);
       wait_vmcnt<4 * LK>();  // K(0)
+    } else if constexpr (STAGES == 2) {
+      issue_k(0);
+      issue_k(1);
+      issue_v(0);  // group 0
+      wait_vmcnt<2 * LK>();  // K(0)
     } else {
       issue_k(0);
       issue_k(1);
@@ -538,49 +558,77 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
 
 // gfx950 tile table for the forward kernel, by head dim (padded to 64, 128
 // or 256; other dims run zero-padded in the next size up):
-//   D <= 64 : BN 64, 8 waves (2 per SIMD), 4 stages  (64 KiB LDS)
-//   D <= 128: BN 64, 8 waves (2 per SIMD), 4 stages  (128 KiB LDS)
-//   D <= 256: BN 32, 4 waves (1 per SIMD), 4 stages  (128 KiB LDS)
-// One workgroup per CU.  BN = 64 keeps two 32x32 score blocks per wave per
-// tile (two independent MFMA chains) while the score, operand and O
-// registers fit the 256-register budget of two waves per SIMD.
-// The D <= 128 row can be rebuilt as a candidate of the tile study (keys per
-// tile, waves, workgroups per CU): -DSK_FWD_D128_TILE=32,4,2 (4 waves, two
-// workgroups per CU) or 32,8,1; the table's entry is 64,8,1.
-#ifndef SK_FWD_D128_TILE
-#define SK_FWD_D128_TILE 64, 8, 1
-#endif
+//   D <= 64 : BN 64, 8 waves (2 per SIMD), 4 stages, 1 WG/CU  (64 KiB LDS)
+//   D <= 128, long work: BN 64, 8 waves (2 per SIMD), 4 stages, 1 WG/CU
+//     (128 KiB LDS)
+//   D <= 128, short work: BN 64, 4 waves, 2 stages, 2 WGs/CU (64 KiB LDS
+//     each, 2 waves per SIMD in all)
+//   D <= 256: BN 32, 4 waves (1 per SIMD), 4 stages, 1 WG/CU  (128 KiB LDS)
+// BN = 64 keeps two 32x32 score blocks per wave per tile (two independent
+// MFMA chains) while the score, operand and O registers fit the
+// 256-register budget of two waves per SIMD.  At D <= 128 the two-workgroup
+// entry halves the rows per workgroup (128) and lets one workgroup's
+// prologue, epilogue and causal-diagonal idle waves overlap the other's
+// tiles, at the price of twice the L2-to-LDS traffic per MFMA, one barrier
+// per tile and one tile of load look-ahead.  It is taken when the query
+// length is at most 2,048 (4,096 under the causal mask, whose diagonal idles
+// waves) or the 8-wave grid has fewer than 2,048 blocks (8 per CU).
+// Measured at D = 128 bf16 against the 8-wave entry: 2-6% faster at
+// S <= 2,048, 0.5-2.3% at causal S = 4,096, up to 31% on small grids; 0.3-1.1%
+// slower non-causal at S = 4,096 and 0.7-2% slower at S = 8,192-16,384 with
+// 2,048 or more 8-wave blocks.
+// A tile-study build fixes one D <= 128 entry for every shape (keys per
+// tile, waves, workgroups per CU, ring depth): -DSK_FWD_D128_TILE=64,8,1,4,
+// 64,4,2,2, 32,4,2,4 or 32,8,1,4.
 struct FwdConfig {
-  int dp, bn, nw, occ;
+  int dp, bn, nw, occ, stages;
 };
 struct FwdTile {
-  int bn, nw, occ;
+  int bn, nw, occ, stages;
 };
-constexpr FwdTile kFwdD128{SK_FWD_D128_TILE};
+#ifdef SK_FWD_D128_TILE
+constexpr FwdTile kFwdD128Long{SK_FWD_D128_TILE};
+constexpr FwdTile kFwdD128Short{SK_FWD_D128_TILE};
+#else
+constexpr FwdTile kFwdD128Long{64, 8, 1, 4};
+constexpr FwdTile kFwdD128Short{64, 4, 2, 2};
+#endif
+static_assert(kFwdD128Long.stages == 4 || kFwdD128Long.stages == 2, "ring depth 4 or 2");
+static_assert(kFwdD128Short.stages == 4 || kFwdD128Short.stages == 2, "ring depth 4 or 2");
 
-static FwdConfig fwd_config(int d) {
-  if (d <= 64) return {64, 64, 8, 1};
-  if (d <= 128) return {128, kFwdD128.bn, kFwdD128.nw, kFwdD128.occ};
-  return {256, 32, 4, 1};
+// Whether a D <= 128 forward over bh (batch, head) pairs of sq queries takes
+// the short-work entry.
+static bool fwd_d128_short(int64_t bh, int sq, bool causal) {
+  const int64_t blocks8 = (int64_t)((sq + 255) / 256) * bh;  // 256-row blocks
+  return sq <= (causal ? 4096 : 2048) || blocks8 < 2048;
 }
 
-int fwd_rows_per_block(int dtype, int d) {
+static FwdConfig fwd_config(int d, int64_t bh, int sq, bool causal) {
+  if (d <= 64) return {64, 64, 8, 1, 4};
+  if (d <= 128) {
+    const FwdTile t = fwd_d128_short(bh, sq, causal) ? kFwdD128Short : kFwdD128Long;
+    return {128, t.bn, t.nw, t.occ, t.stages};
+  }
+  return {256, 32, 4, 1, 4};
+}
+
+int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, bool causal) {
   (void)dtype;
-  return 32 * fwd_config(d).nw;
+  return 32 * fwd_config(d, bh, sq, causal).nw;
 }
 
-template <class T, int DP, int BN, int NW, int OCC>
+template <class T, int DP, int BN, int NW, int OCC, int STAGES = 4>
 static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
   KernelPlan k;
   const bool rope = p.rope.cos != nullptr;
   if (causal && !rope)
-    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, false>;
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, STAGES, OCC, true, false>;
   else if (!rope)
-    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, false>;
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, STAGES, OCC, false, false>;
   else if (causal)
-    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, true, true>;
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, STAGES, OCC, true, true>;
   else
-    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, 4, OCC, false, true>;
+    k.fn = (const void*)fwd_mfma_kernel<T, DP, BN, NW, STAGES, OCC, false, true>;
   k.grid = dim3((unsigned)(p.n_items * p.B * p.Hq));
   k.block = dim3(NW * 64);
   k.kernel = "fwd_mfma_kernel";
@@ -588,7 +636,7 @@ static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
   k.head_dim = DP;
   k.block_m = 32 * NW;
   k.block_n = BN;
-  k.stages = 4;
+  k.stages = STAGES;
   k.causal = causal;
   k.rope = rope;
   return k;
@@ -596,11 +644,15 @@ static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
 
 template <class T>
 static KernelPlan plan_fwd_dt(const FwdParams& p, bool causal) {
-  switch (fwd_config(p.D).dp) {
+  switch (fwd_config(p.D, (int64_t)p.B * p.Hq, p.Sq, causal).dp) {
     case 64:
       return plan_fwd_t<T, 64, 64, 8, 1>(p, causal);
     case 128:
-      return plan_fwd_t<T, 128, kFwdD128.bn, kFwdD128.nw, kFwdD128.occ>(p, causal);
+      if (fwd_d128_short((int64_t)p.B * p.Hq, p.Sq, causal))
+        return plan_fwd_t<T, 128, kFwdD128Short.bn, kFwdD128Short.nw, kFwdD128Short.occ,
+                          kFwdD128Short.stages>(p, causal);
+      return plan_fwd_t<T, 128, kFwdD128Long.bn, kFwdD128Long.nw, kFwdD128Long.occ,
+                        kFwdD128Long.stages>(p, causal);
     default:
       return plan_fwd_t<T, 256, 32, 4, 1>(p, causal);
   }

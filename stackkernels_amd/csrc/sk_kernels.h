@@ -177,8 +177,9 @@ hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream
 hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s);
 
-// Rows of queries one forward workgroup covers for (dtype, head dim).
-int fwd_rows_per_block(int dtype, int d);
+// Rows of queries one forward workgroup covers for (dtype, head dim, batch x
+// query heads, query length, causal mask).
+int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, bool causal);
 // Padded head dim the kernels are compiled for (64, 96, 128 or 256), or 0.
 int padded_head_dim(int d);
 

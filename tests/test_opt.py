@@ -105,12 +105,24 @@ def test_pick_decode_matches_the_launch_plan():
 
 
 def test_pick_forward_and_backward():
+    # D = 128, causal S <= 4096: the short-work entry, 4 waves and two workgroups per CU
     f = pick("flash_attn", (4, 32, 4096, 128), dtype="bfloat16", is_causal=True)
-    assert (f["BLOCK_M"], f["BLOCK_N"], f["num_warps"], f["num_stages"]) == (256, 64, 8, 4)
-    assert f["paired_causal_blocks"] and f["grid"] == 8 * 4 * 32
+    assert (f["BLOCK_M"], f["BLOCK_N"], f["num_warps"], f["num_stages"]) == (128, 64, 4, 2)
+    assert f["paired_causal_blocks"] and f["grid"] == 16 * 4 * 32
+    # non-causal S = 4096 on a full grid (2,048 blocks of 256 rows): the 8-wave entry
     nc = pick("flash_attention", {"batch": 4, "heads": 32, "seq_q": 4096, "head_dim": 128},
               dtype="bfloat16")
+    assert (nc["BLOCK_M"], nc["num_warps"], nc["num_stages"]) == (256, 8, 4)
     assert not nc["paired_causal_blocks"] and nc["grid"] == 16 * 4 * 32
+    nc2 = pick("flash_attn", (8, 32, 2048, 128), dtype="bfloat16")
+    assert (nc2["BLOCK_M"], nc2["num_warps"], nc2["num_stages"]) == (128, 4, 2)
+    # long work on a full grid (2,048 blocks of 256 rows): 8 waves, one workgroup per CU
+    lg = pick("flash_attn", (1, 32, 16384, 128), dtype="bfloat16", is_causal=True)
+    assert (lg["BLOCK_M"], lg["BLOCK_N"], lg["num_warps"], lg["num_stages"]) == (256, 64, 8, 4)
+    assert lg["grid"] == 32 * 32
+    # long but a small grid: the short-work entry again
+    sm = pick("flash_attn", (1, 8, 16384, 128), dtype="bfloat16", is_causal=True)
+    assert (sm["BLOCK_M"], sm["num_warps"], sm["num_stages"]) == (128, 4, 2)
     d256 = pick("flash_fwd", (1, 8, 512, 256), dtype="float16")
     assert (d256["BLOCK_M"], d256["BLOCK_N"], d256["num_warps"]) == (128, 32, 4)
     f32 = pick("flash_attn", (1, 8, 512, 64), dtype="float32")
