@@ -85,18 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "d882a17b621f09da4908d03c90038832ac6c37fdd3e7fe33cb8d0d86047deacc"
+TRAFFIC_SOURCES_SHA256 = "3729bdd190def57540db075fbbb659e2f990f30deb05a81c6ee3de5eec26a497"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 806_547_836,
-    "fwdbwd": 732_043_130,
-    "decode": 8_612_473_654,
-    "decode_mqa": 573_007_088,
-    "decode_varlen": 4_305_218_706,
-    "kv_update": 67_240_131,
-    "decode_paged": 4_305_360_118,
-    "decode_rope": 8_612_484_944,
-    "kv_update_rope": 75_523_403,
-    "decode_step": 4_306_745_635,
+    "fwd": 677_720_095,
+    "fwd_long": 818_214_763,
+    "fwdbwd": 795_555_632,
+    "decode": 8_612_473_665,
+    "decode_mqa": 573_007_057,
+    "decode_varlen": 4_305_218_746,
+    "kv_update": 67_240_134,
+    "decode_paged": 4_305_360_110,
+    "decode_rope": 8_612_484_975,
+    "kv_update_rope": 75_523_838,
+    "decode_step": 4_306_745_526,
 }
 
 
@@ -143,6 +144,9 @@ def causal_pairs(sq: int, sk: int, causal: bool) -> int:
 WORKLOADS = {
     "fwd": dict(name="C2 flash_attention fwd bf16 causal MHA", B=4, Hq=32, Hkv=32, Sq=4096,
                 Sk=4096, D=128, causal=True, dtype="bf16", kind="fwd"),
+    # A long causal prefill on a full grid: the forward table's 8-wave entry.
+    "fwd_long": dict(name="flash_attention fwd bf16 causal MHA, long sequence", B=1, Hq=32,
+                     Hkv=32, Sq=16384, Sk=16384, D=128, causal=True, dtype="bf16", kind="fwd"),
     "fwdbwd": dict(name="C3 flash_attention fwd+bwd bf16 causal GQA bottom-right", B=2, Hq=32,
                    Hkv=8, Sq=2048, Sk=8192, D=128, causal=True, dtype="bf16", kind="fwdbwd"),
     "decode": dict(name="C4 flash_decode bf16 GQA", B=64, Hq=32, Hkv=8, Sq=1, Sk=32768, D=128,
@@ -778,7 +782,9 @@ def run_cpu_baseline(w: dict, budget_s: float):
     if w["kind"] == "decode":
         hkv_chunk = 1
     else:
-        hkv_chunk = max(1, 4 // grp)  # 4 query heads per chunk bounds the score tensor
+        # 4 query heads per chunk bounds the score tensor, one for long sequences
+        # (16,384^2 fp32 scores are 1 GiB per head)
+        hkv_chunk = max(1, 4 // grp) if w["Sq"] * w["Sk"] <= (1 << 26) else 1
     hq_chunk = hkv_chunk * grp
     q = torch.randn(1, hq_chunk, w["Sq"], w["D"], generator=g).bfloat16().float()
     k = torch.randn(1, hkv_chunk, w["Sk"], w["D"], generator=g).bfloat16().float()
