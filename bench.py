@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "3729bdd190def57540db075fbbb659e2f990f30deb05a81c6ee3de5eec26a497"
+TRAFFIC_SOURCES_SHA256 = "55e543e33564bb2f9c0ffd63d9ba6948d770921505e7a1b2acd0496170ed62ab"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 677_720_095,
-    "fwd_long": 818_214_763,
-    "fwdbwd": 795_555_632,
-    "decode": 8_612_473_665,
-    "decode_mqa": 573_007_057,
-    "decode_varlen": 4_305_218_746,
-    "kv_update": 67_240_134,
-    "decode_paged": 4_305_360_110,
-    "decode_rope": 8_612_484_975,
-    "kv_update_rope": 75_523_838,
-    "decode_step": 4_306_745_526,
+    "fwd": 677_192_380,
+    "fwd_long": 814_792_355,
+    "fwdbwd": 797_000_937,
+    "decode": 8_612_473_775,
+    "decode_mqa": 573_007_150,
+    "decode_varlen": 4_305_218_831,
+    "kv_update": 67_240_136,
+    "decode_paged": 4_305_360_289,
+    "decode_rope": 8_612_485_024,
+    "kv_update_rope": 75_523_465,
+    "decode_step": 4_306_745_671,
 }
 
 

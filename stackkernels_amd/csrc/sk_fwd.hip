@@ -54,6 +54,8 @@
 //   workgroup runs query blocks j and n-1-j back to back when the grid
 //   stays at two or more workgroups per CU, which evens out the work per
 //   workgroup and halves the per-item fixed cost.
+#include <type_traits>
+
 #include "sk_common.h"
 #include "sk_kernels.h"
 #include "sk_rope.h"
@@ -346,8 +348,12 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
   // of S(t+1) is taken in the last slots, after its MFMAs have completed.
   // The operand reads run KLEAD (K) and OLEAD (V^T) MFMAs ahead.  Each slot
   // is fenced with sched_barrier so the in-order issue keeps this order.
+  // next: std::true_type, or std::false_type for the block's last tile,
+  // whose body leaves out the score MFMAs, their K reads and the row maximum
+  // of a tile past the end.
   auto body = [&](int stg_k, int stg_v, f32x16 (&nx)[KB], const f32x16 (&sc)[KB],
-                  float neg_m) {
+                  float neg_m, auto next) {
+    constexpr bool kNext = decltype(next)::value;
     constexpr int NS = KD * KB;
     constexpr int NO = DB * KN;
     constexpr int NM = NS + NO;
@@ -379,16 +385,18 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
     float y[NE], e[NE];
     float psum[2] = {0.f, 0.f};
     float mx = kNegInf;
+    if constexpr (kNext) {
 #pragma unroll
-    for (int i = 0; i < KLEAD; ++i) a[i] = ld128(kaddr(i));
+      for (int i = 0; i < KLEAD; ++i) a[i] = ld128(kaddr(i));
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
+      for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
+    }
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
-      if (i + KLEAD < NS) a[i + KLEAD] = ld128(kaddr(i + KLEAD));
+      if (kNext && i + KLEAD < NS) a[i + KLEAD] = ld128(kaddr(i + KLEAD));
       if (i + OLEAD >= NS && i + OLEAD - NS < NO) vt[i + OLEAD - NS] = read_vt(i + OLEAD - NS);
       if (i < NS) {
-        nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
+        if constexpr (kNext) nx[i % KB] = mfma32<T>(a[i], qreg[i / KB], nx[i % KB]);
       } else {
         const int j = i - NS;
         oacc[j % DB] = mfma32<T>(vt[j], pk[j / DB], oacc[j % DB]);
@@ -411,22 +419,25 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
           asm volatile("" : "+v"(psum[0]), "+v"(psum[1]));
         }
       }
+      if constexpr (kNext) {
 #pragma unroll
-      for (int q = 0; q < NX / 2; ++q)
-        if (i == MS + q * (NM - MS) / (NX / 2))
-          mx = __builtin_elementwise_maximum(
-              mx, __builtin_elementwise_maximum(nx[q >> 3][(2 * q) & 15], nx[q >> 3][(2 * q + 1) & 15]));
-      if (i >= MS) asm volatile("" : "+v"(mx));
+        for (int q = 0; q < NX / 2; ++q)
+          if (i == MS + q * (NM - MS) / (NX / 2))
+            mx = __builtin_elementwise_maximum(
+                mx, __builtin_elementwise_maximum(nx[q >> 3][(2 * q) & 15], nx[q >> 3][(2 * q + 1) & 15]));
+        if (i >= MS) asm volatile("" : "+v"(mx));
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += psum[0] + psum[1];
     return xhalf_max(mx);
   };
 
-  // Pipeline.  Stage indices are tile % 4 and the loop is unrolled by 4, so
-  // they are compile-time constants.  Even tiles' scores live in s0, odd in
-  // s1.  A wave that sees tile t always computes S(t+1) in its body; on its
-  // last visible tile that result (from a stale stage) is never read.
+  // Pipeline.  Stage indices are tile % STAGES and the loop is unrolled by
+  // STAGES, so they are compile-time constants.  Even tiles' scores live in
+  // s0, odd in s1.  A wave that sees tile t computes S(t+1) in its body; on
+  // a visible tile before the block's last, when t+1 is past the wave's
+  // causal limit, that result (from a stale stage) is never read.
   //
   // kSync == 2 (one barrier per two tiles): barrier k (k even) makes K(k+1),
   // K(k+2), V(k), V(k+1) visible to every wave (issued at barrier k-2, so all
@@ -507,21 +518,38 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
     gemm0(0, s0);
     if (active(0)) neg_m = rescale(mask_max(0, s0));
   }
-  for (int t0 = 0; t0 < n_tiles; t0 += STAGES) {
+  // Every tile but the last in a loop unrolled by the ring depth; the last
+  // tile (stage known only at run time, scores in s0 or s1 by its parity)
+  // without the look-ahead score tile.  (At D = 256 the peeled copy does not
+  // fit the register budget: all tiles run in the loop.)
+  constexpr bool kPeel = DP <= 128;
+  const int n_main = kPeel ? n_tiles - 1 : n_tiles;
+  for (int t0 = 0; t0 < n_main; t0 += STAGES) {
 #pragma unroll
     for (int u = 0; u < STAGES; ++u) {
       const int t = t0 + u;
-      if (t >= n_tiles) break;
+      if (t >= n_main) break;
       f32x16(&cur)[KB] = (u & 1) ? s1 : s0;
       f32x16(&nxt)[KB] = (u & 1) ? s0 : s1;
       barrier_issue(t, u);
       if (active(t)) {
-        float mt = body((u + 1) % STAGES, u, nxt, cur, neg_m);
+        float mt = body((u + 1) % STAGES, u, nxt, cur, neg_m, std::true_type{});
         if (active(t + 1)) {
           if (masked(t + 1)) mt = mask_max(t + 1, nxt);
           neg_m = rescale(mt);
         }
       }
+    }
+  }
+  if (kPeel && n_main >= 0) {
+    const int t = n_main;
+    const int u = t % STAGES;
+    barrier_issue(t, u);
+    if (active(t)) {
+      if (t & 1)
+        body(0, u, s0, s1, neg_m, std::false_type{});
+      else
+        body(0, u, s1, s0, neg_m, std::false_type{});
     }
   }
 
