@@ -223,7 +223,14 @@ def pick(
         lines.append("  (override " + ("applied through num_splits" if honoured else
                      "returned as given: the tiles are compiled in; the launcher runs the "
                      "table's kernels") + ")")
-    lines.append("Rejected Candidates: None (one compiled configuration per head dim and group size)")
+    if op_name in _FWD_OPS and code != 0 and 64 < prob["D"] <= 128:  # not fp32
+        lines.append("Rejected Candidates: the other D = 128 forward entry of the table (short "
+                     "work: S_q <= 2048, causal S_q <= 4096 or fewer than 2048 blocks of 256 rows "
+                     "-> 4 wavefronts, two workgroups per CU, 2-deep ring; else 8 wavefronts, one "
+                     "per CU, 4-deep ring)")
+    else:
+        lines.append("Rejected Candidates: None (one compiled configuration per head dim and "
+                     "group size)")
     return chosen, "\n".join(lines)
 
 

@@ -151,7 +151,9 @@ def test_pick_explain_override_and_errors():
     assert ov == {"SPLIT_KV": 16} and "user_override" in text and "16 splits" in text
     assert "applied through num_splits" in text
     _, text = pick("flash_attn", (1, 8, 128, 64), override={"BLOCK_M": 64}, explain=True)
-    assert "returned as given" in text
+    assert "returned as given" in text and "Rejected Candidates: None" in text
+    _, text = pick("flash_attn", (4, 32, 4096, 128), is_causal=True, explain=True)
+    assert "BM=128" in text and "the other D = 128 forward entry" in text
     with pytest.raises(NotImplementedError, match="attention path"):
         pick("rms_norm", (4, 1024))
     with pytest.raises(ValueError, match="dtype"):
