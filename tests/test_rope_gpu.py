@@ -228,3 +228,26 @@ def test_forward_rope_c2_shape_equals_forward_on_rotated_q():
         base = flash_attention(qr, k, v, True)
     torch.cuda.synchronize()
     assert torch.equal(out, base)
+
+
+def test_forward_rope_long_work_entry_equals_forward_on_rotated_q():
+    """A shape past the short-work limits of the D = 128 forward table (causal,
+    S_q = 4352, 2,176 blocks of 256 rows: the 8-wave entry): the fused rotation
+    still gives the bits of the plain forward on the oracle-rotated q."""
+    from stackkernels_amd._opt.pick import pick
+
+    b, h, s, d = 4, 32, 4352, 128
+    assert pick("flash_attn", (b, h, s, d), dtype="bfloat16", is_causal=True)["BLOCK_M"] == 256
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(37)
+    q = torch.randn(b, h, s, d, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(b, h, s, d, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(b, h, s, d, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = _tables(d, 2 * s)
+    starts = torch.tensor([0, 7, 1000, s - 1], dtype=torch.int32)
+    with torch.no_grad():
+        out = flash_attention(q, k, v, True, rope_cos=cos, rope_sin=sin, start_pos=starts.cuda())
+        qr = _rotated(q, cos, sin, orc.rope_positions(starts.numpy(), b, s))
+        base = flash_attention(qr, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
