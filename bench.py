@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "55e543e33564bb2f9c0ffd63d9ba6948d770921505e7a1b2acd0496170ed62ab"
+TRAFFIC_SOURCES_SHA256 = "9a0ad0abb2b35be0ccf9609aec4563763c99cf4cb9a6335a49b4c8acf7a8acd0"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 677_192_380,
-    "fwd_long": 814_792_355,
-    "fwdbwd": 797_000_937,
-    "decode": 8_612_473_775,
-    "decode_mqa": 573_007_150,
-    "decode_varlen": 4_305_218_831,
-    "kv_update": 67_240_136,
-    "decode_paged": 4_305_360_289,
-    "decode_rope": 8_612_485_024,
-    "kv_update_rope": 75_523_465,
-    "decode_step": 4_306_745_671,
+    "fwd": 683_250_583,
+    "fwd_long": 844_131_930,
+    "fwdbwd": 792_144_290,
+    "decode": 8_612_473_661,
+    "decode_mqa": 573_007_091,
+    "decode_varlen": 4_305_218_728,
+    "kv_update": 67_240_160,
+    "decode_paged": 4_305_360_111,
+    "decode_rope": 8_612_484_900,
+    "kv_update_rope": 75_523_391,
+    "decode_step": 4_306_745_437,
 }
 
 

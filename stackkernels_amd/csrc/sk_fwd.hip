@@ -585,26 +585,29 @@ __global__ void __launch_bounds__(NW * 64, OCC) fwd_mfma_kernel(FwdParams p) {
 }
 
 // gfx950 tile table for the forward kernel, by head dim (padded to 64, 128
-// or 256; other dims run zero-padded in the next size up):
-//   D <= 64 : BN 64, 8 waves (2 per SIMD), 4 stages, 1 WG/CU  (64 KiB LDS)
-//   D <= 128, long work: BN 64, 8 waves (2 per SIMD), 4 stages, 1 WG/CU
-//     (128 KiB LDS)
-//   D <= 128, short work: BN 64, 4 waves, 2 stages, 2 WGs/CU (64 KiB LDS
-//     each, 2 waves per SIMD in all)
+// or 256; other dims run zero-padded in the next size up) and, at D <= 128,
+// by the amount of work:
+//   D <= 64,  long work:  BN 64, 8 waves (2 per SIMD), 4 stages, 1 WG/CU (64 KiB LDS)
+//   D <= 64,  short work: BN 64, 4 waves, 4 stages, 2 WGs/CU (64 KiB LDS each)
+//   D <= 128, long work:  BN 64, 8 waves (2 per SIMD), 4 stages, 1 WG/CU (128 KiB LDS)
+//   D <= 128, short work: BN 64, 4 waves, 2 stages, 2 WGs/CU (64 KiB LDS each)
 //   D <= 256: BN 32, 4 waves (1 per SIMD), 4 stages, 1 WG/CU  (128 KiB LDS)
 // BN = 64 keeps two 32x32 score blocks per wave per tile (two independent
 // MFMA chains) while the score, operand and O registers fit the
-// 256-register budget of two waves per SIMD.  At D <= 128 the two-workgroup
-// entry halves the rows per workgroup (128) and lets one workgroup's
-// prologue, epilogue and causal-diagonal idle waves overlap the other's
-// tiles, at the price of twice the L2-to-LDS traffic per MFMA, one barrier
-// per tile and one tile of load look-ahead.  It is taken when the query
-// length is at most 2,048 (4,096 under the causal mask, whose diagonal idles
-// waves) or the 8-wave grid has fewer than 2,048 blocks (8 per CU).
-// Measured at D = 128 bf16 against the 8-wave entry: 2-6% faster at
-// S <= 2,048, 0.5-2.3% at causal S = 4,096, up to 31% on small grids; 0.3-1.1%
-// slower non-causal at S = 4,096 and 0.7-2% slower at S = 8,192-16,384 with
-// 2,048 or more 8-wave blocks.
+// 256-register budget of two waves per SIMD.  The two-workgroup entries
+// halve the rows per workgroup (128) and let one workgroup's prologue,
+// epilogue and causal-diagonal idle waves overlap the other's tiles, at the
+// price of twice the L2-to-LDS traffic per MFMA (and, at D = 128, where two
+// 4-deep rings do not fit the LDS, one barrier per tile and one tile of load
+// look-ahead).  They are taken for short work: a query length of at most
+// 2,048 (4,096 under the causal mask, whose diagonal idles waves) or an
+// 8-wave grid of fewer than 2,048 blocks (8 per CU).  Measured against the
+// 8-wave entries, D = 128 bf16: 2-6% faster at S <= 2,048, 0.5-2.3% at
+// causal S = 4,096, up to 31% on small grids; 0.3-1.1% slower non-causal at
+// S = 4,096 and 0.7-2% slower at S = 8,192-16,384 with 2,048 or more 8-wave
+// blocks.  D = 64 bf16: 6.5-9.6% faster at S <= 2,048 and causal S = 4,096,
+// 49% on a small grid; even non-causal at S = 4,096, 0.9% slower causal at
+// S = 16,384.
 // A tile-study build fixes one D <= 128 entry for every shape (keys per
 // tile, waves, workgroups per CU, ring depth): -DSK_FWD_D128_TILE=64,8,1,4,
 // 64,4,2,2, 32,4,2,4 or 32,8,1,4.
@@ -623,19 +626,22 @@ constexpr FwdTile kFwdD128Short{64, 4, 2, 2};
 #endif
 static_assert(kFwdD128Long.stages == 4 || kFwdD128Long.stages == 2, "ring depth 4 or 2");
 static_assert(kFwdD128Short.stages == 4 || kFwdD128Short.stages == 2, "ring depth 4 or 2");
+constexpr FwdTile kFwdD64Long{64, 8, 1, 4};
+constexpr FwdTile kFwdD64Short{64, 4, 2, 4};
 
 // Whether a D <= 128 forward over bh (batch, head) pairs of sq queries takes
 // the short-work entry.
-static bool fwd_d128_short(int64_t bh, int sq, bool causal) {
+static bool fwd_short(int64_t bh, int sq, bool causal) {
   const int64_t blocks8 = (int64_t)((sq + 255) / 256) * bh;  // 256-row blocks
   return sq <= (causal ? 4096 : 2048) || blocks8 < 2048;
 }
 
 static FwdConfig fwd_config(int d, int64_t bh, int sq, bool causal) {
-  if (d <= 64) return {64, 64, 8, 1, 4};
   if (d <= 128) {
-    const FwdTile t = fwd_d128_short(bh, sq, causal) ? kFwdD128Short : kFwdD128Long;
-    return {128, t.bn, t.nw, t.occ, t.stages};
+    const bool sh = fwd_short(bh, sq, causal);
+    const FwdTile t = d <= 64 ? (sh ? kFwdD64Short : kFwdD64Long)
+                              : (sh ? kFwdD128Short : kFwdD128Long);
+    return {d <= 64 ? 64 : 128, t.bn, t.nw, t.occ, t.stages};
   }
   return {256, 32, 4, 1, 4};
 }
@@ -672,11 +678,16 @@ static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
 
 template <class T>
 static KernelPlan plan_fwd_dt(const FwdParams& p, bool causal) {
+  const bool sh = fwd_short((int64_t)p.B * p.Hq, p.Sq, causal);
   switch (fwd_config(p.D, (int64_t)p.B * p.Hq, p.Sq, causal).dp) {
     case 64:
-      return plan_fwd_t<T, 64, 64, 8, 1>(p, causal);
+      if (sh)
+        return plan_fwd_t<T, 64, kFwdD64Short.bn, kFwdD64Short.nw, kFwdD64Short.occ,
+                          kFwdD64Short.stages>(p, causal);
+      return plan_fwd_t<T, 64, kFwdD64Long.bn, kFwdD64Long.nw, kFwdD64Long.occ,
+                        kFwdD64Long.stages>(p, causal);
     case 128:
-      if (fwd_d128_short((int64_t)p.B * p.Hq, p.Sq, causal))
+      if (sh)
         return plan_fwd_t<T, 128, kFwdD128Short.bn, kFwdD128Short.nw, kFwdD128Short.occ,
                           kFwdD128Short.stages>(p, causal);
       return plan_fwd_t<T, 128, kFwdD128Long.bn, kFwdD128Long.nw, kFwdD128Long.occ,

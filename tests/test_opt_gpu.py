@@ -1,7 +1,7 @@
 """On the MI355X: the device profile reads gfx950 correctly, and the
 occupancy the HIP runtime reports for the kernels ``pick`` names equals what
 the gfx950 table was sized for (one 8-wave forward workgroup per CU, or two
-4-wave ones for short work at D = 128; one dK/dV workgroup per CU, two dQ
+4-wave ones for short work at D <= 128; one dK/dV workgroup per CU, two dQ
 workgroups per CU at D <= 128, eight one-wave decode workgroups, three 4-wave
 MQA decode workgroups)."""
 
@@ -27,7 +27,8 @@ def test_device_profile_is_mi355x():
 @pytest.mark.parametrize("op,shape,kw,lds,per_cu", [
     ("flash_attn", (4, 32, 4096, 128), dict(dtype="bfloat16", is_causal=True), 65536, 2),
     ("flash_attn", (1, 32, 16384, 128), dict(dtype="bfloat16", is_causal=True), 131072, 1),
-    ("flash_attn", (2, 16, 1024, 64), dict(dtype="float16"), 65536, 1),
+    ("flash_attn", (2, 16, 1024, 64), dict(dtype="float16"), 65536, 2),
+    ("flash_attn", (1, 32, 16384, 64), dict(dtype="float16", is_causal=True), 65536, 1),
     ("flash_decode", (64, 32, 1, 128), dict(dtype="bfloat16", kv_len=32768, num_kv_heads=8),
      None, 8),
     ("flash_decode", (8, 64, 1, 128), dict(dtype="float16", kv_len=131072, num_kv_heads=1),
