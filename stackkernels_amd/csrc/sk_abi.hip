@@ -146,9 +146,11 @@ int make_rope(const void* cos, const void* sin, int rope_dtype, int rope_rows,
   return SK_OK;
 }
 
-size_t bwd_ws_bytes(int B, int Hq, int Sq) {
+// Backward scratch: delta and lse * log2(e) (fp32 per query row), then the
+// dS tiles of the five-GEMM backward where it runs.
+size_t bwd_ws_bytes(int dtype, int B, int Hq, int Sq, int Sk, int D) {
   const size_t rows = (size_t)B * Hq * Sq;
-  return 2 * ((rows * sizeof(float) + 255) / 256 * 256);
+  return 2 * ((rows * sizeof(float) + 255) / 256 * 256) + sk::bwd_ds_bytes(dtype, B, Hq, Sq, Sk, D);
 }
 
 }  // namespace
@@ -272,7 +274,7 @@ int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int
   int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
   if (rc) return rc;
   if (!bytes) return fail(SK_EINVAL, "bytes pointer is NULL");
-  *bytes = bwd_ws_bytes(B, Hq, Sq);
+  *bytes = bwd_ws_bytes(dtype, B, Hq, Sq, Sk, D);
   return SK_OK;
 }
 
@@ -284,7 +286,7 @@ int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const
   int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
   if (rc) return rc;
   if ((int64_t)B * Hq * Sq == 0 && (int64_t)B * Hkv * Sk == 0) return SK_OK;
-  const size_t need = bwd_ws_bytes(B, Hq, Sq);
+  const size_t need = bwd_ws_bytes(dtype, B, Hq, Sq, Sk, D);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(SK_EWORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   if ((int64_t)B * Hq * Sq > 0 &&
@@ -304,6 +306,10 @@ int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const
   p.delta = (float*)workspace;
   p.lse_log2 = (float*)((char*)workspace + rows_bytes);
   p.dq_acc = nullptr;
+  const size_t ds_bytes = sk::bwd_ds_bytes(dtype, B, Hq, Sq, Sk, D);
+  p.ds = ds_bytes > 0 ? (char*)workspace + 2 * rows_bytes : nullptr;
+  p.ds_nkb = (Sk + 31) / 32;
+  p.ds_nqt = (Sq + 31) / 32;
   p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
@@ -779,7 +785,7 @@ int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, 
     p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
     k = op == SK_OP_BWD_DKV ? sk::plan_bwd_dkv(dtype, p, is_causal != 0)
                             : sk::plan_bwd_dq(dtype, p, is_causal != 0);
-    ws = bwd_ws_bytes(B, Hq, Sq);
+    ws = bwd_ws_bytes(dtype, B, Hq, Sq, Sk, D);
   } else if (decode) {
     int ns = 0, per = 0;
     if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &ns, &per))) return rc;

@@ -78,6 +78,11 @@
 #ifndef SK_BWD_DKV_KB
 #define SK_BWD_DKV_KB 1
 #endif
+// Five-GEMM backward at D = 128 (1, the table) or seven GEMMs everywhere (0):
+// the dK/dV kernel stores dS and bwd_dq_ds_kernel computes dQ from it.
+#ifndef SK_BWD_FIVE_GEMM
+#define SK_BWD_FIVE_GEMM 1
+#endif
 #include "sk_kernels.h"
 
 namespace sk {
@@ -363,6 +368,39 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // Role 0, tile in stage stg (P buffer pb): S, causal mask, P =
   // exp2(S*scale*log2e - lse*log2e), published for role 1, dV^T += dO^T P.
   int cur_gi = 0, cur_m0 = m_begin;  // role 0's tile
+  // Five-GEMM backward: role 1 stores each tile's dS (32 keys x 32 queries,
+  // 16-bit) for the dQ kernel.  A lane holds key l32 and, as pieces of 4
+  // queries, P_m = queries 8 m + 4 hl + {0..3}: P_0, P_1 = g[0].xy, .zw and
+  // P_2, P_3 = g[1].xy, .zw.  Chunk (key r, m) -- queries 8 m .. 8 m + 7, the
+  // pieces of lanes r and r + 32 -- is formed by one lane-half swap per
+  // dword and stored at byte 1024 (m % 2) + 16 (r + 32 (m / 2)) of the 2 KiB
+  // tile, so each wave writes the tile with two contiguous 1 KiB stores.
+  // Key groups past S_k store nothing.
+  int ds_gi = 0, ds_m0 = m_begin;  // role 1's dS tile
+  auto store_ds = [&](const u32x4 (&g)[2]) SK_INLINE {
+    if constexpr (KB == 1 && SK_BWD_FIVE_GEMM) {
+      if (p.ds != nullptr) {
+        if (nw < p.Sk) {
+          const int64_t tile = ((bh0 + ds_gi) * p.ds_nkb + (nw >> 5)) * p.ds_nqt + (ds_m0 >> 5);
+          // lane r < 32 gets chunks (r, 0), (r, 1); lane r + 32 chunks (r, 2), (r, 3)
+          const auto a0 = __builtin_amdgcn_permlane32_swap(g[0][0], g[1][0], false, false);
+          const auto a1 = __builtin_amdgcn_permlane32_swap(g[0][1], g[1][1], false, false);
+          const auto b0 = __builtin_amdgcn_permlane32_swap(g[0][2], g[1][2], false, false);
+          const auto b1 = __builtin_amdgcn_permlane32_swap(g[0][3], g[1][3], false, false);
+          uint8_t* dst = (uint8_t*)p.ds + tile * 2048 + 16 * lane;
+          *reinterpret_cast<u32x4*>(dst) =
+              u32x4{(uint32_t)a0[0], (uint32_t)a1[0], (uint32_t)a0[1], (uint32_t)a1[1]};
+          *reinterpret_cast<u32x4*>(dst + 1024) =
+              u32x4{(uint32_t)b0[0], (uint32_t)b1[0], (uint32_t)b0[1], (uint32_t)b1[1]};
+        }
+        ds_m0 += BMQ;
+        if (ds_m0 >= p.Sq) {
+          ds_m0 = m_begin;
+          ++ds_gi;
+        }
+      }
+    }
+  };
   auto step0 = [&](int stg, int pbi) {
     f32x16 sc = score(stg);
     if (CAUSAL && nw + 31 > cur_m0 + diag) {
@@ -628,7 +666,13 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   };
   // Role 1: tile j in stage st (dO(j) rows: dP(j) into dn), tile j-1 in
   // stage stp (Q(j-1)^T, delta(j-1)), P(j-1) in buffer pbp; dpv holds dP(j-1).
-  auto body1 = [&](int j, int st, int stp, int pbp, const f32x16 (&dpv)[KB], f32x16 (&dn)[KB]) SK_INLINE {
+  // dprev: the packed dS of tile j-2, stored here before this step's DMA
+  // issue (so no store is issued after a tile load whose wait comes first:
+  // one counter covers loads and stores, and they may complete out of
+  // order); receives dS(j-1).
+  auto body1 = [&](int j, int st, int stp, int pbp, const f32x16 (&dpv)[KB], f32x16 (&dn)[KB],
+                   u32x4 (&dprev)[2]) SK_INLINE {
+    if (SK_BWD_FIVE_GEMM && j >= 2) store_ds(dprev);
     const uint8_t* pb = smem + p_lds + pbp * 4 * kPBlock;
     f32x4 pr[KB][4], dv[4];
     auto pr_slot = [&](int kb, int q) { return pf(pair_t(kb, 2 * q)) + 1 - SL; };
@@ -714,6 +758,10 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
         }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (SK_BWD_FIVE_GEMM) {
+      dprev[0] = dsk[0][0];
+      dprev[1] = dsk[0][1];
+    }
   };
   // Each role runs its own copy of the step loop (the same barriers in the
   // same order).  role_body(st, par) runs step j >= 1 with tile j in stage
@@ -753,9 +801,11 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       });
       return;
     }
+    u32x4 dprev[2];
     run_v2([&](int j, int st, int par) SK_INLINE {
-      body1(j, st, (st + STAGES - 1) % STAGES, par ^ 1, sv[par ^ 1], sv[par]);
+      body1(j, st, (st + STAGES - 1) % STAGES, par ^ 1, sv[par ^ 1], sv[par], dprev);
     });
+    if (SK_BWD_FIVE_GEMM && n_it >= 2) store_ds(dprev);  // dS of tile n_it - 2
     // dS and dK^T of the last tile (stage chosen at run time; the dP
     // register set by a branch, so both sets stay in registers)
     const int jl = n_it - 1;
@@ -784,6 +834,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
             const u32x4 x = lds_tr_pair(smem + tr_lo[c] + o, smem + tr_hi[c] + o);
             acc[kb][c] = mfma32<T>(x, dsk[s2], acc[kb][c]);
           }
+        if (SK_BWD_FIVE_GEMM && kb == 0) store_ds(dsk);
       }
     };
     if (jl & 1)
@@ -1237,6 +1288,185 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
     }
 }
 
+// dQ of the five-GEMM backward (bwd_dq_ds_kernel): dQ^T += K^T dS^T over the
+// dS tiles the dK/dV kernel stored, so S and dP are computed once per
+// (query tile, key tile) instead of twice.  A workgroup of 4 waves owns
+// 32 x QW x 4 query rows of one (b, h_q), QW query tiles of 32 per wave;
+// 32-key K tiles and each wave's 2 KiB dS tiles of the same keys stream
+// through an LDS ring, STAGES - 2 tiles ahead.  K^T is read transposed from
+// the K tile and dS^T transposed from the key-major dS tile with the same key
+// order in the MFMA's k-slots (keys 4 hl + {0..3} and 8 + 4 hl + {0..3} of
+// each 16-key step), so the lane of query l32 holds its 8 dS values of a
+// k-step as the B operand, and each K^T read feeds QW MFMAs.  The dK/dV kernel writes the dS tiles of every 128-key
+// block from the first query tile that can see the block; a wave reads a
+// tile only if its query tile lies in that range (else the DMA is empty and
+// the tile reads as zeros).  dS of keys past S_k is finite and meets K rows
+// that read as zeros.
+// dQ-from-dS tile: query tiles of 32 per wave, ring depth, workgroups per
+// CU.  Two query tiles per wave let each K^T operand read feed two MFMAs and
+// halve the steps (each closed by a workgroup barrier) per query: at C3 the
+// backward ran 1.549 ms with 2,3,2, 1.555 with 2,6,1, 1.645 with 1,5,2.
+#ifndef SK_BWD_DQDS_TILE
+#define SK_BWD_DQDS_TILE 2, 3, 2
+#endif
+struct DqDsTile {
+  int qw, stages, occ;
+};
+constexpr DqDsTile kDqDs{SK_BWD_DQDS_TILE};
+
+template <class T, int DP, int QW, int STAGES, int OCC, bool CAUSAL>
+__global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
+  constexpr int NW = 4;
+  constexpr int BN = 32;
+  constexpr int PD = STAGES - 2 >= 1 ? STAGES - 2 : 1;  // tiles issued ahead
+  static_assert(STAGES >= 3, "a ring of at least three stages");
+  using L = BwdTile<DP, BN>;  // K tiles
+  constexpr int BM = 32 * QW * NW;
+  constexpr int DB = DP / 32;  // 32-wide head-dim blocks of dQ^T
+  constexpr int KN = BN / 16;  // k-steps over keys
+  constexpr int LK = L::kSegs / NW;
+  constexpr int kDs = 2048;  // one 32-query dS tile
+  constexpr int kStageBytes = L::kTileBytes + NW * QW * kDs;
+  constexpr int kLoads = LK + 2 * QW;  // DMAs per wave per tile
+  constexpr int RB = L::kRowBytes;
+  static_assert(L::kSegs % NW == 0, "tile segments must divide over the waves");
+  static_assert(KN == 2 && DB <= 4, "32-key tiles, D <= 128");
+  static_assert(STAGES * kStageBytes * OCC <= 160 * 1024, "workgroups per CU must fit the LDS");
+  static_assert(kLoads * (PD - 1) < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStageBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5;
+
+  // Work item: (batch, query head) major, heaviest query block first.
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int bh = w / p.n_mblocks;
+  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
+  const int b = bh / p.Hq;
+  const int hkv = (bh - b * p.Hq) / p.group;
+  const int m0 = mblk * BM;
+  const int mw = m0 + 32 * QW * wave;  // first query row of this wave
+  const int diag = p.Sk - p.Sq;
+
+  const uint16_t* kbase = (const uint16_t*)p.k + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+  uint32_t goff[LK];
+#pragma unroll
+  for (int j = 0; j < LK; ++j) {
+    const int seg = wave + j * NW;
+    const int r = seg * L::kSegRows + lane / L::kCpr;
+    const int c = (lane % L::kCpr) ^ swz_rt<DP>(r);
+    goff[j] = c * 8 < p.D ? (uint32_t)((r * p.D + c * 8) * 2) : kBufferOob;
+  }
+  // This wave's dS tiles: query tile qt (mw / 32 + q), key tile t at
+  // tile (bh * ds_nkb + t) * ds_nqt + qt.  Key tiles [0, kt_lim[q]) were
+  // written for query tile qt.
+  const uint8_t* ds_row[QW];
+  int kt_lim[QW];
+#pragma unroll
+  for (int q = 0; q < QW; ++q) {
+    const int r0 = mw + 32 * q;
+    ds_row[q] = (const uint8_t*)p.ds + ((int64_t)bh * p.ds_nkb * p.ds_nqt + (r0 >> 5)) * kDs;
+    kt_lim[q] = r0 < p.Sq ? p.ds_nkb : 0;
+    if (CAUSAL && r0 < p.Sq) {
+      const int last = r0 + 31 + diag;  // last key a row of the tile can see
+      kt_lim[q] = last < 0 ? 0 : min(p.ds_nkb, (last / 128 + 1) * 4);
+    }
+  }
+  // The dS tile lands in LDS key-major (row r, queries 8 m .. 8 m + 7 at byte
+  // 64 r + 16 m); DMA h, lane i fills chunk c = 64 h + i, i.e. (r, m) =
+  // (c / 4, c % 4), stored by the dK/dV kernel at 1024 (m % 2) + 16 (r + 32
+  // (m / 2)).
+  uint32_t ds_goff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 16 * h + (lane >> 2), m = lane & 3;
+    ds_goff[h] = (uint32_t)(1024 * (m & 1) + 16 * (r + 32 * (m >> 1)));
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue_tile = [&](int t) {
+    const int n0 = t * BN;
+    const int bytes = tile_bytes(min(BN, p.Sk - n0), p.D, p.D);
+    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.D, bytes);
+    const uint32_t st = lds0 + (t % STAGES) * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < LK; ++j) buffer_load_lds_b128(kr, st + (wave + j * NW) * 1024, goff[j]);
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const i32x4 dr =
+          make_rsrc_words(ds_row[q] + (int64_t)t * p.ds_nqt * kDs, t < kt_lim[q] ? kDs : 0);
+      const uint32_t sd = st + L::kTileBytes + (wave * QW + q) * kDs;
+      buffer_load_lds_b128(dr, sd, ds_goff[0]);
+      buffer_load_lds_b128(dr, sd + 1024, ds_goff[1]);
+    }
+  };
+
+  int n_end = p.Sk;
+  if (CAUSAL) n_end = min(p.Sk, m0 + BM + diag);
+  const int n_tiles = n_end > 0 ? (n_end + BN - 1) / BN : 0;
+#pragma unroll
+  for (int t = 0; t < PD; ++t)
+    if (t < n_tiles) issue_tile(t);
+
+  f32x16 dqacc[QW][DB];
+#pragma unroll
+  for (int q = 0; q < QW; ++q)
+#pragma unroll
+    for (int c = 0; c < DB; ++c) dqacc[q][c] = f32x16{};
+  // K^T: transposed reads of the K tile (head-dim block c); dS^T: transposed
+  // reads of each dS tile, rows 4 hl + j16 / 4 (+8), columns lane % 32.
+  int kt_lo[DB], kt_hi[DB];
+  tr_offsets<DP, DB>(lane, 0, kt_lo, kt_hi);
+  const int j16 = lane & 15;
+  const int ds_lo = L::kTileBytes + wave * QW * kDs + (4 * hl + (j16 >> 2)) * 64 +
+                    32 * ((lane >> 4) & 1) + 8 * (j16 & 3);
+
+  for (int t = 0; t < n_tiles; ++t) {
+    wait_tiles<kLoads, PD - 1>(min(PD - 1, n_tiles - 1 - t));  // tile t landed
+    __syncthreads();  // ... for every wave; every read of the stage refilled next retired
+    if (t + PD < n_tiles) issue_tile(t + PD);
+    const uint8_t* st = smem + (t % STAGES) * kStageBytes;
+    u32x4 kt[KN][DB], dst[QW][KN];
+#pragma unroll
+    for (int s2 = 0; s2 < KN; ++s2) {
+#pragma unroll
+      for (int q = 0; q < QW; ++q)
+        dst[q][s2] = lds_tr_pair(st + ds_lo + q * kDs + 1024 * s2, st + ds_lo + q * kDs + 512 + 1024 * s2);
+#pragma unroll
+      for (int c = 0; c < DB; ++c)
+        kt[s2][c] = lds_tr_pair(st + 16 * s2 * RB + kt_lo[c], st + 16 * s2 * RB + kt_hi[c]);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < KN; ++s2)
+#pragma unroll
+      for (int c = 0; c < DB; ++c)
+#pragma unroll
+        for (int q = 0; q < QW; ++q) dqacc[q][c] = mfma32<T>(kt[s2][c], dst[q][s2], dqacc[q][c]);
+  }
+
+#pragma unroll
+  for (int q = 0; q < QW; ++q) {
+    const int row = mw + 32 * q + (lane & 31);
+    if (row < p.Sq) {
+      uint16_t* dqp = (uint16_t*)p.dq + ((int64_t)bh * p.Sq + row) * p.D;
+#pragma unroll
+      for (int c = 0; c < DB; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * c + 8 * i + 4 * hl;
+          if (d < p.D) {
+            const f32x16& a = dqacc[q][c];
+            *reinterpret_cast<u32x2*>(dqp + d) =
+                u32x2{pack2<T>(a[4 * i] * p.scale, a[4 * i + 1] * p.scale),
+                      pack2<T>(a[4 * i + 2] * p.scale, a[4 * i + 3] * p.scale)};
+          }
+        }
+    }
+  }
+}
+
 // gfx950 tile table for the backward, by head dim (padded to 64, 128 or 256;
 // other dims run zero-padded in the next size up), 4 ring stages:
 //   dK/dV: 8 waves, one workgroup per CU, 128 keys per workgroup, 32-query
@@ -1342,7 +1572,49 @@ KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal) {
   return KernelPlan{};
 }
 
+// The five-GEMM backward (dS tiles in the workspace) runs where the dK/dV
+// kernel's pipelined schedule stores them: 16-bit inputs, padded head dim
+// 128, 32 keys per wave.  Its tiles take B * H_q * S_q * S_k * 2 bytes
+// (rounded up to 32 x 32 tiles); above kBwdDsMaxBytes the seven-GEMM
+// backward runs instead.  It gives the seven-GEMM results bit for bit (the
+// same dS values, summed into dQ in the same key order): the dS stores cost
+// the dK/dV kernel about 8%, and the dQ pass, which no longer recomputes S
+// and dP, runs after it instead of beside it.  C3 backward 4.7% faster, MHA
+// S = 4096 1.8% faster (one box, alternating libraries).
+constexpr size_t kBwdDsMaxBytes = size_t(4) << 30;
+
+size_t bwd_ds_bytes(int dtype, int B, int Hq, int Sq, int Sk, int D) {
+  if (!SK_BWD_FIVE_GEMM) return 0;
+  if (dtype != BF16::code && dtype != F16::code) return 0;
+  if (D <= 64 || D > 128 || SK_BWD_DKV_STAGES != 6 || SK_BWD_DKV_KB != 1) return 0;
+  const size_t bytes = (size_t)B * Hq * ((Sk + 31) / 32) * ((Sq + 31) / 32) * 2048;
+  return bytes <= kBwdDsMaxBytes ? bytes : 0;
+}
+
+template <class T>
+static KernelPlan plan_dq_ds_t(BwdParams& p, bool causal) {
+  constexpr int NW = 4, QW = kDqDs.qw;
+  p.n_mblocks = (p.Sq + 32 * QW * NW - 1) / (32 * QW * NW);
+  p.ds_nkb = (p.Sk + 31) / 32;
+  p.ds_nqt = (p.Sq + 31) / 32;
+  KernelPlan k;
+  k.fn = causal ? (const void*)bwd_dq_ds_kernel<T, 128, QW, kDqDs.stages, kDqDs.occ, true>
+                : (const void*)bwd_dq_ds_kernel<T, 128, QW, kDqDs.stages, kDqDs.occ, false>;
+  k.grid = dim3((unsigned)((int64_t)p.n_mblocks * p.B * p.Hq));
+  k.block = dim3(NW * 64);
+  k.kernel = "bwd_dq_ds_kernel";
+  k.elem = T::code;
+  k.head_dim = 128;
+  k.block_m = 32 * QW * NW;
+  k.block_n = 32;
+  k.stages = kDqDs.stages;
+  k.causal = causal;
+  return k;
+}
+
 KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal) {
+  if (bwd_ds_bytes(dtype, p.B, p.Hq, p.Sq, p.Sk, p.D) > 0)
+    return dtype == BF16::code ? plan_dq_ds_t<BF16>(p, causal) : plan_dq_ds_t<F16>(p, causal);
   if (dtype == BF16::code) return plan_dq_dt<BF16>(p, causal);
   if (dtype == F16::code) return plan_dq_dt<F16>(p, causal);
   if (dtype == 0) return plan_bwd_dq_f32(p, causal);
@@ -1423,6 +1695,14 @@ hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream
   const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (kv.head_dim == 256 ? 2 : 1);
   const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
   if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  if (bwd_ds_bytes(dtype, p.B, p.Hq, p.Sq, p.Sk, p.D) > 0) {
+    // Five-GEMM backward: dQ reads the dS tiles dK/dV writes, on one stream.
+    if (p.ds == nullptr) return hipErrorInvalidValue;
+    hipError_t e = run_plan(kv, &q, s);
+    if (e != hipSuccess) return e;
+    return run_plan(dq, &q, s);
+  }
+  q.ds = nullptr;
   const SideEntry* se = g_kv > 256 && g_q > 0 ? side_entry(s) : nullptr;
   if (!se) {
     hipError_t e = run_plan(kv, &q, s);

@@ -101,6 +101,11 @@ struct BwdParams {
   float* delta;     // [B*Hq*Sq] fp32 scratch: rowsum(dO * O)
   float* lse_log2;  // [B*Hq*Sq] fp32 scratch: lse * log2(e) (+inf for empty rows)
   float* dq_acc;    // [B*Hq*Sq*D] fp32 scratch (dQ accumulator) or null
+  // dS tiles [B*Hq][ds_nkb][ds_nqt] of 32 keys x 32 queries (16-bit, key-major
+  // rows of 64 bytes), written by the dK/dV kernel and read by the dQ kernel
+  // of the five-GEMM backward; null for the seven-GEMM backward.
+  void* ds;
+  int ds_nkb, ds_nqt;
   int B, Hq, Hkv, Sq, Sk, D, group;
   float scale, scale_log2;  // signed sm_scale and sm_scale * log2(e)
   // MFMA kernels: the score exponent uses |sm_scale| * log2(e) (never 0, so a
@@ -164,6 +169,10 @@ KernelPlan plan_decode_combine(int dtype, const DecParams& p);
 // The backward plans fill the block counts of p they derive.
 KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal);
 KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal);
+// Bytes of dS tiles the five-GEMM backward needs for this shape, or 0 when it
+// runs the seven-GEMM backward (head dims other than 65-128, fp32, or more
+// than kBwdDsMaxBytes of tiles).
+size_t bwd_ds_bytes(int dtype, int B, int Hq, int Sq, int Sk, int D);
 KernelPlan plan_bwd_dkv_f32(BwdParams& p, bool causal);
 KernelPlan plan_bwd_dq_f32(BwdParams& p, bool causal);
 

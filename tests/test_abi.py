@@ -110,8 +110,18 @@ def test_decode_argument_errors(lib):
 
 def test_bwd_workspace(lib):
     nb = ctypes.c_size_t()
+    rows = 2 * 2 * 32 * 2048 * 4  # delta and lse * log2(e), fp32 per query row
+    # C3 (bf16, D = 128): plus the five-GEMM backward's dS tiles, 32 x 32 x 2 bytes each
     assert lib.sk_attn_bwd_workspace(2, 2, 32, 8, 2048, 8192, 128, 1, ctypes.byref(nb)) == 0
-    assert nb.value >= 2 * 2 * 32 * 2048 * 4
+    assert nb.value == rows + 2 * 32 * (8192 // 32) * (2048 // 32) * 2048
+    # ragged lengths round up to whole tiles
+    assert lib.sk_attn_bwd_workspace(1, 1, 2, 1, 33, 65, 96, 0, ctypes.byref(nb)) == 0
+    assert nb.value == 2 * 512 + 2 * 3 * 2 * 2048  # 66 fp32 rows -> 264 bytes -> 512 (256-aligned)
+    # the seven-GEMM backward (no dS tiles): D = 64, D = 256, fp32, and beyond 4 GiB of tiles
+    for dtype, d, sq, sk in ((2, 64, 2048, 8192), (2, 256, 2048, 8192), (0, 128, 2048, 8192),
+                             (2, 128, 16384, 16384)):
+        assert lib.sk_attn_bwd_workspace(dtype, 2, 32, 8, sq, sk, d, 1, ctypes.byref(nb)) == 0
+        assert nb.value == 2 * 2 * 32 * sq * 4, (dtype, d)
 
 
 def test_varlen_and_cache_argument_errors(lib):

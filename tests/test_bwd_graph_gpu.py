@@ -1,13 +1,15 @@
-"""The backward's dQ kernel on the library's side stream, eagerly and under
-HIP graph capture.
+"""The backward's two launch shapes, eagerly and under HIP graph capture.
 
-When the dK/dV grid runs more than one round of workgroups, ``sk_attn_bwd``
-forks the dQ kernel onto the side stream the library keeps for the caller's
-stream, after the preprocess pass, and joins it back with events.  The kernels use no
-atomics, so the result does not depend on how the two overlap: every replay
-of a captured backward (fork and join become graph edges) must equal, bit for
-bit, the eager call on the same inputs, and the eager call must match the
-oracle-checked fp32 reference within the bf16 tolerance.
+Seven GEMMs (head dims other than 65-128): when the dK/dV grid runs more than
+one round of workgroups, ``sk_attn_bwd`` forks the dQ kernel onto the side
+stream the library keeps for the caller's stream, after the preprocess pass,
+and joins it back with events.  Five GEMMs (D = 128): the dK/dV kernel stores
+dS in the workspace and the dQ kernel reads it after it, on the caller's
+stream.  The kernels use no atomics, so the result does not depend on how
+they overlap: every replay of a captured backward (fork and join become graph
+edges) must equal, bit for bit, the eager call on the same inputs, and the
+eager call must match the oracle-checked fp32 reference within the bf16
+tolerance.
 """
 
 import pytest
@@ -22,7 +24,14 @@ from _gpu_util import TOL, assert_close_maxabs, native_loaded
 pytestmark = pytest.mark.gpu
 
 # B=2, H_kv=8, S_k=4096: 32 key blocks x 16 = 512 dK/dV workgroups, two rounds.
-SHAPE = dict(b=2, hq=16, hkv=8, sq=512, sk=4096, d=128)
+SHAPE = dict(b=2, hq=16, hkv=8, sq=512, sk=4096)
+DIMS = {"seven_gemm_fork": 64, "five_gemm": 128}
+
+
+@pytest.fixture(params=sorted(DIMS), autouse=True)
+def _head_dim(request):
+    SHAPE["d"] = DIMS[request.param]
+    yield
 
 
 def _inputs(dtype, seed):

@@ -129,16 +129,23 @@ def test_pick_forward_and_backward():
     assert f32["kernel_variant"] == "fwd_f32_kernel"
     b = pick("flash_bwd", (2, 32, 2048, 128), dtype="bfloat16", kv_len=8192, num_kv_heads=8,
              is_causal=True)
-    assert b["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_kernel"
-    assert b["grid"] == (8192 // 128) * 2 * 8 and b["dq"]["grid"] == (2048 // 128) * 2 * 32
+    # D = 128: the five-GEMM backward (dQ from the dS tiles dK/dV stores)
+    assert b["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_ds_kernel"
+    assert b["grid"] == (8192 // 128) * 2 * 8 and b["dq"]["grid"] == (2048 // 256) * 2 * 32
     # dK/dV: the 6-deep pipelined ring at D = 128, the 4-deep one elsewhere;
     # 8 waves (two roles x four 32-key groups) in both
     assert (b["num_stages"], b["num_warps"]) == (6, 8)
     for d in (64, 256):
         o = pick("flash_bwd", (2, 8, 512, d), dtype="bfloat16", kv_len=1024, num_kv_heads=2)
         assert (o["num_stages"], o["num_warps"]) == (4, 8)
-    assert (b["dq"]["num_stages"], b["dq"]["num_warps"], b["dq"]["BLOCK_N"]) == (4, 4, 32)
-    assert b["workspace_bytes"] >= 2 * 2 * 32 * 2048 * 4
+        assert o["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_kernel"  # seven GEMMs
+    # dQ from the stored dS: 4 waves x 64 queries, 32-key tiles, 3-deep ring
+    assert (b["dq"]["num_stages"], b["dq"]["num_warps"], b["dq"]["BLOCK_N"],
+            b["dq"]["BLOCK_M"]) == (3, 4, 32, 256)
+    assert b["workspace_bytes"] == 2 * 2 * 32 * 2048 * 4 + 2 * 32 * 256 * 64 * 2048
+    for d in (64, 256):
+        o = pick("flash_bwd", (2, 8, 512, d), dtype="bfloat16", kv_len=1024, num_kv_heads=2)
+        assert (o["dq"]["num_stages"], o["dq"]["num_warps"]) == (4, 4)
 
 
 def test_pick_explain_override_and_errors():
