@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "9a0ad0abb2b35be0ccf9609aec4563763c99cf4cb9a6335a49b4c8acf7a8acd0"
+TRAFFIC_SOURCES_SHA256 = "e531178ab306d6c72d76afd7c4660637e0862211d980e391ff224f6864967b62"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 683_250_583,
-    "fwd_long": 844_131_930,
-    "fwdbwd": 792_144_290,
-    "decode": 8_612_473_661,
-    "decode_mqa": 573_007_091,
-    "decode_varlen": 4_305_218_728,
-    "kv_update": 67_240_160,
-    "decode_paged": 4_305_360_111,
-    "decode_rope": 8_612_484_900,
-    "kv_update_rope": 75_523_391,
-    "decode_step": 4_306_745_437,
+    "fwd": 677_633_325,
+    "fwd_long": 809_459_981,
+    "fwdbwd": 4_662_703_135,
+    "decode": 8_612_474_001,
+    "decode_mqa": 573_007_233,
+    "decode_varlen": 4_305_219_072,
+    "kv_update": 67_240_136,
+    "decode_paged": 4_305_360_569,
+    "decode_rope": 8_612_485_275,
+    "kv_update_rope": 75_523_330,
+    "decode_step": 4_306_745_804,
 }
 
 

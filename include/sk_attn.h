@@ -80,8 +80,12 @@ SK_API int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, v
                 int is_causal, float sm_scale, void* stream);
 
 /*
- * Bytes of scratch sk_attn_bwd needs for these dims (two fp32 row statistics
- * per query row: delta = rowsum(dO * O) and lse * log2(e)).  Replaces
+ * Bytes of scratch sk_attn_bwd needs for these dims: two fp32 row statistics
+ * per query row (delta = rowsum(dO * O) and lse * log2(e)) and, where the
+ * five-GEMM backward runs (16-bit inputs, head dim 65-128), dS in 16-bit
+ * 32 x 32 tiles: B * Hq * ceil(Sk / 32) * ceil(Sq / 32) * 2048 bytes (2.1 GB
+ * at B = 2, Hq = 32, Sq = 2048, Sk = 8192); shapes whose tiles would exceed
+ * 4 GiB run the seven-GEMM backward without them.  Replaces
  * allocate_delta_buffer
  * (reference: src/stackkernels/_opt/memory/workspace.py:16-23).
  */
@@ -98,13 +102,15 @@ SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int 
  * (B,Hkv,Sk,D); lse (B,Hq,Sq) fp32 as written by sk_attn_fwd.  dk and dv are
  * summed over the query heads that share a KV head.  Rows with lse = -inf
  * contribute nothing.  workspace: >= sk_attn_bwd_workspace() bytes, any
- * contents (the call initialises what it uses).  When the dK/dV grid runs
- * more than one round of workgroups (more than 256 workgroups), the dQ kernel
- * runs on the library's side stream for `stream`, forked from `stream` after
- * the preprocess pass and joined back into it (also when a launch fails);
- * under graph capture the fork and the join are recorded as graph edges.  A
- * call under capture on a stream that has never run an eager backward keeps
- * the one-stream order.
+ * contents (the call initialises what it uses).  Five-GEMM backward (head
+ * dim 65-128, 16-bit): the dK/dV kernel stores dS in the workspace and the
+ * dQ kernel reads it, both on `stream`.  Seven-GEMM backward (other head
+ * dims): when the dK/dV grid runs more than one round of workgroups (more
+ * than 256 workgroups), the dQ kernel runs on the library's side stream for
+ * `stream`, forked from `stream` after the preprocess pass and joined back
+ * into it (also when a launch fails); under graph capture the fork and the
+ * join are recorded as graph edges.  A call under capture on a stream that
+ * has never run an eager backward keeps the one-stream order.
  */
 SK_API int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const void* v,
                 const void* o, const float* lse, void* dq, void* dk, void* dv,
