@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "e531178ab306d6c72d76afd7c4660637e0862211d980e391ff224f6864967b62"
+TRAFFIC_SOURCES_SHA256 = "7a3abbb4d4d143b20302cb12bff5d04f041828a40374129696d656879c015e58"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 677_633_325,
-    "fwd_long": 809_459_981,
-    "fwdbwd": 4_662_703_135,
-    "decode": 8_612_474_001,
-    "decode_mqa": 573_007_233,
-    "decode_varlen": 4_305_219_072,
-    "kv_update": 67_240_136,
-    "decode_paged": 4_305_360_569,
-    "decode_rope": 8_612_485_275,
-    "kv_update_rope": 75_523_330,
-    "decode_step": 4_306_745_804,
+    "fwd": 682_459_545,
+    "fwd_long": 844_382_362,
+    "fwdbwd": 4_539_090_415,
+    "decode": 8_612_473_664,
+    "decode_mqa": 573_007_050,
+    "decode_varlen": 4_305_218_731,
+    "kv_update": 67_240_132,
+    "decode_paged": 4_305_360_243,
+    "decode_rope": 8_612_484_952,
+    "kv_update_rope": 75_523_404,
+    "decode_step": 4_306_745_776,
 }
 
 

@@ -83,6 +83,14 @@
 #ifndef SK_BWD_FIVE_GEMM
 #define SK_BWD_FIVE_GEMM 1
 #endif
+// Non-temporal hint on the dS tiles: bit 0 on the dK/dV kernel's stores,
+// bit 1 on the dQ kernel's loads.  The tiles are written once and read once,
+// and the hint keeps them from evicting the Q/dO and K tiles the kernels
+// re-read from L2: with both bits the C3 backward is 4.6% faster and MHA
+// S = 4096 2.0% faster (bit-identical results).
+#ifndef SK_BWD_DS_NT
+#define SK_BWD_DS_NT 3
+#endif
 #include "sk_kernels.h"
 
 namespace sk {
@@ -388,10 +396,15 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
           const auto b0 = __builtin_amdgcn_permlane32_swap(g[0][2], g[1][2], false, false);
           const auto b1 = __builtin_amdgcn_permlane32_swap(g[0][3], g[1][3], false, false);
           uint8_t* dst = (uint8_t*)p.ds + tile * 2048 + 16 * lane;
-          *reinterpret_cast<u32x4*>(dst) =
-              u32x4{(uint32_t)a0[0], (uint32_t)a1[0], (uint32_t)a0[1], (uint32_t)a1[1]};
-          *reinterpret_cast<u32x4*>(dst + 1024) =
-              u32x4{(uint32_t)b0[0], (uint32_t)b1[0], (uint32_t)b0[1], (uint32_t)b1[1]};
+          const u32x4 c0{(uint32_t)a0[0], (uint32_t)a1[0], (uint32_t)a0[1], (uint32_t)a1[1]};
+          const u32x4 c1{(uint32_t)b0[0], (uint32_t)b1[0], (uint32_t)b0[1], (uint32_t)b1[1]};
+          if constexpr (SK_BWD_DS_NT & 1) {
+            __builtin_nontemporal_store(c0, reinterpret_cast<u32x4*>(dst));
+            __builtin_nontemporal_store(c1, reinterpret_cast<u32x4*>(dst + 1024));
+          } else {
+            *reinterpret_cast<u32x4*>(dst) = c0;
+            *reinterpret_cast<u32x4*>(dst + 1024) = c1;
+          }
         }
         ds_m0 += BMQ;
         if (ds_m0 >= p.Sq) {
@@ -1398,8 +1411,13 @@ __global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
       const i32x4 dr =
           make_rsrc_words(ds_row[q] + (int64_t)t * p.ds_nqt * kDs, t < kt_lim[q] ? kDs : 0);
       const uint32_t sd = st + L::kTileBytes + (wave * QW + q) * kDs;
-      buffer_load_lds_b128(dr, sd, ds_goff[0]);
-      buffer_load_lds_b128(dr, sd + 1024, ds_goff[1]);
+      if constexpr (SK_BWD_DS_NT & 2) {
+        buffer_load_lds_b128_nt(dr, sd, ds_goff[0]);
+        buffer_load_lds_b128_nt(dr, sd + 1024, ds_goff[1]);
+      } else {
+        buffer_load_lds_b128(dr, sd, ds_goff[0]);
+        buffer_load_lds_b128(dr, sd + 1024, ds_goff[1]);
+      }
     }
   };
 

@@ -234,6 +234,19 @@ __device__ __forceinline__ void buffer_load_lds_b128(i32x4 rsrc, uint32_t lds_wa
       : "memory", "m0");
 }
 
+// buffer_load_lds_b128 with the non-temporal hint, for data read once
+// (streamed past the caches' reuse).
+__device__ __forceinline__ void buffer_load_lds_b128_nt(i32x4 rsrc, uint32_t lds_wave_base,
+                                                        uint32_t offset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen nt lds"
+      :
+      : "s"(lds_wave_base), "v"(offset), "s"(rsrc)
+      : "memory", "m0");
+}
+
 // 4 bytes per lane from a buffer straight into LDS: lane i writes
 // lds_wave_base + 4 * i.  Same contract as buffer_load_lds_b128.
 __device__ __forceinline__ void buffer_load_lds_b32(i32x4 rsrc, uint32_t lds_wave_base,
