@@ -225,7 +225,9 @@ def pick(
                      "table's kernels") + ")")
     if op_name in _FWD_OPS and code != 0 and 64 < prob["D"] <= 128:  # not fp32
         lines.append("Rejected Candidates: the other D = 128 forward entry of the table (short "
-                     "work: S_q <= 2048, causal S_q <= 4096 or fewer than 2048 blocks of 256 rows "
+                     "work: S_q <= 2048, causal S_q <= 4096 or fewer than 2048 blocks of 256 rows, "
+                     "unless a query row sees 4096 keys or more on average and the 8-wavefront "
+                     "grid stays even (no causal mask, paired blocks, or at most 256 blocks) "
                      "-> 4 wavefronts, two workgroups per CU, 2-deep ring; else 8 wavefronts, one "
                      "per CU, 4-deep ring)")
     else:

@@ -165,15 +165,11 @@ const char* sk_last_error(void) { return g_err; }
 
 // Sizes and work split of the forward: query blocks per (b, h) and, under
 // the causal mask, whether blocks j and n_mblocks-1-j are paired in one
-// workgroup (when that still leaves SK_FWD_PAIR_MIN paired workgroups, two
-// per CU; a tile-study build can raise it to keep every block on its own).
-#ifndef SK_FWD_PAIR_MIN
-#define SK_FWD_PAIR_MIN 512
-#endif
+// workgroup (when that still leaves SK_FWD_PAIR_MIN paired workgroups).
 static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
                      sk::FwdParams* p) {
   p->B = B, p->Hq = Hq, p->Hkv = Hkv, p->Sq = Sq, p->Sk = Sk, p->D = D, p->group = Hq / Hkv;
-  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D, (int64_t)B * Hq, Sq, is_causal != 0);
+  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D, (int64_t)B * Hq, Sq, Sk, is_causal != 0);
   p->n_mblocks = (Sq + rows - 1) / rows;
   if ((int64_t)p->n_mblocks * B * Hq > 0x7fffffffLL)
     return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p->n_mblocks * B * Hq);

@@ -629,16 +629,29 @@ static_assert(kFwdD128Short.stages == 4 || kFwdD128Short.stages == 2, "ring dept
 constexpr FwdTile kFwdD64Long{64, 8, 1, 4};
 constexpr FwdTile kFwdD64Short{64, 4, 2, 4};
 
-// Whether a D <= 128 forward over bh (batch, head) pairs of sq queries takes
-// the short-work entry.
-static bool fwd_short(int64_t bh, int sq, bool causal) {
-  const int64_t blocks8 = (int64_t)((sq + 255) / 256) * bh;  // 256-row blocks
-  return sq <= (causal ? 4096 : 2048) || blocks8 < 2048;
+// Whether a D <= 128 forward over bh (batch, head) pairs of sq queries
+// against sk keys takes the short-work entry: short query sequences or a
+// small grid, unless the query blocks see long runs of keys (on average at
+// least SK_FWD_LONG_KEYS, so the per-block fixed cost the short entry halves
+// is small) and the long entry's grid stays even (no causal mask, paired
+// blocks, or at most one workgroup per CU).
+static bool fwd_short(int64_t bh, int sq, int sk, bool causal) {
+  const int64_t n8 = (sq + 255) / 256;  // 256-row blocks of the long entry
+  const int64_t blocks8 = n8 * bh;
+  if (!(sq <= (causal ? 4096 : 2048) || blocks8 < 2048)) return false;
+  // Keys a query row sees on average (bottom-right causal: row i sees
+  // i + 1 + sk - sq of them, clamped to [0, sk]).
+  const int64_t keys = !causal ? sk
+                       : sk >= sq ? (int64_t)sk - sq / 2
+                                  : (int64_t)sk * sk / (2 * (int64_t)sq);
+  const bool even =
+      !causal || (n8 >= 2 && (n8 + 1) / 2 * bh >= SK_FWD_PAIR_MIN) || blocks8 <= 256;
+  return !(SK_FWD_LONG_KEYS > 0 && keys >= SK_FWD_LONG_KEYS && even);
 }
 
-static FwdConfig fwd_config(int d, int64_t bh, int sq, bool causal) {
+static FwdConfig fwd_config(int d, int64_t bh, int sq, int sk, bool causal) {
   if (d <= 128) {
-    const bool sh = fwd_short(bh, sq, causal);
+    const bool sh = fwd_short(bh, sq, sk, causal);
     const FwdTile t = d <= 64 ? (sh ? kFwdD64Short : kFwdD64Long)
                               : (sh ? kFwdD128Short : kFwdD128Long);
     return {d <= 64 ? 64 : 128, t.bn, t.nw, t.occ, t.stages};
@@ -646,9 +659,9 @@ static FwdConfig fwd_config(int d, int64_t bh, int sq, bool causal) {
   return {256, 32, 4, 1, 4};
 }
 
-int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, bool causal) {
+int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, int sk, bool causal) {
   (void)dtype;
-  return 32 * fwd_config(d, bh, sq, causal).nw;
+  return 32 * fwd_config(d, bh, sq, sk, causal).nw;
 }
 
 template <class T, int DP, int BN, int NW, int OCC, int STAGES = 4>
@@ -678,8 +691,8 @@ static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
 
 template <class T>
 static KernelPlan plan_fwd_dt(const FwdParams& p, bool causal) {
-  const bool sh = fwd_short((int64_t)p.B * p.Hq, p.Sq, causal);
-  switch (fwd_config(p.D, (int64_t)p.B * p.Hq, p.Sq, causal).dp) {
+  const bool sh = fwd_short((int64_t)p.B * p.Hq, p.Sq, p.Sk, causal);
+  switch (fwd_config(p.D, (int64_t)p.B * p.Hq, p.Sq, p.Sk, causal).dp) {
     case 64:
       if (sh)
         return plan_fwd_t<T, 64, kFwdD64Short.bn, kFwdD64Short.nw, kFwdD64Short.occ,

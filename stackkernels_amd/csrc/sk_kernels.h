@@ -6,6 +6,19 @@
 #include <stddef.h>
 #include <stdint.h>
 
+// Causal forward: blocks j and n_mblocks-1-j run in one workgroup when that
+// still leaves SK_FWD_PAIR_MIN workgroups (a tile-study build can raise it
+// to keep every block on its own).
+#ifndef SK_FWD_PAIR_MIN
+#define SK_FWD_PAIR_MIN 512
+#endif
+// Forward tile table: average visible keys per query row from which the
+// long-work entry is taken when its grid stays even (0: query length and
+// grid size alone decide).
+#ifndef SK_FWD_LONG_KEYS
+#define SK_FWD_LONG_KEYS 4096
+#endif
+
 namespace sk {
 
 // Rotary position embedding (rotate-half form) applied to a vector as it is
@@ -187,8 +200,8 @@ hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s);
 
 // Rows of queries one forward workgroup covers for (dtype, head dim, batch x
-// query heads, query length, causal mask).
-int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, bool causal);
+// query heads, query length, key length, causal mask).
+int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, int sk, bool causal);
 // Padded head dim the kernels are compiled for (64, 96, 128 or 256), or 0.
 int padded_head_dim(int d);
 

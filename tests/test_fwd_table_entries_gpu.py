@@ -3,9 +3,11 @@
 The table picks by shape: short work (S_q <= 2048, causal S_q <= 4096, or
 fewer than 2048 blocks of 256 rows in the grid) runs 4 waves with two
 workgroups per CU (a 2-deep K/V ring at D = 128, 4-deep at D = 64); long
-work runs 8 waves with one workgroup per CU on a 4-deep ring.  The
-BASELINE-size tests exercise the short entry, so these shapes sit just past
-its limits (and one long sequence on a small grid stays in it).  Each case first asserts which entry ``pick``
+work runs 8 waves with one workgroup per CU on a 4-deep ring, and so do
+query blocks that see 4,096 keys or more on average where the long entry's
+grid stays even.  The BASELINE-size tests exercise the short entry, so these
+shapes sit just past its limits (and one long sequence on a small grid stays
+in it), or pair short query sequences with long key sequences.  Each case first asserts which entry ``pick``
 reports, then checks heads at the start, middle and end of the batch against
 the float64 oracle: O within the stated 2e-2 max-abs, LSE within 1e-3.
 Inputs are generated on the device (seeded) so the large cases stay quick.
@@ -22,24 +24,29 @@ from _gpu_util import TOL, assert_close_maxabs, assert_lse_close, native_loaded,
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("b,h,s,d,causal,dt,rows", [
-    (8, 32, 2304, 128, False, torch.bfloat16, 256),  # non-causal past S_q = 2048, 2,304 blocks
-    (4, 32, 4352, 128, True, torch.bfloat16, 256),   # causal past S_q = 4096, 2,176 blocks
-    (8, 32, 2112, 128, False, torch.float16, 256),   # fp16, ragged last block
-    (1, 8, 5000, 128, True, torch.bfloat16, 128),    # long but a small grid: the short entry
-    (2, 16, 4096, 128, True, torch.float16, 128),    # causal S_q = 4096: the short entry
-    (4, 32, 4352, 64, True, torch.bfloat16, 256),    # D = 64, both entries
-    (2, 16, 2112, 64, False, torch.float16, 128),
+@pytest.mark.parametrize("b,h,s,sk,d,causal,dt,rows", [
+    (8, 32, 2304, 2304, 128, False, torch.bfloat16, 256),  # non-causal past S_q = 2048, 2,304 blocks
+    (4, 32, 4352, 4352, 128, True, torch.bfloat16, 256),   # causal past S_q = 4096, 2,176 blocks
+    (8, 32, 2112, 2112, 128, False, torch.float16, 256),   # fp16, ragged last block
+    (1, 8, 5000, 5000, 128, True, torch.bfloat16, 128),    # long but a small grid: the short entry
+    (2, 16, 4096, 4096, 128, True, torch.float16, 128),    # causal S_q = 4096: the short entry
+    (4, 32, 4352, 4352, 64, True, torch.bfloat16, 256),    # D = 64, both entries
+    (2, 16, 2112, 2112, 64, False, torch.float16, 128),
+    (4, 32, 2048, 8192, 128, True, torch.bfloat16, 256),   # long key rows, paired blocks
+    (2, 32, 2048, 8192, 128, True, torch.bfloat16, 128),   # the same rows, uneven grid: short
+    (2, 32, 2000, 8192, 128, False, torch.float16, 256),   # long key rows, no mask, ragged
+    (1, 32, 2048, 16384, 64, True, torch.bfloat16, 256),   # D = 64, 256 blocks in one round
 ])
-def test_forward_table_entry_matches_oracle(b, h, s, d, causal, dt, rows):
+def test_forward_table_entry_matches_oracle(b, h, s, sk, d, causal, dt, rows):
     from oracle import attention_oracle as orc
 
     name = {torch.bfloat16: "bfloat16", torch.float16: "float16"}[dt]
-    cfg = pick("flash_attn", (b, h, s, d), dtype=name, is_causal=causal)
+    cfg = pick("flash_attn", (b, h, s, d), dtype=name, kv_len=sk, is_causal=causal)
     assert cfg["BLOCK_M"] == rows and cfg["num_warps"] == rows // 32
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(s)
-    q, k, v = (torch.randn(b, h, s, d, generator=g, device=dev, dtype=dt) for _ in range(3))
+    g = torch.Generator(device=dev).manual_seed(s + sk)
+    q = torch.randn(b, h, s, d, generator=g, device=dev, dtype=dt)
+    k, v = (torch.randn(b, h, sk, d, generator=g, device=dev, dtype=dt) for _ in range(2))
     out, lse = flash_attn_fwd(q, k, v, is_causal=causal)
     torch.cuda.synchronize()
     assert native_loaded()
@@ -48,6 +55,6 @@ def test_forward_table_entry_matches_oracle(b, h, s, d, causal, dt, rows):
             return t[bi:bi + 1, hi:hi + 1]
 
         o_ref, lse_ref = orc.attention_forward(np64(sl(q)), np64(sl(k)), np64(sl(v)), causal)
-        what = f"(b={bi}, h={hi}, S={s}, D={d}, causal={causal}, {name})"
+        what = f"(b={bi}, h={hi}, S_q={s}, S_k={sk}, D={d}, causal={causal}, {name})"
         assert_close_maxabs(sl(out), o_ref, TOL[dt], "O " + what)
         assert_lse_close(sl(lse), lse_ref, "LSE " + what)

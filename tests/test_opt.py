@@ -123,6 +123,17 @@ def test_pick_forward_and_backward():
     # long but a small grid: the short-work entry again
     sm = pick("flash_attn", (1, 8, 16384, 128), dtype="bfloat16", is_causal=True)
     assert (sm["BLOCK_M"], sm["num_warps"], sm["num_stages"]) == (128, 4, 2)
+    # short query sequences against long key sequences: the 8-wave entry where its grid
+    # stays even (paired blocks, no mask, or at most 256 blocks), the short one elsewhere
+    def rows(b, sq, sk, causal):
+        return pick("flash_attn", (b, 32, sq, 128), dtype="bfloat16", kv_len=sk,
+                    num_kv_heads=8, is_causal=causal)["BLOCK_M"]
+    assert rows(2, 2048, 8192, True) == 128    # 512 unpaired 256-row blocks: uneven
+    assert rows(4, 2048, 8192, True) == 256    # 512 paired workgroups
+    assert rows(2, 2048, 8192, False) == 256   # no mask
+    assert rows(1, 2048, 16384, True) == 256   # 256 blocks, one round
+    assert rows(4, 2048, 4096, True) == 128    # 3,072 keys per row on average
+    assert rows(4, 4096, 4096, False) == 256   # full grid (unchanged)
     d256 = pick("flash_fwd", (1, 8, 512, 256), dtype="float16")
     assert (d256["BLOCK_M"], d256["BLOCK_N"], d256["num_warps"]) == (128, 32, 4)
     f32 = pick("flash_attn", (1, 8, 512, 64), dtype="float32")
