@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "7a3abbb4d4d143b20302cb12bff5d04f041828a40374129696d656879c015e58"
+TRAFFIC_SOURCES_SHA256 = "e016427e5a883764e12c804204797b6ba409819cd0b42bf09720f8f8455675b8"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 682_459_545,
-    "fwd_long": 844_382_362,
-    "fwdbwd": 4_539_090_415,
-    "decode": 8_612_473_664,
-    "decode_mqa": 573_007_050,
-    "decode_varlen": 4_305_218_731,
+    "fwd": 679_929_543,
+    "fwd_long": 847_755_123,
+    "fwdbwd": 4_551_480_224,
+    "decode": 8_612_473_658,
+    "decode_mqa": 573_007_081,
+    "decode_varlen": 4_305_218_773,
     "kv_update": 67_240_132,
-    "decode_paged": 4_305_360_243,
-    "decode_rope": 8_612_484_952,
-    "kv_update_rope": 75_523_404,
-    "decode_step": 4_306_745_776,
+    "decode_paged": 4_305_360_173,
+    "decode_rope": 8_612_484_940,
+    "kv_update_rope": 75_523_294,
+    "decode_step": 4_306_745_673,
 }
 
 
