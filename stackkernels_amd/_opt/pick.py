@@ -227,7 +227,8 @@ def pick(
         lines.append("Rejected Candidates: the other D = 128 forward entry of the table (short "
                      "work: S_q <= 2048, causal S_q <= 4096 or fewer than 2048 blocks of 256 rows, "
                      "unless a query row sees 4096 keys or more on average and the 8-wavefront "
-                     "grid stays even (no causal mask, paired blocks, or at most 256 blocks) "
+                     "workgroups fill whole rounds of the 256 CUs (a multiple of 256, or 2048 "
+                     "or more) "
                      "-> 4 wavefronts, two workgroups per CU, 2-deep ring; else 8 wavefronts, one "
                      "per CU, 4-deep ring)")
     else:

@@ -165,7 +165,7 @@ const char* sk_last_error(void) { return g_err; }
 
 // Sizes and work split of the forward: query blocks per (b, h) and, under
 // the causal mask, whether blocks j and n_mblocks-1-j are paired in one
-// workgroup (when that still leaves SK_FWD_PAIR_MIN paired workgroups).
+// workgroup (when that still leaves enough workgroups: fwd_pair_min).
 static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
                      sk::FwdParams* p) {
   p->B = B, p->Hq = Hq, p->Hkv = Hkv, p->Sq = Sq, p->Sk = Sk, p->D = D, p->group = Hq / Hkv;
@@ -174,7 +174,8 @@ static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, i
   if ((int64_t)p->n_mblocks * B * Hq > 0x7fffffffLL)
     return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p->n_mblocks * B * Hq);
   p->pair_items = dtype != SK_F32 && is_causal && p->n_mblocks >= 2 &&
-                  (int64_t)((p->n_mblocks + 1) / 2) * B * Hq >= SK_FWD_PAIR_MIN;
+                  (int64_t)((p->n_mblocks + 1) / 2) * B * Hq >=
+                      sk::fwd_pair_min(dtype, D, (int64_t)B * Hq, Sq, Sk, is_causal != 0);
   p->n_items = p->pair_items ? (p->n_mblocks + 1) / 2 : p->n_mblocks;
   return SK_OK;
 }

@@ -633,8 +633,8 @@ constexpr FwdTile kFwdD64Short{64, 4, 2, 4};
 // against sk keys takes the short-work entry: short query sequences or a
 // small grid, unless the query blocks see long runs of keys (on average at
 // least SK_FWD_LONG_KEYS, so the per-block fixed cost the short entry halves
-// is small) and the long entry's grid stays even (no causal mask, paired
-// blocks, or at most one workgroup per CU).
+// is small) and the long entry's workgroups fill whole rounds of the 256 CUs
+// (a multiple of 256, or 2,048 or more).
 static bool fwd_short(int64_t bh, int sq, int sk, bool causal) {
   const int64_t n8 = (sq + 255) / 256;  // 256-row blocks of the long entry
   const int64_t blocks8 = n8 * bh;
@@ -644,8 +644,9 @@ static bool fwd_short(int64_t bh, int sq, int sk, bool causal) {
   const int64_t keys = !causal ? sk
                        : sk >= sq ? (int64_t)sk - sq / 2
                                   : (int64_t)sk * sk / (2 * (int64_t)sq);
-  const bool even =
-      !causal || (n8 >= 2 && (n8 + 1) / 2 * bh >= SK_FWD_PAIR_MIN) || blocks8 <= 256;
+  const bool paired = causal && n8 >= 2 && (n8 + 1) / 2 * bh >= SK_FWD_PAIR_MIN_LONG;
+  const int64_t g8 = paired ? (n8 + 1) / 2 * bh : blocks8;  // long-entry workgroups
+  const bool even = g8 % 256 == 0 || g8 >= 2048;
   return !(SK_FWD_LONG_KEYS > 0 && keys >= SK_FWD_LONG_KEYS && even);
 }
 
@@ -662,6 +663,11 @@ static FwdConfig fwd_config(int d, int64_t bh, int sq, int sk, bool causal) {
 int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, int sk, bool causal) {
   (void)dtype;
   return 32 * fwd_config(d, bh, sq, sk, causal).nw;
+}
+
+int fwd_pair_min(int dtype, int d, int64_t bh, int sq, int sk, bool causal) {
+  (void)dtype;
+  return d <= 128 && !fwd_short(bh, sq, sk, causal) ? SK_FWD_PAIR_MIN_LONG : SK_FWD_PAIR_MIN;
 }
 
 template <class T, int DP, int BN, int NW, int OCC, int STAGES = 4>

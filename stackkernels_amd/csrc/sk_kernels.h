@@ -7,10 +7,15 @@
 #include <stdint.h>
 
 // Causal forward: blocks j and n_mblocks-1-j run in one workgroup when that
-// still leaves SK_FWD_PAIR_MIN workgroups (a tile-study build can raise it
-// to keep every block on its own).
+// still leaves one round of workgroups on 256 CUs: SK_FWD_PAIR_MIN for the
+// entries with two workgroups per CU, SK_FWD_PAIR_MIN_LONG for the 8-wave
+// D <= 128 entry with one (a tile-study build can raise them to keep every
+// block on its own).
 #ifndef SK_FWD_PAIR_MIN
 #define SK_FWD_PAIR_MIN 512
+#endif
+#ifndef SK_FWD_PAIR_MIN_LONG
+#define SK_FWD_PAIR_MIN_LONG 256
 #endif
 // Forward tile table: average visible keys per query row from which the
 // long-work entry is taken when its grid stays even (0: query length and
@@ -202,6 +207,9 @@ hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s);
 // Rows of queries one forward workgroup covers for (dtype, head dim, batch x
 // query heads, query length, key length, causal mask).
 int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, int sk, bool causal);
+// Fewest paired workgroups for which a causal forward of that shape pairs
+// its query blocks.
+int fwd_pair_min(int dtype, int d, int64_t bh, int sq, int sk, bool causal);
 // Padded head dim the kernels are compiled for (64, 96, 128 or 256), or 0.
 int padded_head_dim(int d);
 

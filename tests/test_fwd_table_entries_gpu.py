@@ -5,7 +5,7 @@ fewer than 2048 blocks of 256 rows in the grid) runs 4 waves with two
 workgroups per CU (a 2-deep K/V ring at D = 128, 4-deep at D = 64); long
 work runs 8 waves with one workgroup per CU on a 4-deep ring, and so do
 query blocks that see 4,096 keys or more on average where the long entry's
-grid stays even.  The BASELINE-size tests exercise the short entry, so these
+workgroups fill whole rounds of the 256 CUs.  The BASELINE-size tests exercise the short entry, so these
 shapes sit just past its limits (and one long sequence on a small grid stays
 in it), or pair short query sequences with long key sequences.  Each case first asserts which entry ``pick``
 reports, then checks heads at the start, middle and end of the batch against
@@ -33,7 +33,8 @@ pytestmark = pytest.mark.gpu
     (4, 32, 4352, 4352, 64, True, torch.bfloat16, 256),    # D = 64, both entries
     (2, 16, 2112, 2112, 64, False, torch.float16, 128),
     (4, 32, 2048, 8192, 128, True, torch.bfloat16, 256),   # long key rows, paired blocks
-    (2, 32, 2048, 8192, 128, True, torch.bfloat16, 128),   # the same rows, uneven grid: short
+    (2, 32, 2048, 8192, 128, True, torch.bfloat16, 256),   # the same rows, 256 paired workgroups
+    (1, 32, 2048, 4608, 128, True, torch.float16, 128),    # 3,584 keys per row on average: short
     (2, 32, 2000, 8192, 128, False, torch.float16, 256),   # long key rows, no mask, ragged
     (1, 32, 2048, 16384, 64, True, torch.bfloat16, 256),   # D = 64, 256 blocks in one round
 ])

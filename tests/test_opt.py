@@ -120,20 +120,32 @@ def test_pick_forward_and_backward():
     lg = pick("flash_attn", (1, 32, 16384, 128), dtype="bfloat16", is_causal=True)
     assert (lg["BLOCK_M"], lg["BLOCK_N"], lg["num_warps"], lg["num_stages"]) == (256, 64, 8, 4)
     assert lg["grid"] == 32 * 32
-    # long but a small grid: the short-work entry again
-    sm = pick("flash_attn", (1, 8, 16384, 128), dtype="bfloat16", is_causal=True)
+    # long but a small grid: the short-work entry again where the 8-wave grid would leave
+    # part of a round idle (384 paired workgroups on 256 CUs), the 8-wave one where it
+    # fills one round (256 paired workgroups)
+    sm = pick("flash_attn", (1, 24, 8192, 128), dtype="bfloat16", is_causal=True)
     assert (sm["BLOCK_M"], sm["num_warps"], sm["num_stages"]) == (128, 4, 2)
+    sm8 = pick("flash_attn", (1, 8, 16384, 128), dtype="bfloat16", is_causal=True)
+    assert (sm8["BLOCK_M"], sm8["num_warps"], sm8["num_stages"]) == (256, 8, 4)
+    assert sm8["paired_causal_blocks"] and sm8["grid"] == 256
     # short query sequences against long key sequences: the 8-wave entry where its grid
-    # stays even (paired blocks, no mask, or at most 256 blocks), the short one elsewhere
+    # fills whole rounds of 256 workgroups, the short one elsewhere
     def rows(b, sq, sk, causal):
         return pick("flash_attn", (b, 32, sq, 128), dtype="bfloat16", kv_len=sk,
                     num_kv_heads=8, is_causal=causal)["BLOCK_M"]
-    assert rows(2, 2048, 8192, True) == 128    # 512 unpaired 256-row blocks: uneven
+    assert rows(2, 2048, 8192, True) == 256    # 256 paired workgroups (one per CU)
+    assert rows(2, 1024, 8192, True) == 256    # 256 blocks, one round, unpaired
+    assert rows(1, 2048, 4608, True) == 128    # 3,584 keys per row on average
     assert rows(4, 2048, 8192, True) == 256    # 512 paired workgroups
     assert rows(2, 2048, 8192, False) == 256   # no mask
     assert rows(1, 2048, 16384, True) == 256   # 256 blocks, one round
     assert rows(4, 2048, 4096, True) == 128    # 3,072 keys per row on average
     assert rows(4, 4096, 4096, False) == 256   # full grid (unchanged)
+    assert rows(3, 2048, 8192, False) == 256   # 768 blocks of 256 rows: 3 whole rounds
+    assert rows(6, 2048, 8192, True) == 256    # 768 paired workgroups: 3 whole rounds
+    for b, h, causal in ((1, 40, False), (3, 40, True)):  # 320 blocks; 480 paired workgroups
+        assert pick("flash_attn", (b, h, 2048, 128), dtype="bfloat16", kv_len=8192,
+                    is_causal=causal)["BLOCK_M"] == 128
     d256 = pick("flash_fwd", (1, 8, 512, 256), dtype="float16")
     assert (d256["BLOCK_M"], d256["BLOCK_N"], d256["num_warps"]) == (128, 32, 4)
     f32 = pick("flash_attn", (1, 8, 512, 64), dtype="float32")
