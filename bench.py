@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "e016427e5a883764e12c804204797b6ba409819cd0b42bf09720f8f8455675b8"
+TRAFFIC_SOURCES_SHA256 = "6fb8193ba035a0e9202201c54f7b6e5eebc40498e480136c83a159f36eb67f61"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 679_929_543,
-    "fwd_long": 847_755_123,
-    "fwdbwd": 4_551_480_224,
-    "decode": 8_612_473_658,
-    "decode_mqa": 573_007_081,
-    "decode_varlen": 4_305_218_773,
-    "kv_update": 67_240_132,
-    "decode_paged": 4_305_360_173,
-    "decode_rope": 8_612_484_940,
-    "kv_update_rope": 75_523_294,
-    "decode_step": 4_306_745_673,
+    "fwd": 682_022_659,
+    "fwd_long": 841_517_817,
+    "fwdbwd": 4_539_297_847,
+    "decode": 8_612_473_663,
+    "decode_mqa": 573_007_175,
+    "decode_varlen": 4_305_218_629,
+    "kv_update": 67_240_126,
+    "decode_paged": 4_305_360_105,
+    "decode_rope": 8_612_484_945,
+    "kv_update_rope": 75_523_374,
+    "decode_step": 4_306_745_472,
 }
 
 
