@@ -635,7 +635,7 @@ constexpr FwdTile kFwdD64Short{64, 4, 2, 4};
 // least SK_FWD_LONG_KEYS, so the per-block fixed cost the short entry halves
 // is small) and the long entry's workgroups fill whole rounds of the 256 CUs
 // (a multiple of 256, or 2,048 or more).
-static bool fwd_short(int64_t bh, int sq, int sk, bool causal) {
+static bool fwd_short(int d, int64_t bh, int sq, int sk, bool causal) {
   const int64_t n8 = (sq + 255) / 256;  // 256-row blocks of the long entry
   const int64_t blocks8 = n8 * bh;
   if (!(sq <= (causal ? 4096 : 2048) || blocks8 < 2048)) return false;
@@ -644,7 +644,8 @@ static bool fwd_short(int64_t bh, int sq, int sk, bool causal) {
   const int64_t keys = !causal ? sk
                        : sk >= sq ? (int64_t)sk - sq / 2
                                   : (int64_t)sk * sk / (2 * (int64_t)sq);
-  const bool paired = causal && n8 >= 2 && (n8 + 1) / 2 * bh >= SK_FWD_PAIR_MIN_LONG;
+  const int occ8 = d <= 64 ? kFwdD64Long.occ : kFwdD128Long.occ;
+  const bool paired = causal && n8 >= 2 && (n8 + 1) / 2 * bh >= 256LL * occ8 * SK_FWD_PAIR_ROUNDS;
   const int64_t g8 = paired ? (n8 + 1) / 2 * bh : blocks8;  // long-entry workgroups
   const bool even = g8 % 256 == 0 || g8 >= 2048;
   return !(SK_FWD_LONG_KEYS > 0 && keys >= SK_FWD_LONG_KEYS && even);
@@ -652,7 +653,7 @@ static bool fwd_short(int64_t bh, int sq, int sk, bool causal) {
 
 static FwdConfig fwd_config(int d, int64_t bh, int sq, int sk, bool causal) {
   if (d <= 128) {
-    const bool sh = fwd_short(bh, sq, sk, causal);
+    const bool sh = fwd_short(d, bh, sq, sk, causal);
     const FwdTile t = d <= 64 ? (sh ? kFwdD64Short : kFwdD64Long)
                               : (sh ? kFwdD128Short : kFwdD128Long);
     return {d <= 64 ? 64 : 128, t.bn, t.nw, t.occ, t.stages};
@@ -667,7 +668,7 @@ int fwd_rows_per_block(int dtype, int d, int64_t bh, int sq, int sk, bool causal
 
 int fwd_pair_min(int dtype, int d, int64_t bh, int sq, int sk, bool causal) {
   (void)dtype;
-  return d <= 128 && !fwd_short(bh, sq, sk, causal) ? SK_FWD_PAIR_MIN_LONG : SK_FWD_PAIR_MIN;
+  return 256 * fwd_config(d, bh, sq, sk, causal).occ * SK_FWD_PAIR_ROUNDS;
 }
 
 template <class T, int DP, int BN, int NW, int OCC, int STAGES = 4>
@@ -697,7 +698,7 @@ static KernelPlan plan_fwd_t(const FwdParams& p, bool causal) {
 
 template <class T>
 static KernelPlan plan_fwd_dt(const FwdParams& p, bool causal) {
-  const bool sh = fwd_short((int64_t)p.B * p.Hq, p.Sq, p.Sk, causal);
+  const bool sh = fwd_short(p.D, (int64_t)p.B * p.Hq, p.Sq, p.Sk, causal);
   switch (fwd_config(p.D, (int64_t)p.B * p.Hq, p.Sq, p.Sk, causal).dp) {
     case 64:
       if (sh)

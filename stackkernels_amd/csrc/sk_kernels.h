@@ -6,16 +6,12 @@
 #include <stddef.h>
 #include <stdint.h>
 
-// Causal forward: blocks j and n_mblocks-1-j run in one workgroup when that
-// still leaves one round of workgroups on 256 CUs: SK_FWD_PAIR_MIN for the
-// entries with two workgroups per CU, SK_FWD_PAIR_MIN_LONG for the 8-wave
-// D <= 128 entry with one (a tile-study build can raise them to keep every
-// block on its own).
-#ifndef SK_FWD_PAIR_MIN
-#define SK_FWD_PAIR_MIN 512
-#endif
-#ifndef SK_FWD_PAIR_MIN_LONG
-#define SK_FWD_PAIR_MIN_LONG 256
+// Causal forward: blocks j and n_mblocks-1-j run in one workgroup when the
+// paired workgroups still fill SK_FWD_PAIR_ROUNDS rounds of the 256 CUs at
+// the table entry's workgroups per CU (a tile-study build can raise it to
+// keep every block on its own).
+#ifndef SK_FWD_PAIR_ROUNDS
+#define SK_FWD_PAIR_ROUNDS 1
 #endif
 // Forward tile table: average visible keys per query row from which the
 // long-work entry is taken when its grid stays even (0: query length and

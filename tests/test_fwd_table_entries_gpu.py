@@ -37,6 +37,7 @@ pytestmark = pytest.mark.gpu
     (1, 32, 2048, 4608, 128, True, torch.float16, 128),    # 3,584 keys per row on average: short
     (2, 32, 2000, 8192, 128, False, torch.float16, 256),   # long key rows, no mask, ragged
     (1, 32, 2048, 16384, 64, True, torch.bfloat16, 256),   # D = 64, 256 blocks in one round
+    (1, 16, 4096, 4096, 256, True, torch.bfloat16, 128),   # D = 256, 256 paired workgroups
 ])
 def test_forward_table_entry_matches_oracle(b, h, s, sk, d, causal, dt, rows):
     from oracle import attention_oracle as orc

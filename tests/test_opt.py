@@ -148,6 +148,14 @@ def test_pick_forward_and_backward():
                     is_causal=causal)["BLOCK_M"] == 128
     d256 = pick("flash_fwd", (1, 8, 512, 256), dtype="float16")
     assert (d256["BLOCK_M"], d256["BLOCK_N"], d256["num_warps"]) == (128, 32, 4)
+    # causal blocks are paired while the paired grid fills one round: 256 workgroups at one
+    # per CU (D = 256, the 8-wave entry), 512 at two per CU (the short-work entry)
+    p256 = pick("flash_fwd", (1, 16, 4096, 256), dtype="bfloat16", is_causal=True)
+    assert p256["paired_causal_blocks"] and p256["grid"] == 256
+    u256 = pick("flash_fwd", (1, 8, 4096, 256), dtype="bfloat16", is_causal=True)
+    assert not u256["paired_causal_blocks"] and u256["grid"] == 256
+    s128 = pick("flash_fwd", (1, 16, 4096, 128), dtype="bfloat16", is_causal=True)
+    assert s128["BLOCK_M"] == 128 and not s128["paired_causal_blocks"] and s128["grid"] == 512
     f32 = pick("flash_attn", (1, 8, 512, 64), dtype="float32")
     assert f32["kernel_variant"] == "fwd_f32_kernel"
     b = pick("flash_bwd", (2, 32, 2048, 128), dtype="bfloat16", kv_len=8192, num_kv_heads=8,
