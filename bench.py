@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "6fb8193ba035a0e9202201c54f7b6e5eebc40498e480136c83a159f36eb67f61"
+TRAFFIC_SOURCES_SHA256 = "fa9388dbc2bd0c71541fb099f987d6f91d4fa1b51f49264ced35e6b5cefc6ed1"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 682_022_659,
-    "fwd_long": 841_517_817,
-    "fwdbwd": 4_539_297_847,
-    "decode": 8_612_473_663,
-    "decode_mqa": 573_007_175,
-    "decode_varlen": 4_305_218_629,
-    "kv_update": 67_240_126,
-    "decode_paged": 4_305_360_105,
-    "decode_rope": 8_612_484_945,
-    "kv_update_rope": 75_523_374,
-    "decode_step": 4_306_745_472,
+    "fwd": 679_832_706,
+    "fwd_long": 847_654_650,
+    "fwdbwd": 4_552_900_127,
+    "decode": 8_612_473_677,
+    "decode_mqa": 573_007_102,
+    "decode_varlen": 4_305_218_702,
+    "kv_update": 67_240_134,
+    "decode_paged": 4_305_360_111,
+    "decode_rope": 8_612_484_943,
+    "kv_update_rope": 75_523_400,
+    "decode_step": 4_306_745_642,
 }
 
 
