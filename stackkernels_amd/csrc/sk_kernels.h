@@ -14,8 +14,8 @@
 #define SK_FWD_PAIR_ROUNDS 1
 #endif
 // Forward tile table: average visible keys per query row from which the
-// long-work entry is taken when its grid stays even (0: query length and
-// grid size alone decide).
+// long-work entry is taken when its workgroups fill whole rounds of the CUs
+// (0: query length and grid size alone decide).
 #ifndef SK_FWD_LONG_KEYS
 #define SK_FWD_LONG_KEYS 4096
 #endif
