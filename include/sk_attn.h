@@ -41,7 +41,7 @@ extern "C" {
 #define SK_API
 #endif
 
-#define SK_ABI_VERSION 6
+#define SK_ABI_VERSION 7
 
 /* Element type codes. */
 #define SK_F32 0
@@ -80,17 +80,37 @@ SK_API int sk_attn_fwd(int dtype, const void* q, const void* k, const void* v, v
                 int is_causal, float sm_scale, void* stream);
 
 /*
- * Bytes of scratch sk_attn_bwd needs for these dims: two fp32 row statistics
- * per query row (delta = rowsum(dO * O) and lse * log2(e)) and, where the
- * five-GEMM backward runs (16-bit inputs, head dim 65-128), dS in 16-bit
- * 32 x 32 tiles: B * Hq * ceil(Sk / 32) * ceil(Sq / 32) * 2048 bytes (2.1 GB
- * at B = 2, Hq = 32, Sq = 2048, Sk = 8192); shapes whose tiles would exceed
- * 4 GiB run the seven-GEMM backward without them.  Replaces
- * allocate_delta_buffer
+ * Most bytes of dS tiles one sk_attn_bwd call uses (2 GiB), whatever the
+ * shape and the workspace it is given.
+ */
+#define SK_BWD_DS_CAP_BYTES 2147483648ULL
+
+/*
+ * Preferred bytes of scratch for sk_attn_bwd with these dims: the two fp32
+ * row statistics per query row (delta = rowsum(dO * O) and lse * log2(e),
+ * each array rounded up to 256 bytes: the minimum,
+ * sk_attn_bwd_workspace_min) and, where the five-GEMM backward runs (16-bit
+ * inputs, head dim 65-128), its 16-bit 32 x 32 dS tiles for one chunk of
+ * (batch, KV head) pairs.  Each pair needs 2048 bytes per tile that a
+ * visible 128-key block writes, for each of its Hq / Hkv query heads: about
+ * Sq * Sk * 2 bytes per query head, half that under a square causal mask
+ * (117 MB per pair at B = 2, Hq = 32, Hkv = 8, Sq = 2048, Sk = 8192 causal,
+ * so 1.88 GB for all 16 pairs).  The chunk is the whole batch where that
+ * fits under SK_BWD_DS_CAP_BYTES, else the fewest even chunks that do; when
+ * one pair's tiles exceed the cap the seven-GEMM backward runs and the
+ * minimum is all it needs.  Replaces allocate_delta_buffer
  * (reference: src/stackkernels/_opt/memory/workspace.py:16-23).
  */
 SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
                           int is_causal, size_t* bytes);
+
+/*
+ * Minimum bytes of scratch for sk_attn_bwd: the two row statistics, with
+ * which it runs the seven-GEMM backward.  The reference's counterpart is
+ * the same delta buffer (src/stackkernels/_opt/memory/workspace.py:16-23).
+ */
+SK_API int sk_attn_bwd_workspace_min(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                              int is_causal, size_t* bytes);
 
 /*
  * Backward attention.  Replaces flash_attn_bwd
@@ -101,11 +121,16 @@ SK_API int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int 
  * All tensors contiguous BHSD: dout, q, o, dq (B,Hq,Sq,D); k, v, dk, dv
  * (B,Hkv,Sk,D); lse (B,Hq,Sq) fp32 as written by sk_attn_fwd.  dk and dv are
  * summed over the query heads that share a KV head.  Rows with lse = -inf
- * contribute nothing.  workspace: >= sk_attn_bwd_workspace() bytes, any
- * contents (the call initialises what it uses).  Five-GEMM backward (head
- * dim 65-128, 16-bit): the dK/dV kernel stores dS in the workspace and the
- * dQ kernel reads it, both on `stream`.  Seven-GEMM backward (other head
- * dims): when the dK/dV grid runs more than one round of workgroups (more
+ * contribute nothing.  workspace: at least sk_attn_bwd_workspace_min()
+ * bytes (SK_EWORKSPACE otherwise), any contents (the call initialises what
+ * it uses).  Five-GEMM backward (head dim 65-128, 16-bit), when the bytes
+ * past the row statistics hold one (batch, KV head) pair's dS tiles: the
+ * pairs run in the fewest even chunks whose tiles fit those bytes (at most
+ * SK_BWD_DS_CAP_BYTES of them); for each chunk the dK/dV kernel stores dS in
+ * the workspace and the dQ kernel reads it, both on `stream`.  The results
+ * are the same bit for bit for every chunking and equal the seven-GEMM
+ * backward's.  Seven-GEMM backward (other head dims, fp32, or a workspace
+ * too small for one pair's tiles): when the dK/dV grid runs more than one round of workgroups (more
  * than 256 workgroups), the dQ kernel runs on the library's side stream for
  * `stream`, forked from `stream` after the preprocess pass and joined back
  * into it (also when a launch fails); under graph capture the fork and the
@@ -374,6 +399,7 @@ SK_API int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v
 #define SK_CFG_LDS_BYTES 10     /* device-reported, or -1                       */
 #define SK_CFG_VGPRS 11         /* device-reported registers per lane, or -1    */
 #define SK_CFG_WG_PER_CU 12     /* device-reported resident workgroups per CU, or -1 */
+#define SK_CFG_CHUNKS 13        /* backward: launches of the kernel per call (chunks of pairs) */
 #define SK_CFG_LEN 16
 
 SK_API int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,

@@ -15,7 +15,7 @@ import threading
 
 SK_F32, SK_F16, SK_BF16 = 0, 1, 2
 SK_OK, SK_EINVAL, SK_EUNSUPPORTED, SK_EWORKSPACE = 0, -1, -2, -3
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "csrc")
 LIB_PATH = os.environ.get("SK_ATTN_LIB", os.path.join(_LIB_DIR, "libsk_attn.so"))
@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple] = {
                              _i64p, _i64p, _i64p, _i64p, _c_int, _c_float, _vp]),
     "sk_attn_bwd_workspace": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                        _c_int, _sizep]),
+    "sk_attn_bwd_workspace_min": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                           _c_int, _c_int, _sizep]),
     "sk_attn_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                              ctypes.c_size_t, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_int, _c_float, _vp]),

@@ -20,12 +20,26 @@ from stackkernels_amd._core.attention import _lib
 
 def bwd_workspace(dtype: torch.dtype, B: int, Hq: int, Hkv: int, Sq: int, Sk: int, D: int,
                   is_causal: bool, device) -> torch.Tensor:
-    """uint8 scratch for ``sk_attn_bwd`` (D: the kernel head dim; at least 16 bytes)."""
+    """uint8 scratch for ``sk_attn_bwd`` (D: the kernel head dim; at least 16 bytes).
+
+    The library's preferred size (row statistics plus one chunk of the
+    five-GEMM backward's dS tiles, at most ``SK_BWD_DS_CAP_BYTES`` of them);
+    if torch cannot allocate that, the minimum (row statistics only), with
+    which the call runs the seven-GEMM backward: the same results, slower.
+    """
+    lib = _lib.load()
+    code = _lib.dtype_code(dtype)
+    args = (code, B, Hq, Hkv, Sq, Sk, D, int(bool(is_causal)))
     nb = ctypes.c_size_t(0)
-    _lib.check(_lib.load().sk_attn_bwd_workspace(_lib.dtype_code(dtype), B, Hq, Hkv, Sq, Sk, D,
-                                                 int(bool(is_causal)), ctypes.byref(nb)),
-               "flash_attn_bwd")
-    return torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device)
+    _lib.check(lib.sk_attn_bwd_workspace(*args, ctypes.byref(nb)), "flash_attn_bwd")
+    nmin = ctypes.c_size_t(0)
+    _lib.check(lib.sk_attn_bwd_workspace_min(*args, ctypes.byref(nmin)), "flash_attn_bwd")
+    try:
+        return torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device)
+    except torch.OutOfMemoryError:
+        if nb.value <= nmin.value:
+            raise
+    return torch.empty(max(nmin.value, 16), dtype=torch.uint8, device=device)
 
 
 def decode_workspace(dtype: torch.dtype, B: int, Hq: int, Hkv: int, Sk: int, D: int, device,

@@ -40,7 +40,7 @@ _DTYPE_CODES = {"float32": 0, "fp32": 0, "float": 0, "float16": 1, "fp16": 1, "h
 _OP_FWD, _OP_BWD_DKV, _OP_BWD_DQ, _OP_DECODE, _OP_DECODE_COMBINE = 0, 1, 2, 3, 4
 _VARIANT_PAGED, _VARIANT_ROPE = 1, 2
 _SLOTS = ("grid", "threads", "block_m", "block_n", "stages", "head_dim", "splits", "paired",
-          "workspace_bytes", "keys_per_split", "lds_bytes", "vgprs", "wg_per_cu")
+          "workspace_bytes", "keys_per_split", "lds_bytes", "vgprs", "wg_per_cu", "chunks")
 
 
 def _dtype_code(dtype: Any) -> int:
@@ -163,6 +163,9 @@ def pick(
         config["kernel_variant"] = f"{config['kernel_variant']}+{dq['kernel'].split('<')[0]}"
         config["dq"] = _public(dq)
         config["workspace_bytes"] = dkv["workspace_bytes"]
+        # launches of each kernel per call: chunks of (batch, KV head) pairs
+        # whose dS tiles fit the workspace (1 for the seven-GEMM backward)
+        config["chunks"] = dkv["chunks"]
     else:
         k = kernel_config(_OP_DECODE, code, prob, splits_req, variant, query)
         kernels.append(k)
@@ -217,6 +220,10 @@ def pick(
     if op_name in _DECODE_OPS:
         lines.append(f"  - split-KV: {config['SPLIT_KV']} splits of {config['keys_per_split']} keys, "
                      f"{config['workspace_bytes']} bytes of partials")
+    if op_name in _BWD_OPS:
+        lines.append(f"  - workspace: {config['workspace_bytes']} bytes; each kernel runs "
+                     f"{config['chunks']} launch(es), one per chunk of (batch, KV head) pairs "
+                     f"whose dS tiles fit (at most 2 GiB of tiles)")
     lines += ["Selected Configuration:", f"  - {chosen}"]
     if override:
         honoured = op_name in _DECODE_OPS and set(override) <= {"SPLIT_KV"}

@@ -146,11 +146,30 @@ int make_rope(const void* cos, const void* sin, int rope_dtype, int rope_rows,
   return SK_OK;
 }
 
-// Backward scratch: delta and lse * log2(e) (fp32 per query row), then the
-// dS tiles of the five-GEMM backward where it runs.
-size_t bwd_ws_bytes(int dtype, int B, int Hq, int Sq, int Sk, int D) {
+// Backward scratch: delta and lse * log2(e) (fp32 per query row, each array
+// rounded up to 256 bytes), then, for the five-GEMM backward, the dS tiles of
+// one chunk of (batch, KV head) pairs.
+size_t bwd_rows_bytes(int B, int Hq, int Sq) {
   const size_t rows = (size_t)B * Hq * Sq;
-  return 2 * ((rows * sizeof(float) + 255) / 256 * 256) + sk::bwd_ds_bytes(dtype, B, Hq, Sq, Sk, D);
+  return 2 * ((rows * sizeof(float) + 255) / 256 * 256);
+}
+
+// Pairs per chunk of the five-GEMM backward when at most `budget` bytes of
+// dS tiles fit (0: the seven-GEMM backward runs).  The chunks are as even as
+// the budget allows: ceil(pairs / chunks) with the fewest chunks that fit.
+int64_t bwd_chunk_pairs(int64_t pairs, size_t pair_bytes, size_t budget) {
+  if (pairs <= 0 || pair_bytes == 0 || budget < pair_bytes) return 0;
+  const int64_t fit = std::min<int64_t>(pairs, (int64_t)(budget / pair_bytes));
+  const int64_t chunks = (pairs + fit - 1) / fit;
+  return (pairs + chunks - 1) / chunks;
+}
+
+// Bytes sk_attn_bwd_workspace reports: the row statistics plus one chunk of
+// dS tiles under SK_BWD_DS_CAP_BYTES.
+size_t bwd_ws_bytes(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, bool causal) {
+  const size_t pair = sk::bwd_ds_pair_bytes(dtype, Hq, Hkv, Sq, Sk, D, causal);
+  const int64_t chunk = bwd_chunk_pairs((int64_t)B * Hkv, pair, (size_t)SK_BWD_DS_CAP_BYTES);
+  return bwd_rows_bytes(B, Hq, Sq) + (size_t)chunk * pair;
 }
 
 }  // namespace
@@ -267,11 +286,21 @@ int sk_attn_fwd_rope(int dtype, const void* q, const void* k, const void* v, voi
 int sk_attn_bwd_workspace(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
                           size_t* bytes) {
   g_err[0] = 0;
+  int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
+  if (rc) return rc;
+  if (!bytes) return fail(SK_EINVAL, "bytes pointer is NULL");
+  *bytes = bwd_ws_bytes(dtype, B, Hq, Hkv, Sq, Sk, D, is_causal != 0);
+  return SK_OK;
+}
+
+int sk_attn_bwd_workspace_min(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                              int is_causal, size_t* bytes) {
+  g_err[0] = 0;
   (void)is_causal;
   int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
   if (rc) return rc;
   if (!bytes) return fail(SK_EINVAL, "bytes pointer is NULL");
-  *bytes = bwd_ws_bytes(dtype, B, Hq, Sq, Sk, D);
+  *bytes = bwd_rows_bytes(B, Hq, Sq);
   return SK_OK;
 }
 
@@ -283,9 +312,10 @@ int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const
   int rc = check_dims(dtype, B, Hq, Hkv, Sq, Sk, D);
   if (rc) return rc;
   if ((int64_t)B * Hq * Sq == 0 && (int64_t)B * Hkv * Sk == 0) return SK_OK;
-  const size_t need = bwd_ws_bytes(dtype, B, Hq, Sq, Sk, D);
+  const size_t need = bwd_rows_bytes(B, Hq, Sq);
   if (need > 0 && (!workspace || workspace_bytes < need))
-    return fail(SK_EWORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+    return fail(SK_EWORKSPACE, "workspace of %zu bytes given, at least %zu needed",
+                workspace_bytes, need);
   if ((int64_t)B * Hq * Sq > 0 &&
       ((rc = check_ptr("dout", dout)) || (rc = check_ptr("q", q)) || (rc = check_ptr("o", o)) ||
        (rc = check_ptr("lse", lse)) || (rc = check_ptr("dq", dq))))
@@ -303,10 +333,19 @@ int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const
   p.delta = (float*)workspace;
   p.lse_log2 = (float*)((char*)workspace + rows_bytes);
   p.dq_acc = nullptr;
-  const size_t ds_bytes = sk::bwd_ds_bytes(dtype, B, Hq, Sq, Sk, D);
-  p.ds = ds_bytes > 0 ? (char*)workspace + 2 * rows_bytes : nullptr;
-  p.ds_nkb = (Sk + 31) / 32;
+  // The five-GEMM backward where its dS tiles for at least one (batch, KV
+  // head) pair fit the workspace past the row statistics (at most
+  // SK_BWD_DS_CAP_BYTES of it used); else the seven-GEMM backward.
+  const size_t pair_bytes = sk::bwd_ds_pair_bytes(dtype, Hq, Hkv, Sq, Sk, D, is_causal != 0);
+  const size_t ds_budget =
+      std::min<size_t>(workspace_bytes - std::min(workspace_bytes, need), (size_t)SK_BWD_DS_CAP_BYTES);
+  const int64_t chunk = bwd_chunk_pairs((int64_t)B * Hkv, pair_bytes, ds_budget);
+  p.ds = chunk > 0 ? (char*)workspace + need : nullptr;
+  p.n_pairs = (int)chunk;
+  p.bk0 = 0;
   p.ds_nqt = (Sq + 31) / 32;
+  p.ds_c = sk::ds_causal_c(Sq, Sk);
+  p.ds_head_tiles = sk::ds_head_tiles((Sk + 127) / 128, p.ds_nqt, p.ds_c, is_causal != 0);
   p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
@@ -761,7 +800,7 @@ int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, 
   const bool rope = (variant & SK_VARIANT_ROPE) != 0;
   const bool paged = (variant & SK_VARIANT_PAGED) != 0;
   sk::KernelPlan k;
-  int64_t splits = 1, kps = 0, paired = 0;
+  int64_t splits = 1, kps = 0, paired = 0, chunks = 1;
   size_t ws = 0;
   if (op == SK_OP_FWD || (decode && dtype == SK_F32)) {
     if (op == SK_OP_DECODE_COMBINE) {  // fp32 decode has no combine pass
@@ -780,9 +819,19 @@ int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, 
   } else if (op == SK_OP_BWD_DKV || op == SK_OP_BWD_DQ) {
     sk::BwdParams p{};
     p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sq = Sq, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
+    // The plan of one chunk at the workspace size sk_attn_bwd_workspace reports.
+    const int64_t pairs = (int64_t)B * Hkv;
+    const int64_t chunk = bwd_chunk_pairs(
+        pairs, sk::bwd_ds_pair_bytes(dtype, Hq, Hkv, Sq, Sk, D, is_causal != 0),
+        (size_t)SK_BWD_DS_CAP_BYTES);
+    if (chunk > 0) {
+      p.ds = const_cast<int*>(&kStandIn);
+      p.n_pairs = (int)chunk;
+      chunks = (pairs + chunk - 1) / chunk;
+    }
     k = op == SK_OP_BWD_DKV ? sk::plan_bwd_dkv(dtype, p, is_causal != 0)
                             : sk::plan_bwd_dq(dtype, p, is_causal != 0);
-    ws = bwd_ws_bytes(dtype, B, Hq, Sq, Sk, D);
+    ws = bwd_ws_bytes(dtype, B, Hq, Hkv, Sq, Sk, D, is_causal != 0);
   } else if (decode) {
     int ns = 0, per = 0;
     if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &ns, &per))) return rc;
@@ -812,6 +861,7 @@ int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, 
   cfg[SK_CFG_PAIRED] = paired;
   cfg[SK_CFG_WORKSPACE] = (int64_t)ws;
   cfg[SK_CFG_KEYS_PER_SPLIT] = kps;
+  cfg[SK_CFG_CHUNKS] = chunks;
   cfg[SK_CFG_LDS_BYTES] = cfg[SK_CFG_VGPRS] = cfg[SK_CFG_WG_PER_CU] = -1;
   if (kernel_name && name_len)
     snprintf(kernel_name, name_len, "%s<%s, D=%d, BM=%d, BN=%d, stages=%d, causal=%d, paged=%d, rope=%d>",

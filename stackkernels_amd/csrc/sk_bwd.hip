@@ -50,6 +50,7 @@
 // D = 256); 32-key K/V tiles stream through the ring; S^T = K Q^T and
 // dP^T = V dO^T give one query per lane, and dQ^T += K^T dS^T reads K^T
 // transposed from the ring.
+#include <algorithm>
 #include <mutex>
 
 #include "sk_common.h"
@@ -212,8 +213,9 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // the causal mask it sees the most queries), then head-dim half.
   const int w = xcd_work_index(blockIdx.x, gridDim.x);
   const int per_head = p.n_nblocks * kDSplit;
-  const int bk = w / per_head;
-  const int rem = w - bk * per_head;
+  const int bkl = w / per_head;  // pair within this launch
+  const int bk = p.bk0 + bkl;
+  const int rem = w - bkl * per_head;
   const int nblk = rem / kDSplit;
   const int dsp = rem - nblk * kDSplit;
   const int b = bk / p.Hkv;
@@ -383,13 +385,29 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // pieces of lanes r and r + 32 -- is formed by one lane-half swap per
   // dword and stored at byte 1024 (m % 2) + 16 (r + 32 (m / 2)) of the 2 KiB
   // tile, so each wave writes the tile with two contiguous 1 KiB stores.
-  // Key groups past S_k store nothing.
+  // Key groups past S_k store nothing; in the group that holds the last key,
+  // the rows of keys past S_k are stored as zeros (their P is not masked, and
+  // exp2(-lse * log2 e) * delta can overflow to inf, which the dQ kernel's
+  // zero K rows would turn into NaN).  Tile (query head, key tile, query
+  // tile) sits where the dS tile layout (DsLayout) puts it, counted from the
+  // launch's first pair.
   int ds_gi = 0, ds_m0 = m_begin;  // role 1's dS tile
-  auto store_ds = [&](const u32x4 (&g)[2]) SK_INLINE {
+  const int64_t ds_t0 =
+      (int64_t)bkl * p.group * p.ds_head_tiles + 4 * ds_off(nblk, p.ds_nqt, p.ds_c, CAUSAL) +
+      (int64_t)kg * ds_cnt(nblk, p.ds_nqt, p.ds_c, CAUSAL) - ds_qb(nblk, p.ds_c, CAUSAL);
+  auto store_ds = [&](const u32x4 (&gin)[2]) SK_INLINE {
     if constexpr (KB == 1 && SK_BWD_FIVE_GEMM) {
       if (p.ds != nullptr) {
         if (nw < p.Sk) {
-          const int64_t tile = ((bh0 + ds_gi) * p.ds_nkb + (nw >> 5)) * p.ds_nqt + (ds_m0 >> 5);
+          const int64_t tile = ds_t0 + (int64_t)ds_gi * p.ds_head_tiles + (ds_m0 >> 5);
+          u32x4 g[2] = {gin[0], gin[1]};
+          if (nw + 32 > p.Sk) {
+            const uint32_t keep = key < p.Sk ? ~0u : 0u;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) g[h][e] &= keep;
+          }
           // lane r < 32 gets chunks (r, 0), (r, 1); lane r + 32 chunks (r, 2), (r, 3)
           const auto a0 = __builtin_amdgcn_permlane32_swap(g[0][0], g[1][0], false, false);
           const auto a1 = __builtin_amdgcn_permlane32_swap(g[0][1], g[1][1], false, false);
@@ -1310,10 +1328,11 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
 // the K tile and dS^T transposed from the key-major dS tile with the same key
 // order in the MFMA's k-slots (keys 4 hl + {0..3} and 8 + 4 hl + {0..3} of
 // each 16-key step), so the lane of query l32 holds its 8 dS values of a
-// k-step as the B operand, and each K^T read feeds QW MFMAs.  The dK/dV kernel writes the dS tiles of every 128-key
-// block from the first query tile that can see the block; a wave reads a
-// tile only if its query tile lies in that range (else the DMA is empty and
-// the tile reads as zeros).  dS of keys past S_k is finite and meets K rows
+// k-step as the B operand, and each K^T read feeds QW MFMAs.  The dK/dV
+// kernel writes the dS tiles of every 128-key block from the first query
+// tile that can see the block (the dS tile layout); a wave reads a tile only
+// if its query tile lies in that range (else the DMA is empty and the tile
+// reads as zeros).  dS of keys past S_k is stored as zeros and meets K rows
 // that read as zeros.
 // dQ-from-dS tile: query tiles of 32 per wave, ring depth, workgroups per
 // CU.  Two query tiles per wave let each K^T operand read feed two MFMAs and
@@ -1354,10 +1373,12 @@ __global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5;
 
-  // Work item: (batch, query head) major, heaviest query block first.
+  // Work item: (batch, query head) major, heaviest query block first, over
+  // the query heads of the launch's (batch, KV head) pairs.
   const int w = xcd_work_index(blockIdx.x, gridDim.x);
-  const int bh = w / p.n_mblocks;
-  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
+  const int bhl = w / p.n_mblocks;  // query head within this launch
+  const int bh = p.bk0 * p.group + bhl;
+  const int mblk = p.n_mblocks - 1 - (w - bhl * p.n_mblocks);
   const int b = bh / p.Hq;
   const int hkv = (bh - b * p.Hq) / p.group;
   const int m0 = mblk * BM;
@@ -1373,21 +1394,17 @@ __global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
     const int c = (lane % L::kCpr) ^ swz_rt<DP>(r);
     goff[j] = c * 8 < p.D ? (uint32_t)((r * p.D + c * 8) * 2) : kBufferOob;
   }
-  // This wave's dS tiles: query tile qt (mw / 32 + q), key tile t at
-  // tile (bh * ds_nkb + t) * ds_nqt + qt.  Key tiles [0, kt_lim[q]) were
-  // written for query tile qt.
-  const uint8_t* ds_row[QW];
-  int kt_lim[QW];
-#pragma unroll
-  for (int q = 0; q < QW; ++q) {
-    const int r0 = mw + 32 * q;
-    ds_row[q] = (const uint8_t*)p.ds + ((int64_t)bh * p.ds_nkb * p.ds_nqt + (r0 >> 5)) * kDs;
-    kt_lim[q] = r0 < p.Sq ? p.ds_nkb : 0;
-    if (CAUSAL && r0 < p.Sq) {
-      const int last = r0 + 31 + diag;  // last key a row of the tile can see
-      kt_lim[q] = last < 0 ? 0 : min(p.ds_nkb, (last / 128 + 1) * 4);
-    }
-  }
+  // This wave's dS tiles: query tile qt = mw / 32 + q; key tile t = 4 kb + j
+  // of it at tile 4 off(kb) + j cnt(kb) + qt - qb(kb) of the head (the dS
+  // tile layout), written iff qt >= qb(kb), i.e. iff a row of the query tile
+  // sees key 128 kb.  The key block's terms are scalars, recomputed by
+  // issue_tile when t enters a new key block (it is called for t = 0, 1, 2,
+  // ... in order).
+  const uint8_t* ds_head = (const uint8_t*)p.ds + (int64_t)bhl * p.ds_head_tiles * kDs;
+  const int qt0 = mw >> 5;
+  const int q_rows = mw < p.Sq ? min(QW, (p.Sq - mw + 31) >> 5) : 0;  // query tiles in range
+  int cur_kb = -1, cur_cnt = 0, cur_qb = 0;
+  int64_t cur_off = 0;
   // The dS tile lands in LDS key-major (row r, queries 8 m .. 8 m + 7 at byte
   // 64 r + 16 m); DMA h, lane i fills chunk c = 64 h + i, i.e. (r, m) =
   // (c / 4, c % 4), stored by the dK/dV kernel at 1024 (m % 2) + 16 (r + 32
@@ -1406,10 +1423,18 @@ __global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
     const uint32_t st = lds0 + (t % STAGES) * kStageBytes;
 #pragma unroll
     for (int j = 0; j < LK; ++j) buffer_load_lds_b128(kr, st + (wave + j * NW) * 1024, goff[j]);
+    if ((t >> 2) != cur_kb) {
+      cur_kb = t >> 2;
+      cur_off = 4 * ds_off(cur_kb, p.ds_nqt, p.ds_c, CAUSAL);
+      cur_cnt = ds_cnt(cur_kb, p.ds_nqt, p.ds_c, CAUSAL);
+      cur_qb = ds_qb(cur_kb, p.ds_c, CAUSAL);
+    }
 #pragma unroll
     for (int q = 0; q < QW; ++q) {
-      const i32x4 dr =
-          make_rsrc_words(ds_row[q] + (int64_t)t * p.ds_nqt * kDs, t < kt_lim[q] ? kDs : 0);
+      const int rel = qt0 + q - cur_qb;
+      const bool ok = q < q_rows && rel >= 0;
+      const int64_t tile = ok ? cur_off + (int64_t)(t & 3) * cur_cnt + rel : 0;
+      const i32x4 dr = make_rsrc_words(ds_head + tile * kDs, ok ? kDs : 0);
       const uint32_t sd = st + L::kTileBytes + (wave * QW + q) * kDs;
       if constexpr (SK_BWD_DS_NT & 2) {
         buffer_load_lds_b128_nt(dr, sd, ds_goff[0]);
@@ -1521,6 +1546,12 @@ struct DqConfig<256> {
   static constexpr int kMode = 0;
 };
 
+// (Batch, KV head) pairs a dK/dV or dQ-from-dS launch covers: a chunk of the
+// five-GEMM backward, else all of them.
+static int64_t launch_pairs(const BwdParams& p) {
+  return p.n_pairs > 0 ? p.n_pairs : (int64_t)p.B * p.Hkv;
+}
+
 template <class T, int DP, int DO>
 static KernelPlan plan_dkv_t(BwdParams& p, bool causal) {
   // D = 128: the 6-deep pipelined schedule (S one step ahead of P; 3%-7%
@@ -1534,7 +1565,7 @@ static KernelPlan plan_dkv_t(BwdParams& p, bool causal) {
   KernelPlan k;
   k.fn = causal ? (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, KB, true>
                 : (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, KB, false>;
-  k.grid = dim3((unsigned)((int64_t)p.n_nblocks * p.B * p.Hkv * (DP / DO)));
+  k.grid = dim3((unsigned)((int64_t)p.n_nblocks * launch_pairs(p) * (DP / DO)));
   k.block = dim3(512 / KB);
   k.kernel = "bwd_dkv_kernel";
   k.elem = T::code;
@@ -1592,33 +1623,35 @@ KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal) {
 
 // The five-GEMM backward (dS tiles in the workspace) runs where the dK/dV
 // kernel's pipelined schedule stores them: 16-bit inputs, padded head dim
-// 128, 32 keys per wave.  Its tiles take B * H_q * S_q * S_k * 2 bytes
-// (rounded up to 32 x 32 tiles); above kBwdDsMaxBytes the seven-GEMM
-// backward runs instead.  It gives the seven-GEMM results bit for bit (the
-// same dS values, summed into dQ in the same key order): the dS stores cost
+// 128, 32 keys per wave.  Its tiles take 2 KiB per 32 x 32 (key, query)
+// tile that a visible key block writes (the dS tile layout: about
+// B * H_q * S_q * S_k bytes under a square causal mask, twice that without
+// it); the caller's workspace sets how many (batch, KV head) pairs' tiles
+// one dK/dV + dQ launch pair holds, and the pairs run in chunks of that size.
+// It gives the seven-GEMM results bit for bit (the same dS values, summed
+// into dQ in the same key order), whatever the chunking: the dS stores cost
 // the dK/dV kernel about 8%, and the dQ pass, which no longer recomputes S
 // and dP, runs after it instead of beside it.  C3 backward 4.7% faster, MHA
 // S = 4096 1.8% faster (one box, alternating libraries).
-constexpr size_t kBwdDsMaxBytes = size_t(4) << 30;
-
-size_t bwd_ds_bytes(int dtype, int B, int Hq, int Sq, int Sk, int D) {
+size_t bwd_ds_pair_bytes(int dtype, int Hq, int Hkv, int Sq, int Sk, int D, bool causal) {
   if (!SK_BWD_FIVE_GEMM) return 0;
   if (dtype != BF16::code && dtype != F16::code) return 0;
   if (D <= 64 || D > 128 || SK_BWD_DKV_STAGES != 6 || SK_BWD_DKV_KB != 1) return 0;
-  const size_t bytes = (size_t)B * Hq * ((Sk + 31) / 32) * ((Sq + 31) / 32) * 2048;
-  return bytes <= kBwdDsMaxBytes ? bytes : 0;
+  if (Hkv <= 0 || Sq <= 0 || Sk <= 0) return 0;
+  const int nqt = (Sq + 31) / 32;
+  const int c = ds_causal_c(Sq, Sk);
+  const int64_t tiles = ds_head_tiles((Sk + 127) / 128, nqt, c, causal);
+  return (size_t)(Hq / Hkv) * (size_t)tiles * 2048;
 }
 
 template <class T>
 static KernelPlan plan_dq_ds_t(BwdParams& p, bool causal) {
   constexpr int NW = 4, QW = kDqDs.qw;
   p.n_mblocks = (p.Sq + 32 * QW * NW - 1) / (32 * QW * NW);
-  p.ds_nkb = (p.Sk + 31) / 32;
-  p.ds_nqt = (p.Sq + 31) / 32;
   KernelPlan k;
   k.fn = causal ? (const void*)bwd_dq_ds_kernel<T, 128, QW, kDqDs.stages, kDqDs.occ, true>
                 : (const void*)bwd_dq_ds_kernel<T, 128, QW, kDqDs.stages, kDqDs.occ, false>;
-  k.grid = dim3((unsigned)((int64_t)p.n_mblocks * p.B * p.Hq));
+  k.grid = dim3((unsigned)((int64_t)p.n_mblocks * launch_pairs(p) * p.group));
   k.block = dim3(NW * 64);
   k.kernel = "bwd_dq_ds_kernel";
   k.elem = T::code;
@@ -1631,7 +1664,8 @@ static KernelPlan plan_dq_ds_t(BwdParams& p, bool causal) {
 }
 
 KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal) {
-  if (bwd_ds_bytes(dtype, p.B, p.Hq, p.Sq, p.Sk, p.D) > 0)
+  if (p.ds != nullptr &&
+      bwd_ds_pair_bytes(dtype, p.Hq, p.Hkv, p.Sq, p.Sk, p.D, causal) > 0)
     return dtype == BF16::code ? plan_dq_ds_t<BF16>(p, causal) : plan_dq_ds_t<F16>(p, causal);
   if (dtype == BF16::code) return plan_dq_dt<BF16>(p, causal);
   if (dtype == F16::code) return plan_dq_dt<F16>(p, causal);
@@ -1704,23 +1738,41 @@ static const SideEntry* side_entry(hipStream_t s) {
 // work.  Once dQ is queued on the side stream, the caller's stream always
 // waits for it, also when the dK/dV launch fails, so nothing queued after the
 // call can reuse its buffers early and a capture stays joined.
+//
+// Five-GEMM backward (p.ds set, p.n_pairs the pairs per chunk): for each
+// chunk of (batch, KV head) pairs in turn, the dK/dV kernel writes the
+// chunk's dS tiles and the dQ kernel reads them, both on the caller's stream.
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s) {
   if (dtype != BF16::code && dtype != F16::code) return hipErrorInvalidValue;
+  const int64_t pairs = (int64_t)p.B * p.Hkv;
+  if (p.ds != nullptr) {
+    if (bwd_ds_pair_bytes(dtype, p.Hq, p.Hkv, p.Sq, p.Sk, p.D, causal) == 0 || p.n_pairs <= 0)
+      return hipErrorInvalidValue;
+    if ((int64_t)((p.Sk + 127) / 128) * p.n_pairs > 0x7fffffffLL ||
+        (int64_t)((p.Sq + 255) / 256) * p.n_pairs * p.group > 0x7fffffffLL)
+      return hipErrorInvalidConfiguration;
+    for (int64_t c0 = 0; c0 < pairs; c0 += p.n_pairs) {
+      BwdParams q = p;
+      q.bk0 = (int)c0;
+      q.n_pairs = (int)std::min<int64_t>(p.n_pairs, pairs - c0);
+      const KernelPlan kv = plan_bwd_dkv(dtype, q, causal);
+      const KernelPlan dq = plan_bwd_dq(dtype, q, causal);
+      if (!kv.fn || !dq.fn) return hipErrorInvalidValue;
+      hipError_t e = run_plan(kv, &q, s);
+      if (e != hipSuccess) return e;
+      if ((e = run_plan(dq, &q, s)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   BwdParams q = p;
+  q.bk0 = 0;
+  q.n_pairs = (int)pairs;
   const KernelPlan kv = plan_bwd_dkv(dtype, q, causal);
   const KernelPlan dq = plan_bwd_dq(dtype, q, causal);
   if (!kv.fn || !dq.fn) return hipErrorInvalidValue;
   const int64_t g_kv = (int64_t)q.n_nblocks * p.B * p.Hkv * (kv.head_dim == 256 ? 2 : 1);
   const int64_t g_q = (int64_t)q.n_mblocks * p.B * p.Hq;
   if (g_kv > 0x7fffffffLL || g_q > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  if (bwd_ds_bytes(dtype, p.B, p.Hq, p.Sq, p.Sk, p.D) > 0) {
-    // Five-GEMM backward: dQ reads the dS tiles dK/dV writes, on one stream.
-    if (p.ds == nullptr) return hipErrorInvalidValue;
-    hipError_t e = run_plan(kv, &q, s);
-    if (e != hipSuccess) return e;
-    return run_plan(dq, &q, s);
-  }
-  q.ds = nullptr;
   const SideEntry* se = g_kv > 256 && g_q > 0 ? side_entry(s) : nullptr;
   if (!se) {
     hipError_t e = run_plan(kv, &q, s);

@@ -115,11 +115,18 @@ struct BwdParams {
   float* delta;     // [B*Hq*Sq] fp32 scratch: rowsum(dO * O)
   float* lse_log2;  // [B*Hq*Sq] fp32 scratch: lse * log2(e) (+inf for empty rows)
   float* dq_acc;    // [B*Hq*Sq*D] fp32 scratch (dQ accumulator) or null
-  // dS tiles [B*Hq][ds_nkb][ds_nqt] of 32 keys x 32 queries (16-bit, key-major
-  // rows of 64 bytes), written by the dK/dV kernel and read by the dQ kernel
-  // of the five-GEMM backward; null for the seven-GEMM backward.
+  // dS tiles of 32 keys x 32 queries (16-bit, key-major rows of 64 bytes) of
+  // the launch's (batch, KV head) pairs, in the DsLayout order below, written
+  // by the dK/dV kernel and read by the dQ kernel of the five-GEMM backward;
+  // null for the seven-GEMM backward.
   void* ds;
-  int ds_nkb, ds_nqt;
+  int ds_nqt;             // query tiles per head: ceil(Sq / 32)
+  int ds_c;               // causal: ceil((Sk - Sq) / 32); else unused
+  int64_t ds_head_tiles;  // tiles per query head
+  // First (batch, KV head) pair, b * Hkv + h_kv, of this launch and the pair
+  // count: the five-GEMM backward runs the pairs in chunks whose dS tiles
+  // fit the workspace; every other launch covers all B * Hkv pairs.
+  int bk0, n_pairs;
   int B, Hq, Hkv, Sq, Sk, D, group;
   float scale, scale_log2;  // signed sm_scale and sm_scale * log2(e)
   // MFMA kernels: the score exponent uses |sm_scale| * log2(e) (never 0, so a
@@ -129,6 +136,45 @@ struct BwdParams {
   uint32_t op_sign;
   int n_mblocks, n_nblocks;
 };
+
+// dS tile layout of the five-GEMM backward, per query head.  The dK/dV
+// workgroup of key block kb (keys 128 kb .. 128 kb + 127) walks the query
+// tiles [qb(kb), nqt): under the bottom-right causal mask the first tile
+// whose last row sees key 128 kb, qb(kb) = max(0, 4 kb - c) with
+// c = ceil((Sk - Sq) / 32); without the mask 0.  Block kb holds
+// cnt(kb) = max(0, nqt - qb(kb)) tiles for each of its four 32-key tiles,
+// key tile kt = 4 kb + j at tile 4 off(kb) + j cnt(kb) + (qt - qb(kb)) of the
+// head, off(kb) = cnt(0) + ... + cnt(kb - 1): only the tiles some visible
+// key block writes are allocated (about half of the rectangle for a square
+// causal shape).
+__host__ __device__ inline int ds_causal_c(int Sq, int Sk) {
+  const int d = Sk - Sq;
+  return d >= 0 ? (d + 31) / 32 : -((-d) / 32);  // ceil(d / 32)
+}
+__host__ __device__ inline int ds_qb(int kb, int c, bool causal) {
+  return causal ? (4 * kb - c > 0 ? 4 * kb - c : 0) : 0;
+}
+__host__ __device__ inline int ds_cnt(int kb, int nqt, int c, bool causal) {
+  const int r = nqt - ds_qb(kb, c, causal);
+  return r > 0 ? r : 0;
+}
+// off(kb) in closed form: cnt(k) = nqt while 4 k <= c, nqt + c - 4 k while
+// c < 4 k < nqt + c, then 0.
+__host__ __device__ inline int64_t ds_off(int kb, int nqt, int c, bool causal) {
+  if (!causal) return (int64_t)kb * nqt;
+  const int64_t a = (int64_t)nqt + c;
+  const int64_t full = c >= 0 ? c / 4 + 1 : 0;   // k with 4 k <= c
+  const int64_t live = a > 0 ? (a + 3) / 4 : 0;  // k with 4 k < nqt + c
+  const int64_t k1 = kb < full ? kb : full;
+  int64_t s = k1 * nqt;
+  const int64_t hi = kb < live ? kb : live;
+  if (hi > full) s += (hi - full) * a - 2 * (hi - full) * (hi + full - 1);
+  return s;
+}
+// Tiles per query head for nkb key blocks.
+__host__ __device__ inline int64_t ds_head_tiles(int nkb, int nqt, int c, bool causal) {
+  return 4 * ds_off(nkb, nqt, c, causal);
+}
 
 // KV-cache append: k_cache[b, h, slots[b*T + t], :] = k[b, h, t, :], same for v.
 // Strides are element strides (b, h, s); the head dim is contiguous.
@@ -183,10 +229,10 @@ KernelPlan plan_decode_combine(int dtype, const DecParams& p);
 // The backward plans fill the block counts of p they derive.
 KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal);
 KernelPlan plan_bwd_dq(int dtype, BwdParams& p, bool causal);
-// Bytes of dS tiles the five-GEMM backward needs for this shape, or 0 when it
-// runs the seven-GEMM backward (head dims other than 65-128, fp32, or more
-// than kBwdDsMaxBytes of tiles).
-size_t bwd_ds_bytes(int dtype, int B, int Hq, int Sq, int Sk, int D);
+// Bytes of dS tiles the five-GEMM backward needs per (batch, KV head) pair
+// (its query heads' tiles), or 0 where the seven-GEMM backward runs (head
+// dims other than 65-128, fp32).
+size_t bwd_ds_pair_bytes(int dtype, int Hq, int Hkv, int Sq, int Sk, int D, bool causal);
 KernelPlan plan_bwd_dkv_f32(BwdParams& p, bool causal);
 KernelPlan plan_bwd_dq_f32(BwdParams& p, bool causal);
 

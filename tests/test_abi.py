@@ -30,7 +30,8 @@ def header_functions():
 def test_header_declares_expected_api():
     names = set(header_functions())
     assert {"sk_abi_version", "sk_last_error", "sk_attn_fwd", "sk_attn_bwd",
-            "sk_attn_bwd_workspace", "sk_decode_plan", "sk_decode", "sk_decode_workspace",
+            "sk_attn_bwd_workspace", "sk_attn_bwd_workspace_min", "sk_decode_plan", "sk_decode",
+            "sk_decode_workspace",
             "sk_decode_varlen", "sk_kv_cache_update", "sk_decode_paged",
             "sk_kv_cache_update_paged", "sk_attn_fwd_rope", "sk_decode_rope",
             "sk_decode_paged_rope", "sk_kv_cache_update_rope",
@@ -108,18 +109,57 @@ def test_decode_argument_errors(lib):
     assert rc == _lib.SK_EINVAL
 
 
+def _ds_pair_bytes(hq, hkv, sq, sk, causal):
+    """dS bytes per (batch, KV head) pair, from the mask: key block kb (keys
+    128 kb ..) writes a 2 KiB tile for each of its four 32-key tiles and every
+    query tile from the first one holding a row that sees key 128 kb."""
+    nqt = -(-sq // 32)
+    tiles = 0
+    for kb in range(-(-sk // 128)):
+        first = 0
+        if causal:  # first query row i with 128 kb <= i + (sk - sq)
+            first = max(0, 128 * kb - (sk - sq))
+        if first < sq:
+            tiles += 4 * (nqt - first // 32)
+    return (hq // hkv) * tiles * 2048
+
+
 def test_bwd_workspace(lib):
-    nb = ctypes.c_size_t()
+    nb, nmin = ctypes.c_size_t(), ctypes.c_size_t()
     rows = 2 * 2 * 32 * 2048 * 4  # delta and lse * log2(e), fp32 per query row
-    # C3 (bf16, D = 128): plus the five-GEMM backward's dS tiles, 32 x 32 x 2 bytes each
+    # C3 (bf16, D = 128): plus the five-GEMM backward's dS tiles, only those a
+    # visible key block writes (0.875 of the rectangle here), all 16 pairs in one chunk
     assert lib.sk_attn_bwd_workspace(2, 2, 32, 8, 2048, 8192, 128, 1, ctypes.byref(nb)) == 0
+    pair = _ds_pair_bytes(32, 8, 2048, 8192, True)
+    assert pair == 4 * 4 * sum(64 - max(0, 4 * kb - 192) for kb in range(64)) * 2048
+    assert nb.value == rows + 16 * pair and 16 * pair < 0.9 * 2 * 32 * 256 * 64 * 2048
+    assert lib.sk_attn_bwd_workspace_min(2, 2, 32, 8, 2048, 8192, 128, 1, ctypes.byref(nmin)) == 0
+    assert nmin.value == rows
+    # without the mask: the whole rectangle
+    assert lib.sk_attn_bwd_workspace(2, 2, 32, 8, 2048, 8192, 128, 0, ctypes.byref(nb)) == 0
     assert nb.value == rows + 2 * 32 * (8192 // 32) * (2048 // 32) * 2048
-    # ragged lengths round up to whole tiles
+    # square causal: about half of it
+    assert lib.sk_attn_bwd_workspace(2, 1, 4, 4, 4096, 4096, 128, 1, ctypes.byref(nb)) == 0
+    assert nb.value == 2 * 4 * 4096 * 4 + 4 * _ds_pair_bytes(4, 4, 4096, 4096, True)
+    # ragged lengths round up to whole tiles; S_q > S_k and S_q < S_k under the mask
     assert lib.sk_attn_bwd_workspace(1, 1, 2, 1, 33, 65, 96, 0, ctypes.byref(nb)) == 0
-    assert nb.value == 2 * 512 + 2 * 3 * 2 * 2048  # 66 fp32 rows -> 264 bytes -> 512 (256-aligned)
-    # the seven-GEMM backward (no dS tiles): D = 64, D = 256, fp32, and beyond 4 GiB of tiles
+    assert nb.value == 2 * 512 + 2 * 4 * 2 * 2048  # 66 fp32 rows -> 264 bytes -> 512 (256-aligned)
+    for sq, sk in ((33, 65), (200, 70), (1000, 300), (70, 1000), (2048, 2048 + 40), (129, 4000)):
+        for causal in (0, 1):
+            assert lib.sk_attn_bwd_workspace(2, 3, 4, 2, sq, sk, 128, causal, ctypes.byref(nb)) == 0
+            row_b = 2 * (-(-3 * 4 * sq * 4 // 256) * 256)
+            assert nb.value == row_b + 6 * _ds_pair_bytes(4, 2, sq, sk, causal), (sq, sk, causal)
+    # above the 2 GiB cap: the fewest even chunks (B = 4, H = 32, S = 8192 causal: 68 MB
+    # per pair, 31 fit, so 5 chunks of 26 pairs)
+    pair = _ds_pair_bytes(32, 32, 8192, 8192, True)
+    assert (2 << 30) // pair == 31
+    assert lib.sk_attn_bwd_workspace(2, 4, 32, 32, 8192, 8192, 128, 1, ctypes.byref(nb)) == 0
+    assert nb.value == 4 * 32 * 8192 * 4 * 2 + 26 * pair
+    assert nb.value - 4 * 32 * 8192 * 8 <= 2 << 30
+    # the seven-GEMM backward (no dS tiles): D = 64, D = 256, fp32, and one pair's tiles
+    # beyond the cap (S = 65536 causal, 4 query heads per KV head)
     for dtype, d, sq, sk in ((2, 64, 2048, 8192), (2, 256, 2048, 8192), (0, 128, 2048, 8192),
-                             (2, 128, 16384, 16384)):
+                             (2, 128, 65536, 65536)):
         assert lib.sk_attn_bwd_workspace(dtype, 2, 32, 8, sq, sk, d, 1, ctypes.byref(nb)) == 0
         assert nb.value == 2 * 2 * 32 * sq * 4, (dtype, d)
 

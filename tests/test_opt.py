@@ -173,7 +173,15 @@ def test_pick_forward_and_backward():
     # dQ from the stored dS: 4 waves x 64 queries, 32-key tiles, 3-deep ring
     assert (b["dq"]["num_stages"], b["dq"]["num_warps"], b["dq"]["BLOCK_N"],
             b["dq"]["BLOCK_M"]) == (3, 4, 32, 256)
-    assert b["workspace_bytes"] == 2 * 2 * 32 * 2048 * 4 + 2 * 32 * 256 * 64 * 2048
+    # row statistics + the dS tiles visible key blocks write (0.875 of the rectangle), one chunk
+    assert b["workspace_bytes"] == 2 * 2 * 32 * 2048 * 4 + 2 * 32 * 4 * 2048 * sum(
+        64 - max(0, 4 * kb - 192) for kb in range(64))
+    assert b["chunks"] == 1
+    # B = 4, H = 32, S = 8192 causal: the same five-GEMM kernels, in 5 chunks under the cap
+    big = pick("flash_bwd", (4, 32, 8192, 128), dtype="bfloat16", is_causal=True)
+    assert big["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_ds_kernel" and big["chunks"] == 5
+    assert big["grid"] == (8192 // 128) * 26 and big["dq"]["grid"] == (8192 // 256) * 26
+    assert big["workspace_bytes"] <= 4 * 32 * 8192 * 8 + (2 << 30)
     for d in (64, 256):
         o = pick("flash_bwd", (2, 8, 512, d), dtype="bfloat16", kv_len=1024, num_kv_heads=2)
         assert (o["dq"]["num_stages"], o["dq"]["num_warps"]) == (4, 4)
