@@ -62,6 +62,23 @@ def _bwd(do, q, k, v, o, lse, causal, ws_bytes):
     return dq, dk, dv
 
 
+def _check_bound(q, k, v, do, causal, grads):
+    """Gradients against the float64 oracle, elementwise within the repo's PyTorch
+    reference path's own error plus the rounding allowance of the kernels' 16-bit
+    operands (``tests/_bwd_bound.py``): the group sums of dK/dV here reach 5-10, where
+    one bf16 step is 0.03-0.06, so an absolute 2e-2 is not a bound for them."""
+    from oracle import attention_oracle as orc
+
+    exact = orc.attention_backward(np64(q), np64(k), np64(v), np64(do), causal)
+    dt = "bf16" if q.dtype == torch.bfloat16 else "f16"
+    mass = rounding_mass(np64(q), np64(k), np64(v), np64(do), causal, None, dt)
+    qr, kr, vr = (t.detach().cpu().requires_grad_(True) for t in (q, k, v))
+    ref, _ = attention_reference(qr, kr, vr, is_causal=causal)
+    ref.backward(do.cpu())
+    for i, (name, path) in enumerate((("dQ", qr.grad), ("dK", kr.grad), ("dV", vr.grad))):
+        check_backward(np64(grads[i]), np64(path), exact[i], mass[i], dt, name)
+
+
 SHAPES = [
     # b, hq, hkv, sq, sk, causal
     (2, 4, 2, 200, 333, True),    # S_k - S_q = 133: not a multiple of 32
@@ -98,11 +115,7 @@ def test_chunkings_bit_identical(device, dtype, shape, d):
     for name, r in runs.items():
         for x, y, what in zip(full, r, ("dQ", "dK", "dV")):
             assert torch.equal(x, y), f"{what} of the {name} workspace differs"
-    from oracle import attention_oracle as orc
-
-    exact = orc.attention_backward(np64(q), np64(k), np64(v), np64(do), causal)
-    for x, e, what in zip(full, exact, ("dQ", "dK", "dV")):
-        assert_close_maxabs(x, e, TOL[dtype], what)
+    _check_bound(q, k, v, do, causal, full)
 
 
 def test_workspace_below_minimum_is_rejected(device):
@@ -128,7 +141,8 @@ def test_keys_past_sk_with_very_negative_lse(device, dtype, amp):
     do = (8.0 * torch.randn(b, hq, sq, d, generator=g)).to(dtype)
     q, k, v, do = (t.to(device) for t in (q, k, v, do))
     o, lse = flash_attn_fwd(q, k, v)
-    assert float(lse.max()) < (-11.0 if dtype == torch.float16 else -88.0)
+    # fp16: exp(15) = 3.3e6 > 65504; bf16: exp(88) > 2^127
+    assert float(lse.max()) < (-15.0 if dtype == torch.float16 else -88.0)
     pref, mn, pair = _sizes(dtype, b, hq, hkv, sq, sk, d, False)
     five = _bwd(do, q, k, v, o, lse, False, pref)
     seven = _bwd(do, q, k, v, o, lse, False, mn)
@@ -136,16 +150,7 @@ def test_keys_past_sk_with_very_negative_lse(device, dtype, amp):
     for x, y, what in zip(five, seven, ("dQ", "dK", "dV")):
         assert torch.isfinite(x).all(), f"{what}: non-finite values"
         assert torch.equal(x, y), what
-    from oracle import attention_oracle as orc
-
-    exact = orc.attention_backward(np64(q), np64(k), np64(v), np64(do), False)
-    dt = "bf16" if dtype == torch.bfloat16 else "f16"
-    mass = rounding_mass(np64(q), np64(k), np64(v), np64(do), False, None, dt)
-    qr, kr, vr = (t.detach().cpu().requires_grad_(True) for t in (q, k, v))
-    ref, _ = attention_reference(qr, kr, vr, is_causal=False)
-    ref.backward(do.cpu())
-    for i, (name, path) in enumerate((("dQ", qr.grad), ("dK", kr.grad), ("dV", vr.grad))):
-        check_backward(np64(five[i]), np64(path), exact[i], mass[i], dt, name)
+    _check_bound(q, k, v, do, False, five)
 
 
 def test_many_chunks_full_size(device):
