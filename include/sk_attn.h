@@ -303,8 +303,10 @@ SK_API int sk_kv_cache_update_paged(int dtype, const void* k, const void* v, voi
  * (src/stackkernels/_core/positional/rope.py:12-222) before attention.
  */
 
-/* sk_attn_fwd with q rotated on load (query row i is token i).  Forward only:
- * sk_attn_bwd takes the rotated q, which this call does not write out. */
+/* sk_attn_fwd with q rotated on load (query row i is token i).  It does not
+ * write the rotated q out: its backward is sk_rope_rotate(q) into a buffer,
+ * sk_attn_bwd on that rotated q, then sk_rope_rotate(dq, inverse = 1) in
+ * place. */
 SK_API int sk_attn_fwd_rope(int dtype, const void* q, const void* k, const void* v, void* o,
                      float* lse, int B, int Hq, int Hkv, int Sq, int Sk, int D,
                      const int64_t* q_strides, const int64_t* k_strides,
@@ -312,6 +314,24 @@ SK_API int sk_attn_fwd_rope(int dtype, const void* q, const void* k, const void*
                      const void* rope_cos, const void* rope_sin, int rope_dtype, int rope_rows,
                      int64_t rope_stride, const int32_t* rope_pos, int rope_start,
                      float sm_scale, void* stream);
+
+/*
+ * Rotate a (B, H, S, D) tensor by its RoPE angles (inverse = 0) or by their
+ * negatives (inverse = 1, the adjoint: the gradient of the rotation), token t
+ * of batch row b at the position given above (positions as in the other
+ * *_rope calls, tokens = S).  Element strides {b, h, s} for x and out; out
+ * may be x (in place), otherwise it must not overlap it.  The rotation is
+ * the one the fused kernels apply, bit for bit, so it rebuilds the rotated q
+ * that sk_attn_fwd_rope used and carries dq back through the rotation for
+ * sk_attn_bwd.  Replaces rope_fwd / _rope_fwd_kernel and rope_bwd /
+ * _rope_bwd_kernel (reference: src/stackkernels/_core/positional/rope.py:12-222;
+ * the adjoint as in src/stackkernels/torch/embedding.py:46-66).
+ */
+SK_API int sk_rope_rotate(int dtype, const void* x, void* out, int B, int H, int S, int D,
+                   const int64_t* x_strides, const int64_t* out_strides,
+                   const void* rope_cos, const void* rope_sin, int rope_dtype, int rope_rows,
+                   int64_t rope_stride, const int32_t* rope_pos, int rope_start, int inverse,
+                   void* stream);
 
 /* sk_decode (cache_seqlens NULL) or sk_decode_varlen with q rotated on load. */
 SK_API int sk_decode_rope(int dtype, const void* q, const void* k, const void* v, void* o,

@@ -42,6 +42,13 @@ What it restates (all arithmetic in float64 unless a caller asks otherwise):
                               to the tensor type), with one position per (row,
                               token); the fused paths are these composed with
                               ``attention_forward`` / ``decode*`` / ``kv_cache_update*``.
+* ``rope_rotate_adjoint``  -- the gradient of ``rope_rotate`` (its transpose per
+                              (d, d + D/2) plane); for ``precompute_freqs`` tables the
+                              reference's rotation by -theta,
+                              ``src/stackkernels/torch/embedding.py:46-66`` and
+                              ``_core/positional/rope.py:77-134``.  The fused-RoPE
+                              backward is ``attention_backward`` at the rotated q
+                              followed by it on dQ.
 
 How each function is pinned (see ``tests/test_oracle.py``):
 
@@ -75,7 +82,11 @@ How each function is pinned (see ``tests/test_oracle.py``):
   torch's own bfloat16 / float16 casts, ties included.  The reference's RoPE
   tests (``tests/ops/test_rope.py``) hold no fixed vectors: they compare its
   kernel with its torch restatement at start_pos 0, 15, 23, 31, 64, and the
-  same start positions are used here.
+  same start positions are used here.  ``rope_rotate_adjoint`` against the
+  definition of a transpose, <R x, y> = <x, R^T y>, with tables whose halves
+  differ (a sine from the wrong half or a wrong sign breaks it), against
+  R^T R = I for real tables, and bit for bit against the reference's formula
+  ``dy * cos - rotate_half(dy) * sin`` evaluated by torch.
 """
 
 from __future__ import annotations
@@ -396,6 +407,34 @@ def rope_rotate(x, cos, sin, positions) -> np.ndarray:
     rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
     out = (x * cc) + (rot * ss)
     return np.where(ok[:, None, :, None], out, x).astype(np.float32)
+
+
+def rope_rotate_adjoint(y, cos, sin, positions, dtype=np.float32) -> np.ndarray:
+    """Adjoint (transpose) of ``rope_rotate``: the gradient with respect to its
+    input.  Per plane (column d < D/2 and d + D/2) the rotation is
+    y_lo = x_lo c_lo - x_hi s_lo, y_hi = x_hi c_hi + x_lo s_hi, so
+    x_lo = y_lo c_lo + y_hi s_hi, x_hi = y_hi c_hi - y_lo s_lo.  With tables
+    whose halves are equal (``precompute_freqs``) this is the reference's
+    rotation by -theta, ``dx = dy * cos - rotate_half(dy) * sin``
+    (``src/stackkernels/torch/embedding.py:46-66``; Triton
+    ``_rope_bwd_kernel``, ``src/stackkernels/_core/positional/rope.py:77-134``).
+    In ``dtype`` arithmetic (float32: each product and the sum rounded, as
+    ``rope_rotate``; float64 for checks); positions outside the table leave
+    the token as it is."""
+    y = np.asarray(y, dtype=dtype)
+    c = np.asarray(cos, dtype=dtype)
+    s = np.asarray(sin, dtype=dtype)
+    pos = np.asarray(positions, dtype=np.int64)
+    d = y.shape[-1]
+    half = d // 2
+    ok = (pos >= 0) & (pos < c.shape[0])
+    idx = np.where(ok, pos, 0)
+    cc = c[idx][:, None, :, :d]  # (B, 1, S, D)
+    ss = s[idx][:, None, :, :d]
+    lo = y[..., :half] * cc[..., :half] + y[..., half:] * ss[..., half:]
+    hi = y[..., half:] * cc[..., half:] - y[..., :half] * ss[..., :half]
+    out = np.concatenate([lo, hi], axis=-1)
+    return np.where(ok[:, None, :, None], out, y).astype(dtype)
 
 
 def attention_forward_loops(q, k, v, is_causal=False, sm_scale=None):

@@ -68,6 +68,8 @@ SIGNATURES: dict[str, tuple] = {
     "sk_kv_cache_update_paged": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,
                                           _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                           _i64p, _i64p, _i64p, _i64p, _vp]),
+    "sk_rope_rotate": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _i64p, _i64p,
+                                *_ROPE, _c_int, _vp]),
     # *_rope: the call they extend with (cos, sin, table dtype, rows, row
     # stride, per-row positions, start) inserted before sm_scale / stream.
     "sk_attn_fwd_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp,

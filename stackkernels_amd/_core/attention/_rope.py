@@ -73,4 +73,27 @@ def rope_args(cos, sin, start_pos, b: int, d: int, dev: torch.device) -> RopeArg
     return RopeArgs(cos, sin, start_pos, b, d, dev)
 
 
-__all__ = ["RopeArgs", "rope_args"]
+def rope_rotate(x: torch.Tensor, rope: RopeArgs, inverse: bool = False,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """``sk_rope_rotate``: x (B, H, S, D) rotated by its RoPE angles, token t of
+    row b at ``start_pos(+[b]) + t``, or by their negatives (``inverse``, the
+    adjoint: the reference's ``rope_bwd``, ``src/stackkernels/_core/positional/
+    rope.py:137-222``, ``torch/embedding.py:46-66``).  ``out`` may be ``x``."""
+    b, h, s, d = x.shape
+    if x.stride(-1) != 1 or x.data_ptr() % 16 or any(st % (16 // x.element_size())
+                                                     for st in x.stride()[:3]):
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            x = x.clone()
+    if out is None:
+        out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.sk_rope_rotate(_lib.dtype_code(x.dtype), x.data_ptr(), out.data_ptr(), b, h, s,
+                                d, _lib.strides3(x), _lib.strides3(out), *rope.args,
+                                int(bool(inverse)), _lib.stream_ptr(x.device))
+    _lib.check(rc, "rope_rotate")
+    return out
+
+
+__all__ = ["RopeArgs", "rope_args", "rope_rotate"]

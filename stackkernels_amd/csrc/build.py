@@ -19,7 +19,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(os.path.dirname(HERE))
 INCLUDE = os.path.join(REPO, "include")
-SOURCES = ["sk_abi.hip", "sk_fwd.hip", "sk_decode.hip", "sk_fp32.hip", "sk_bwd.hip", "sk_cache.hip"]
+SOURCES = ["sk_abi.hip", "sk_fwd.hip", "sk_decode.hip", "sk_fp32.hip", "sk_bwd.hip", "sk_cache.hip",
+           "sk_rotate.hip"]
 LIB_NAME = "libsk_attn.so"
 ARCH = "gfx950"
 

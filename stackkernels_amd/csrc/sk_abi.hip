@@ -772,6 +772,47 @@ int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v, void*
                            kp_strides, vp_strides, r, stream);
 }
 
+int sk_rope_rotate(int dtype, const void* x, void* out, int B, int H, int S, int D,
+                   const int64_t* x_strides, const int64_t* out_strides, const void* rope_cos,
+                   const void* rope_sin, int rope_dtype, int rope_rows, int64_t rope_stride,
+                   const int32_t* rope_pos, int rope_start, int inverse, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(dtype, B, H, 1, S, 0, D);
+  if (rc) return rc;
+  if ((rc = check_strides(dtype, "x", x_strides)) || (rc = check_strides(dtype, "out", out_strides)))
+    return rc;
+  sk::RopeParams r{};
+  const int64_t rows = (int64_t)B * H * S;
+  if ((rc = make_rope(rope_cos, rope_sin, rope_dtype, rope_rows, rope_stride, rope_pos,
+                      rope_start, D, rows > 0 ? S : 0, &r)))
+    return rc;
+  if (rows == 0) return SK_OK;
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("out", out))) return rc;
+  if (x != out) {
+    // In place or disjoint: a partial overlap would let one row's write
+    // reach another row's unread input.
+    const int64_t es = elem_bytes(dtype);
+    const int64_t span_x = ((int64_t)(B - 1) * x_strides[0] + (int64_t)(H - 1) * x_strides[1] +
+                            (int64_t)(S - 1) * x_strides[2] + D) * es;
+    const int64_t span_o = ((int64_t)(B - 1) * out_strides[0] + (int64_t)(H - 1) * out_strides[1] +
+                            (int64_t)(S - 1) * out_strides[2] + D) * es;
+    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out;
+    if (xa < oa + (uintptr_t)span_o && oa < xa + (uintptr_t)span_x)
+      return fail(SK_EINVAL, "out overlaps x without being x");
+  }
+  sk::RotateParams p{};
+  p.x = x, p.out = out;
+  p.x_sb = x_strides[0], p.x_sh = x_strides[1], p.x_ss = x_strides[2];
+  p.o_sb = out_strides[0], p.o_sh = out_strides[1], p.o_ss = out_strides[2];
+  p.B = B, p.H = H, p.S = S, p.D = D;
+  p.dtype = dtype;
+  p.inverse = inverse != 0;
+  p.rope = r;
+  const hipError_t e = sk::launch_rope_rotate(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sk_rope_rotate launch");
+  return SK_OK;
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------- introspection

@@ -203,6 +203,21 @@ struct CacheParams {
   RopeParams rope;
 };
 
+// Rotation of a (B, H, S, D) tensor by its RoPE angles (inverse = 0) or by
+// their negatives, the adjoint (inverse = 1): token t of batch row b at the
+// position RopeParams gives it.  out may be x (in place).  Strides are
+// element strides (b, h, s); the head dim is contiguous.
+struct RotateParams {
+  const void* x;
+  void* out;
+  int64_t x_sb, x_sh, x_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int B, H, S, D;
+  int dtype;  // SK_F32 / SK_F16 / SK_BF16
+  int inverse;
+  RopeParams rope;
+};
+
 // What a launcher runs for given parameters: the kernel, its grid and block,
 // and the tile configuration of that instantiation.  Each launcher builds its
 // plan with the plan_* function below and launches exactly that plan, and
@@ -245,6 +260,7 @@ hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s);
 hipError_t launch_bwd_mfma(int dtype, const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_bwd_f32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_kv_cache_update(const CacheParams& p, hipStream_t s);
+hipError_t launch_rope_rotate(const RotateParams& p, hipStream_t s);
 
 // Rows of queries one forward workgroup covers for (dtype, head dim, batch x
 // query heads, query length, key length, causal mask).

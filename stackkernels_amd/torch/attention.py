@@ -20,6 +20,7 @@ import torch.nn as nn
 from stackkernels_amd._core.attention.decode import flash_decode as core_flash_decode
 from stackkernels_amd._core.attention.decode import flash_decode_paged as core_flash_decode_paged
 from stackkernels_amd._core.attention.flash_bwd import flash_attn_bwd
+from stackkernels_amd._core.attention._rope import rope_args, rope_rotate
 from stackkernels_amd._core.attention.flash_fwd import flash_attn_fwd
 from stackkernels_amd._reference.torch.attention import (
     attention_reference,
@@ -104,8 +105,9 @@ def flash_attention(
             ``apply_rope(q, cos=..., sin=..., start_pos=...)`` would, inside the
             kernel's prologue: query row i at position ``start_pos + i``.  k is
             taken as already rotated (as ``kv_cache_update`` with the same tables
-            stores it).  Inference only: raises if a gradient would be needed.
-            Not in the reference, which rotates in a separate pass.
+            stores it).  Differentiable: the backward rotates dq back by the
+            adjoint, as the reference's ``RoPEFunction.backward`` does.  Not in
+            the reference, which rotates in a separate pass.
         start_pos: int, or integer (B,) tensor of per-row positions.
 
     Returns:
@@ -113,17 +115,49 @@ def flash_attention(
     """
     if rope_cos is None and rope_sin is None:
         return FlashAttentionFunction.apply(q, k, v, is_causal, sm_scale)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
-        raise NotImplementedError(
-            "flash_attention with fused RoPE is forward-only; rotate q first to train")
     if should_use_hip(q):
-        out, _ = flash_attn_fwd(ensure_contiguous(q), ensure_contiguous(k), ensure_contiguous(v),
-                                is_causal=is_causal, sm_scale=sm_scale, rope_cos=rope_cos,
-                                rope_sin=rope_sin, start_pos=start_pos)
-        return out
+        return _FlashAttentionRoPEFunction.apply(q, k, v, is_causal, sm_scale, rope_cos, rope_sin,
+                                                 start_pos)
+    # CPU / reference path: the unfused pipeline, differentiable through autograd.
     qr = _rope_reference(q, rope_cos, rope_sin, start_pos)
     out, _ = attention_reference(qr, k, v, is_causal=is_causal, sm_scale=sm_scale)
     return out
+
+
+class _FlashAttentionRoPEFunction(torch.autograd.Function):
+    """``flash_attention`` with q rotated in the forward kernel's prologue.
+
+    Forward: ``sk_attn_fwd_rope`` (the rotated q is never written out).
+    Backward: the unfused pipeline's gradient, with the rotated q rebuilt by
+    ``sk_rope_rotate`` bit for bit as the forward formed it:
+    ``dq = R^T dq_rot`` where ``(dq_rot, dk, dv)`` is the attention backward at
+    the rotated q, i.e. the reference's ``RoPEFunction.backward``
+    (``src/stackkernels/torch/embedding.py:46-66``) after its attention
+    backward (``torch/attention.py:63-102``).  k is taken as already rotated,
+    so its gradient is the attention's.  The tables get no gradient.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, q, k, v, is_causal, sm_scale, rope_cos, rope_sin, start_pos):
+        scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else sm_scale
+        qc, kc, vc = ensure_contiguous(q), ensure_contiguous(k), ensure_contiguous(v)
+        out, lse = flash_attn_fwd(qc, kc, vc, is_causal=is_causal, sm_scale=scale,
+                                  rope_cos=rope_cos, rope_sin=rope_sin, start_pos=start_pos)
+        ctx.is_causal = is_causal
+        ctx.sm_scale = scale
+        ctx.rope = rope_args(rope_cos, rope_sin, start_pos, q.shape[0], q.shape[-1], q.device)
+        ctx.save_for_backward(qc, kc, vc, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, do: torch.Tensor):
+        q, k, v, out, lse = ctx.saved_tensors
+        q_rot = rope_rotate(q, ctx.rope)
+        dq, dk, dv = flash_attn_bwd(ensure_contiguous(do), q_rot, k, v, out, lse,
+                                    is_causal=ctx.is_causal, sm_scale=ctx.sm_scale)
+        del q_rot
+        dq = rope_rotate(dq, ctx.rope, inverse=True, out=dq)
+        return dq, dk, dv, None, None, None, None, None
 
 
 def _rope_reference(x, cos, sin, start_pos):

@@ -436,6 +436,51 @@ def test_planted_rope_sign_slip_is_caught():
     assert np.abs(wrong - _rope_complex(x, cos, sin, pos)).max() > 1e-2
 
 
+def test_rope_adjoint_is_the_transpose():
+    """<R x, y> = <x, R^T y> for tables whose two halves differ (so a sine taken from
+    the wrong half, or a wrong sign, breaks the identity), in float64."""
+    rng = np.random.default_rng(6)
+    b, h, s, d = 2, 2, 5, 32
+    cos = rng.standard_normal((12, d))
+    sin = rng.standard_normal((12, d))
+    x = rng.standard_normal((b, h, s, d))
+    y = rng.standard_normal((b, h, s, d))
+    pos = np.array([[0, 3, 11, 7, 2], [5, 5, 1, 9, 4]])
+    rx = orc.rope_rotate(x, cos, sin, pos).astype(np.float64)
+    rty = orc.rope_rotate_adjoint(y, cos, sin, pos, dtype=np.float64)
+    lhs = (rx * y).sum(axis=-1)
+    rhs = (x * rty).sum(axis=-1)
+    np.testing.assert_allclose(lhs, rhs, rtol=1e-5, atol=1e-5)
+    # the same identity fails for the rotation itself in place of its adjoint
+    wrong = orc.rope_rotate(y, cos, sin, pos).astype(np.float64)
+    assert np.abs((x * wrong).sum(axis=-1) - lhs).max() > 1e-1
+
+
+def test_rope_adjoint_undoes_the_rotation_and_matches_the_reference_formula():
+    """With real tables R is orthogonal, so R^T R x = x; and for precompute_freqs tables
+    (equal halves) the adjoint is the reference's backward formula
+    dx = dy * cos - rotate_half(dy) * sin, bit for bit in float32."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(7)
+    b, h, s, d = 2, 3, 6, 64
+    cos, sin = orc.rope_tables(d, 100)
+    x = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    pos = orc.rope_positions(np.array([3, 40]), b, s)
+    back = orc.rope_rotate_adjoint(orc.rope_rotate(x, cos, sin, pos), cos, sin, pos)
+    np.testing.assert_allclose(back, x, rtol=0, atol=1e-5)
+    c32, s32 = cos.astype(np.float32), sin.astype(np.float32)
+    dy = torch.from_numpy(x)
+    cs = torch.from_numpy(c32[pos][:, None])
+    sn = torch.from_numpy(s32[pos][:, None])
+    half = d // 2
+    rot = torch.cat((-dy[..., half:], dy[..., :half]), dim=-1)
+    ref = (dy * cs) - (rot * sn)
+    np.testing.assert_array_equal(orc.rope_rotate_adjoint(x, c32, s32, pos), ref.numpy())
+    # positions outside the table leave their tokens
+    out = orc.rope_rotate_adjoint(x, cos, sin, np.full((b, s), 100))
+    np.testing.assert_array_equal(out, x)
+
+
 def test_round_to_matches_torch_casts():
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(5)

@@ -232,7 +232,27 @@ def test_flash_attention_rope_reference_path():
     qr = orc.rope_rotate(q.numpy(), cos.numpy(), sin.numpy(), orc.rope_positions(4, b, sq))
     want, _ = orc.attention_forward(qr, k.numpy(), v.numpy(), is_causal=True)
     np.testing.assert_allclose(out.numpy(), want, rtol=0, atol=1e-5)
-    with pytest.raises(NotImplementedError, match="forward-only"):
-        flash_attention(q.requires_grad_(True), k, v, True, rope_cos=cos, rope_sin=sin)
     with pytest.raises(ValueError, match="RoPE tables"):
         flash_attention(q.detach(), k, v, rope_cos=cos[:, :16], rope_sin=sin[:, :16])
+
+
+def test_flash_attention_rope_reference_path_backward():
+    """The CPU path with fused-RoPE arguments is the unfused pipeline under autograd:
+    dq = R^T (dq at the rotated q), dk and dv those of attention at the rotated q."""
+    g = torch.Generator().manual_seed(9)
+    b, hq, hkv, sq, sk, d = 2, 4, 2, 6, 10, 32
+    q = torch.randn(b, hq, sq, d, generator=g, dtype=torch.float64).float()
+    k = torch.randn(b, hkv, sk, d, generator=g).requires_grad_(True)
+    v = torch.randn(b, hkv, sk, d, generator=g).requires_grad_(True)
+    do = torch.randn(b, hq, sq, d, generator=g)
+    cos, sin = _tables(d, 64)
+    qg = q.clone().requires_grad_(True)
+    flash_attention(qg, k, v, True, rope_cos=cos, rope_sin=sin, start_pos=4).backward(do)
+    pos = orc.rope_positions(4, b, sq)
+    qr = orc.rope_rotate(q.numpy(), cos.numpy(), sin.numpy(), pos)
+    dqr, dk, dv = orc.attention_backward(qr, k.detach().numpy(), v.detach().numpy(), do.numpy(),
+                                         True)
+    dq = orc.rope_rotate_adjoint(dqr, cos.numpy(), sin.numpy(), pos, dtype=np.float64)
+    np.testing.assert_allclose(qg.grad.numpy(), dq, rtol=0, atol=1e-4)
+    np.testing.assert_allclose(k.grad.numpy(), dk, rtol=0, atol=1e-4)
+    np.testing.assert_allclose(v.grad.numpy(), dv, rtol=0, atol=1e-4)

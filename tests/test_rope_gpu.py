@@ -251,3 +251,115 @@ def test_forward_rope_long_work_entry_equals_forward_on_rotated_q():
         base = flash_attention(qr, k, v, True)
     torch.cuda.synchronize()
     assert torch.equal(out, base)
+
+
+# ------------------------------------------------------------ standalone rotation
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("table_dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("inverse", [False, True])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_rope_rotate_kernel_bitexact(dtype, table_dtype, inverse, in_place):
+    """sk_rope_rotate against the oracle's float32 rotation / adjoint rounded to the
+    tensor type, bit for bit.  Tables with unequal halves, so a sine taken from the
+    wrong half shows; per-row positions, one running past the table; a BSHD view."""
+    from stackkernels_amd._core.attention._rope import rope_args, rope_rotate
+
+    b, h, s, d = 3, 4, 37, 128
+    g = torch.Generator().manual_seed(21 + inverse)
+    x = torch.randn(b, s, h, d, generator=g).to(dtype).cuda().transpose(1, 2)  # strided view
+    cos = torch.randn(50, d, generator=g).to(table_dtype).cuda()
+    sin = torch.randn(50, d, generator=g).to(table_dtype).cuda()
+    starts = torch.tensor([0, 9, 30], dtype=torch.int32)
+    ra = rope_args(cos, sin, starts.cuda(), b, d, x.device)
+    src = x.contiguous() if in_place else x
+    keep = src.clone()
+    y = rope_rotate(src, ra, inverse=inverse, out=src if in_place else None)
+    torch.cuda.synchronize()
+    assert native_loaded()
+    if in_place:
+        assert y.data_ptr() == src.data_ptr()
+    pos = orc.rope_positions(starts.numpy(), b, s)
+    fn = orc.rope_rotate_adjoint if inverse else orc.rope_rotate
+    want = orc.round_to(fn(np64(keep).astype(np.float32), np64(cos), np64(sin), pos), NP_DT[dtype])
+    np.testing.assert_array_equal(np64(y), want)
+
+
+def test_rope_rotate_argument_errors():
+    from stackkernels_amd._core.attention._rope import rope_args, rope_rotate
+
+    x = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16, device="cuda")
+    cos, sin = _tables(128, 4)
+    with pytest.raises(ValueError, match="outside the rope table"):
+        rope_rotate(x, rope_args(cos, sin, 0, 1, 128, x.device))
+    cos, sin = _tables(128, 64)
+    big = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="overlaps"):
+        rope_rotate(big[:, :, :8], rope_args(cos, sin, 0, 1, 128, x.device), out=big[:, :, 4:12])
+
+
+# ------------------------------------------------------------ fused-RoPE backward
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("per_row", [False, True])
+def test_forward_rope_backward_matches_oracle(dtype, causal, d, per_row):
+    """flash_attention(..., rope_cos=, rope_sin=) under autograd: dQ, dK, dV against the
+    float64 oracle of the unfused pipeline -- attention_backward at the rotated q (q
+    rotated as the forward kernel rotates it, rounded to the type), then the adjoint of
+    the rotation on dQ -- within the stated 2e-2; O as the forward on the rotated q."""
+    b, hq, hkv, sq, sk = 2, 4, 2, 150, 230
+    q, k, v = make_qkv(b, hq, hkv, sq, sk, d, dtype, seed=d + 2 * causal + per_row)
+    cos, sin = _tables(d, 1024)
+    starts = torch.tensor([3, 700], dtype=torch.int32) if per_row else None
+    sp = starts.cuda() if per_row else 77
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    out = flash_attention(q, k, v, causal, rope_cos=cos, rope_sin=sin, start_pos=sp)
+    do = torch.randn(out.shape, generator=torch.Generator().manual_seed(5)).to(dtype).cuda()
+    out.backward(do)
+    torch.cuda.synchronize()
+    assert native_loaded()
+    pos = orc.rope_positions(starts.numpy() if per_row else 77, b, sq)
+    qr = orc.round_to(orc.rope_rotate(np64(q).astype(np.float32), np64(cos), np64(sin), pos),
+                      NP_DT[dtype]).astype(np.float64)
+    o_ref, _ = orc.attention_forward(qr, np64(k), np64(v), causal)
+    assert_close_maxabs(out, o_ref, TOL[dtype], "O")
+    dqr, dk, dv = orc.attention_backward(qr, np64(k), np64(v), np64(do), causal)
+    dq = orc.rope_rotate_adjoint(dqr, np64(cos), np64(sin), pos, dtype=np.float64)
+    assert_close_maxabs(q.grad, dq, TOL[dtype], "dQ")
+    assert_close_maxabs(k.grad, dk, TOL[dtype], "dK")
+    assert_close_maxabs(v.grad, dv, TOL[dtype], "dV")
+
+
+def test_forward_rope_backward_c3_shape():
+    """C3 shape (bf16 causal GQA, bottom-right mask, B=2 Hq=32 Hkv=8 Sq=2048 Sk=8192): the
+    fused-RoPE training step gives dK/dV equal to the plain backward at the oracle-rotated
+    q, and dQ equal to the kernel's adjoint rotation of that backward's dQ, bit for bit;
+    one batch row's dQ against the float64 oracle of the composite."""
+    from stackkernels_amd._core.attention._rope import rope_args, rope_rotate
+
+    b, hq, hkv, sq, sk, d = 2, 32, 8, 2048, 8192, 128
+    q, k, v = make_qkv(b, hq, hkv, sq, sk, d, torch.bfloat16, seed=41)
+    cos, sin = _tables(d, 8192)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    out = flash_attention(q, k, v, True, rope_cos=cos, rope_sin=sin, start_pos=sk - sq)
+    do = torch.randn(out.shape, generator=torch.Generator(device="cuda").manual_seed(6),
+                     device="cuda").to(torch.bfloat16)
+    out.backward(do)
+    pos = orc.rope_positions(sk - sq, b, sq)
+    qr = _rotated(q.detach(), cos, sin, pos).requires_grad_(True)
+    kp, vp = k.detach().clone().requires_grad_(True), v.detach().clone().requires_grad_(True)
+    base = flash_attention(qr, kp, vp, True)
+    base.backward(do)
+    dq = rope_rotate(qr.grad, rope_args(cos, sin, sk - sq, b, d, q.device), inverse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    assert torch.equal(k.grad, kp.grad) and torch.equal(v.grad, vp.grad)
+    assert torch.equal(q.grad, dq)
+    dqr, _, _ = orc.attention_backward(np64(qr[1:2, :4]), np64(k[1:2, :1]), np64(v[1:2, :1]),
+                                       np64(do[1:2, :4]), True)
+    want = orc.rope_rotate_adjoint(dqr, np64(cos), np64(sin), pos[1:2], dtype=np.float64)
+    assert_close_maxabs(q.grad[1:2, :4], want, TOL[torch.bfloat16], "dQ (batch 1, heads 0-3)")
