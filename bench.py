@@ -761,8 +761,31 @@ def _cpu_baseline_next_rows(w: dict, budget_s: float):
         "cores": threads,
         "kind": "port",
         "sample": (f"{what} of {w['name']}, {done} repetition(s) in {el:.1f} s; "
-                   f"host {os.cpu_count()} CPUs, torch threads {threads}"),
+                   f"host {os.cpu_count()} CPUs ({host_cpu_model()}), torch threads {threads}"),
+        "host_cpu": host_cpu_model(),
     }
+
+
+def host_cpu_model() -> str:
+    """The host CPU's model line, as ``lscpu`` prints it ("Model name"), read from
+    /proc/cpuinfo; ``lscpu`` itself where that file has none."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return "unknown"
 
 
 def run_cpu_baseline(w: dict, budget_s: float):
@@ -813,8 +836,10 @@ def run_cpu_baseline(w: dict, budget_s: float):
         "kind": "port",
         "sample": (f"attention_reference (fp32 torch restatement of the reference CPU path) on "
                    f"batch row 0, {hq_chunk} query head(s) / {hkv_chunk} KV head(s) of {w['name']}, "
-                   f"{done} repetition(s) in {el:.1f} s; host {os.cpu_count()} CPUs, "
+                   f"{done} repetition(s) in {el:.1f} s; host {os.cpu_count()} CPUs "
+                   f"({host_cpu_model()}), "
                    f"torch threads {threads}"),
+        "host_cpu": host_cpu_model(),
     }
 
 

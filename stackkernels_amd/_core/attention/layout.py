@@ -2,10 +2,12 @@
 
 ``validate_attention_layout`` keeps the reference's checks and ``ValueError``
 messages (``src/stackkernels/_opt/memory/layout.py:7-41``).
-``padded_head_dim`` is this build's own rule: the gfx950 kernels are compiled
-for head dims padded to 64, 96, 128 or 256.  ``get_padded_head_dim`` is the
-reference's name for it (``layout.py:44-56``, where the answer is the Triton
-tile width); here it raises ``ValueError`` above 256, where no kernel exists.
+``get_padded_head_dim`` keeps the reference's helper and its values
+(``layout.py:44-56``: the power-of-two tile width, 16 up to D = 16, 32 up to
+32, then 64, 128, 256 and the next power of two beyond).  ``padded_head_dim``
+is this build's own rule, what the launchers use: the gfx950 kernels are
+compiled for head dims padded to 64, 96, 128 or 256 (0 above 256, where no
+kernel exists).
 """
 
 from __future__ import annotations
@@ -45,8 +47,11 @@ MAX_HEAD_DIM = 256
 
 
 def get_padded_head_dim(D: int) -> int:
-    """Head dim the kernels run ``D`` at (64, 96, 128 or 256); ValueError above 256."""
-    p = padded_head_dim(int(D))
-    if p == 0:
-        raise ValueError(f"head dim {D} > {MAX_HEAD_DIM} has no kernel")
-    return p
+    """The reference's tile padding of ``D``: the smallest power of two >= D, at least
+    16 (``src/stackkernels/_opt/memory/layout.py:44-56``).  The kernels here run at
+    ``padded_head_dim(D)`` instead."""
+    D = int(D)
+    for p in (16, 32, 64, 128, 256):
+        if D <= p:
+            return p
+    return 1 << (D - 1).bit_length()

@@ -235,10 +235,13 @@ def test_layout_and_workspace():
     assert layout.validate_attention_layout(q, k, k) == (2, 8, 2, 16, 32, 80)
     with pytest.raises(ValueError, match="divisible"):
         layout.validate_attention_layout(torch.zeros(2, 3, 16, 80), k, k)
-    assert [layout.get_padded_head_dim(d) for d in (16, 64, 80, 96, 128, 200)] == \
-        [64, 64, 96, 96, 128, 256]
-    with pytest.raises(ValueError):
-        layout.get_padded_head_dim(300)
+    # the reference's helper and values (power-of-two tile width, at least 16) ...
+    assert [layout.get_padded_head_dim(d) for d in (1, 16, 17, 32, 64, 80, 96, 128, 200, 256,
+                                                    300, 513)] == \
+        [16, 16, 32, 32, 64, 128, 128, 128, 256, 256, 512, 1024]
+    # ... and the head dims the gfx950 kernels run at
+    assert [layout.padded_head_dim(d) for d in (16, 64, 80, 96, 128, 200, 256, 300)] == \
+        [64, 64, 96, 96, 128, 256, 256, 0]
     ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu")
     assert ns == 8 and ws.numel() == 64 * 32 * 8 * (128 + 1) * 4
     ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu", num_splits=4)
