@@ -179,6 +179,26 @@ WORKLOADS = {
 }
 
 
+# Tile-table study shapes: selectable with --workload, not part of the default
+# run (the head dims and plans the headline configs do not exercise).
+STUDY_WORKLOADS = {
+    "fwd_d64": dict(name="tile study: flash_attention fwd bf16 causal MHA, D=64", B=4, Hq=32,
+                    Hkv=32, Sq=4096, Sk=4096, D=64, causal=True, dtype="bf16", kind="fwd"),
+    "fwd_d64_long": dict(name="tile study: flash_attention fwd bf16 causal MHA, D=64, long "
+                              "sequence", B=1, Hq=32, Hkv=32, Sq=16384, Sk=16384, D=64,
+                         causal=True, dtype="bf16", kind="fwd"),
+    "fwd_d256": dict(name="tile study: flash_attention fwd bf16 causal MHA, D=256", B=2, Hq=16,
+                     Hkv=16, Sq=4096, Sk=4096, D=256, causal=True, dtype="bf16", kind="fwd"),
+    "fwdbwd_d64": dict(name="tile study: C3 shape fwd+bwd bf16 causal GQA bottom-right, D=64",
+                       B=2, Hq=32, Hkv=8, Sq=2048, Sk=8192, D=64, causal=True, dtype="bf16",
+                       kind="fwdbwd"),
+    "fwdbwd_d256": dict(name="tile study: C3 shape fwd+bwd bf16 causal GQA bottom-right, D=256",
+                        B=2, Hq=32, Hkv=8, Sq=2048, Sk=8192, D=256, causal=True, dtype="bf16",
+                        kind="fwdbwd"),
+}
+ALL_WORKLOADS = {**WORKLOADS, **STUDY_WORKLOADS}
+
+
 NUM_SPLITS = 0  # --num-splits: decode split count override (0: the gfx950 table's)
 
 
@@ -390,6 +410,10 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
         nb = ctypes.c_size_t(0)
         _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
                    "plan")
+        if NUM_SPLITS:
+            ns.value = NUM_SPLITS
+            _lib.check(lib.sk_decode_workspace(code, B, Hq, Hkv, Sk, D, NUM_SPLITS,
+                                               ctypes.byref(nb)), "workspace")
         ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
         q, kp, vp = inputs[0]
         o = torch.empty_like(q)
@@ -410,6 +434,10 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
         nb = ctypes.c_size_t(0)
         _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
                    "plan")
+        if NUM_SPLITS:
+            ns.value = NUM_SPLITS
+            _lib.check(lib.sk_decode_workspace(code, B, Hq, Hkv, Sk, D, NUM_SPLITS,
+                                               ctypes.byref(nb)), "workspace")
         ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
         q, k, v = inputs[0]
         o = torch.empty_like(q)
@@ -562,18 +590,20 @@ def run_gpu(w: dict, steps: int, warmup: int):
             flash_decode(q, k, v, num_splits=NUM_SPLITS or None)
     elif w["kind"] == "decode_varlen":
         q0 = inputs[0][0]
-        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        details["num_splits"] = (NUM_SPLITS or
+                                 plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0])
         lens_dev = varlen_lengths(w).to(dev)
         details["mean_length"] = round(float(lens_dev.float().mean()), 1)
 
         def step(i):
             q, k, v = inputs[0]
-            flash_decode(q, k, v, cache_seqlens=lens_dev)
+            flash_decode(q, k, v, cache_seqlens=lens_dev, num_splits=NUM_SPLITS or None)
     elif w["kind"] == "decode_paged":
         from stackkernels_amd._core.attention.decode import flash_decode_paged
 
         q0 = inputs[0][0]
-        details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        details["num_splits"] = (NUM_SPLITS or
+                                 plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0])
         lens_dev = varlen_lengths(w).to(dev)
         table_dev = paged_table(w).to(dev)
         details["mean_length"] = round(float(lens_dev.float().mean()), 1)
@@ -581,7 +611,7 @@ def run_gpu(w: dict, steps: int, warmup: int):
 
         def step(i):
             q, kp, vp = inputs[0]
-            flash_decode_paged(q, kp, vp, table_dev, lens_dev)
+            flash_decode_paged(q, kp, vp, table_dev, lens_dev, num_splits=NUM_SPLITS or None)
     elif w["kind"] == "decode_rope":
         q0 = inputs[0][0]
         details["num_splits"] = plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
@@ -844,7 +874,7 @@ def run_cpu_baseline(w: dict, budget_s: float):
 
 
 def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
-    w = WORKLOADS[key]
+    w = ALL_WORKLOADS[key]
     units, unit = work_units(w)
     ms_step, ms_kernel, details = run_gpu(w, steps, warmup)
     value = _rate(units, unit, ms_step / 1e3)
@@ -933,16 +963,18 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["copy", "gemm"], default="fwd",
+    ap.add_argument("--workload", choices=sorted(ALL_WORKLOADS) + ["copy", "gemm"], default="fwd",
                     help="headline workload (default fwd = C2); 'copy' times a plain 1 GiB "
                          "device copy, the calibration kernel for the HBM-traffic counters; "
-                         "'gemm' times a bf16 8192^3 torch.matmul, the sustained-MFMA reference")
+                         "'gemm' times a bf16 8192^3 torch.matmul, the sustained-MFMA reference; "
+                         "fwd_d64, fwd_d64_long, fwd_d256, fwdbwd_d64, fwdbwd_d256 are tile-study "
+                         "shapes outside the default run")
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload (0 disables)")
     ap.add_argument("--num-splits", type=int, default=0,
-                    help="decode / decode_mqa: run this split count instead of the table's "
-                         "(tile-table study; 0 = the table)")
+                    help="decode, decode_mqa, decode_varlen, decode_paged: run this split count "
+                         "instead of the table's (tile-table study; 0 = the table)")
     args = ap.parse_args()
     global NUM_SPLITS
     NUM_SPLITS = args.num_splits
@@ -977,7 +1009,7 @@ def main() -> int:
         # the sustained-MFMA reference of this part, beside the attention rates
         extra.append(gemm_calibration(args.steps, args.warmup))
         print(f"# gemm: {extra[-1]['TFLOP/s']} TFLOP/s", file=sys.stderr, flush=True)
-    w = WORKLOADS[args.workload]
+    w = ALL_WORKLOADS[args.workload]
     line = {
         "metric": METRIC,
         "value": head["value"],

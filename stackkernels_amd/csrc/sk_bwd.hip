@@ -76,6 +76,19 @@
 #define SK_BWD_DKV_STAGES 6
 #endif
 // Key blocks of 32 per dK/dV wave in the 6-deep schedule: 2 or 1.
+// The D = 64 dK/dV ring: 6 (the pipelined schedule, the table), or 4 for the
+// one-tile-per-step schedule in a tile-study build.  Against 4, bit-identical:
+// C3 shape at D = 64 9.9% faster, causal MHA S = 8192 7.1%, causal S = 2048
+// 6.2%, non-causal S = 2048 / 4096 1.2% / 2.0%; causal S = 1024 2.1% slower
+// and causal S = 4096 even (one box, alternating libraries).
+#ifndef SK_BWD_DKV_STAGES_D64
+#define SK_BWD_DKV_STAGES_D64 6
+#endif
+// Output head-dim columns per dK/dV workgroup at D = 256: 128 (two
+// workgroups per key block, the table) or 256 in a tile-study build.
+#ifndef SK_BWD_DKV_DO_D256
+#define SK_BWD_DKV_DO_D256 128
+#endif
 #ifndef SK_BWD_DKV_KB
 #define SK_BWD_DKV_KB 1
 #endif
@@ -164,7 +177,7 @@ __device__ __forceinline__ u32x4 lds_tr_pair(const uint8_t* lo, const uint8_t* h
 //
 // Two schedules: a 4-deep ring where a step is one tile's S, P and dV (role
 // 0) or dS, dK and the next dP (role 1), each phase a block of MFMAs or of
-// VALU work; and, at D = 128, a 6-deep ring where role 0 computes S one tile
+// VALU work; and, at D = 64 and D = 128, a 6-deep ring where role 0 computes S one tile
 // ahead so that every step interleaves MFMAs with the VALU work of the
 // previous tile in the same wave (a wave overlaps MFMA and VALU issue only
 // with its own instructions).
@@ -1511,12 +1524,12 @@ __global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
 }
 
 // gfx950 tile table for the backward, by head dim (padded to 64, 128 or 256;
-// other dims run zero-padded in the next size up), 4 ring stages:
+// other dims run zero-padded in the next size up):
 //   dK/dV: 8 waves, one workgroup per CU, 128 keys per workgroup, 32-query
 //          tiles (at D = 256 the output head dim is split over two
-//          workgroups); LDS ring 4 x (Q + dO + stats) + P exchange
-//          = 72 / 104 / 152 KiB, at D = 128 6 x (Q + dO + stats) + P
-//          exchange = 140 KiB.
+//          workgroups); LDS ring 6 x (Q + dO + stats) + P exchange
+//          = 92 / 140 KiB at D = 64 / 128 (the pipelined schedule),
+//          4 x (Q + dO + stats) + P exchange = 152 KiB at D = 256.
 //   dQ:    4 waves, 128 query rows per workgroup, 32-key tiles; ring
 //          4 x (K + V) = 32 / 64 / 128 KiB, so two workgroups fit a CU at
 //          D <= 128.
@@ -1539,11 +1552,17 @@ struct DqConfig {
   static constexpr int kOcc = kDqSmall.occ;
   static constexpr int kMode = kDqSmall.mode;
 };
+// SK_BWD_DQ_TILE_D256 overrides the D = 256 row (32 keys, one workgroup per
+// CU, schedule 0) for candidate builds.
+#ifndef SK_BWD_DQ_TILE_D256
+#define SK_BWD_DQ_TILE_D256 32, 1, 0
+#endif
+constexpr DqTile kDq256{SK_BWD_DQ_TILE_D256};
 template <>
 struct DqConfig<256> {
-  static constexpr int kBn = 32;
-  static constexpr int kOcc = 1;
-  static constexpr int kMode = 0;
+  static constexpr int kBn = kDq256.bn;
+  static constexpr int kOcc = kDq256.occ;
+  static constexpr int kMode = kDq256.mode;
 };
 
 // (Batch, KV head) pairs a dK/dV or dQ-from-dS launch covers: a chunk of the
@@ -1554,10 +1573,11 @@ static int64_t launch_pairs(const BwdParams& p) {
 
 template <class T, int DP, int DO>
 static KernelPlan plan_dkv_t(BwdParams& p, bool causal) {
-  // D = 128: the 6-deep pipelined schedule (S one step ahead of P; 3%-7%
-  // faster there, 2% slower at D = 64); SK_BWD_DKV_STAGES=4 builds the
-  // 4-deep one-tile-per-step schedule instead.
-  constexpr int STAGES = DP == 128 ? SK_BWD_DKV_STAGES : 4;
+  // D = 128 and D = 64: the 6-deep pipelined schedule (S one step ahead of
+  // P; 3%-7% faster at D = 128, up to 10% at D = 64); SK_BWD_DKV_STAGES=4
+  // and SK_BWD_DKV_STAGES_D64=4 build the 4-deep one-tile-per-step schedule
+  // instead.  D = 256 keeps the 4-deep one (the 6-deep ring does not fit).
+  constexpr int STAGES = DP == 128 ? SK_BWD_DKV_STAGES : DP == 64 ? SK_BWD_DKV_STAGES_D64 : 4;
   // Keys per wave: 64 (two 32-key blocks; four waves, one per SIMD) in the
   // 6-deep schedule, else 32 (eight waves).
   constexpr int KB = STAGES == 6 ? SK_BWD_DKV_KB : 1;
@@ -1602,7 +1622,7 @@ template <class T>
 static KernelPlan plan_dkv_dt(BwdParams& p, bool causal) {
   if (p.D <= 64) return plan_dkv_t<T, 64, 64>(p, causal);
   if (p.D <= 128) return plan_dkv_t<T, 128, 128>(p, causal);
-  if (p.D <= 256) return plan_dkv_t<T, 256, 128>(p, causal);
+  if (p.D <= 256) return plan_dkv_t<T, 256, SK_BWD_DKV_DO_D256>(p, causal);
   return KernelPlan{};
 }
 

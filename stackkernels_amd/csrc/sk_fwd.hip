@@ -626,8 +626,15 @@ constexpr FwdTile kFwdD128Short{64, 4, 2, 2};
 #endif
 static_assert(kFwdD128Long.stages == 4 || kFwdD128Long.stages == 2, "ring depth 4 or 2");
 static_assert(kFwdD128Short.stages == 4 || kFwdD128Short.stages == 2, "ring depth 4 or 2");
+// -DSK_FWD_D64_TILE=64,4,2,4 or 64,8,1,4 fixes one D <= 64 entry for every
+// shape (tile study).
+#ifdef SK_FWD_D64_TILE
+constexpr FwdTile kFwdD64Long{SK_FWD_D64_TILE};
+constexpr FwdTile kFwdD64Short{SK_FWD_D64_TILE};
+#else
 constexpr FwdTile kFwdD64Long{64, 8, 1, 4};
 constexpr FwdTile kFwdD64Short{64, 4, 2, 4};
+#endif
 
 // Whether a D <= 128 forward over bh (batch, head) pairs of sq queries
 // against sk keys takes the short-work entry: short query sequences or a

@@ -1,6 +1,6 @@
 """GPU parity of the backward's software pipelines at every short trip count.
 
-The dK/dV kernel at D = 128 runs a 6-deep ring with S computed one query tile
+The dK/dV kernel at D = 64 and 128 runs a 6-deep ring with S computed one query tile
 ahead and a step's first operands read before its barrier; the dQ kernel at
 D <= 128 computes S^T one key tile ahead with the last tile peeled out of a
 loop unrolled by the ring depth.  Their prologues, wait counts and tails
@@ -51,6 +51,13 @@ def _check(b, hq, hkv, sq, sk, d, dtype, causal, seed):
 def test_dkv_query_tile_counts(n, causal):
     # one KV head with a group of 1: the dK/dV workgroup walks n query tiles
     _check(1, 2, 2, 32 * n, 128, 128, torch.bfloat16, causal, seed=100 + n)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", list(range(1, 10)))
+def test_dkv_query_tile_counts_d64(n, causal):
+    # the same 6-deep schedule at D = 64
+    _check(1, 2, 2, 32 * n, 128, 64, torch.float16, causal, seed=150 + n)
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 5])

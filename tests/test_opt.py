@@ -163,12 +163,13 @@ def test_pick_forward_and_backward():
     # D = 128: the five-GEMM backward (dQ from the dS tiles dK/dV stores)
     assert b["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_ds_kernel"
     assert b["grid"] == (8192 // 128) * 2 * 8 and b["dq"]["grid"] == (2048 // 256) * 2 * 32
-    # dK/dV: the 6-deep pipelined ring at D = 128, the 4-deep one elsewhere;
+    # dK/dV: the 6-deep pipelined ring at D = 128 (and 64), the 4-deep one at D = 256;
     # 8 waves (two roles x four 32-key groups) in both
     assert (b["num_stages"], b["num_warps"]) == (6, 8)
-    for d in (64, 256):
+    # the same 6-deep ring at D = 64, the 4-deep one at D = 256; both seven GEMMs
+    for d, stages in ((64, 6), (256, 4)):
         o = pick("flash_bwd", (2, 8, 512, d), dtype="bfloat16", kv_len=1024, num_kv_heads=2)
-        assert (o["num_stages"], o["num_warps"]) == (4, 8)
+        assert (o["num_stages"], o["num_warps"]) == (stages, 8)
         assert o["kernel_variant"] == "bwd_dkv_kernel+bwd_dq_kernel"  # seven GEMMs
     # dQ from the stored dS: 4 waves x 64 queries, 32-key tiles, 3-deep ring
     assert (b["dq"]["num_stages"], b["dq"]["num_warps"], b["dq"]["BLOCK_N"],
