@@ -350,8 +350,8 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
     if w["kind"] == "decode_step":
         ns = ctypes.c_int(0)
         nb = ctypes.c_size_t(0)
-        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
-                   "plan")
+        _lib.check(lib.sk_decode_plan_varlen(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns),
+                                             ctypes.byref(nb)), "plan")
         ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
         q, k, v = inputs[0]
         o = torch.empty_like(q)
@@ -408,8 +408,8 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
     if w["kind"] == "decode_paged":
         ns = ctypes.c_int(0)
         nb = ctypes.c_size_t(0)
-        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
-                   "plan")
+        _lib.check(lib.sk_decode_plan_varlen(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns),
+                                             ctypes.byref(nb)), "plan")
         if NUM_SPLITS:
             ns.value = NUM_SPLITS
             _lib.check(lib.sk_decode_workspace(code, B, Hq, Hkv, Sk, D, NUM_SPLITS,
@@ -432,8 +432,8 @@ def _abi_launcher(w: dict, inputs, do, torch, dev):
     if w["kind"] == "decode_varlen":
         ns = ctypes.c_int(0)
         nb = ctypes.c_size_t(0)
-        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
-                   "plan")
+        _lib.check(lib.sk_decode_plan_varlen(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns),
+                                             ctypes.byref(nb)), "plan")
         if NUM_SPLITS:
             ns.value = NUM_SPLITS
             _lib.check(lib.sk_decode_workspace(code, B, Hq, Hkv, Sk, D, NUM_SPLITS,
@@ -590,8 +590,8 @@ def run_gpu(w: dict, steps: int, warmup: int):
             flash_decode(q, k, v, num_splits=NUM_SPLITS or None)
     elif w["kind"] == "decode_varlen":
         q0 = inputs[0][0]
-        details["num_splits"] = (NUM_SPLITS or
-                                 plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0])
+        details["num_splits"] = (NUM_SPLITS or plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"],
+                                                    w["D"], per_row=True)[0])
         lens_dev = varlen_lengths(w).to(dev)
         details["mean_length"] = round(float(lens_dev.float().mean()), 1)
 
@@ -602,8 +602,8 @@ def run_gpu(w: dict, steps: int, warmup: int):
         from stackkernels_amd._core.attention.decode import flash_decode_paged
 
         q0 = inputs[0][0]
-        details["num_splits"] = (NUM_SPLITS or
-                                 plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0])
+        details["num_splits"] = (NUM_SPLITS or plan(q0.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"],
+                                                    w["D"], per_row=True)[0])
         lens_dev = varlen_lengths(w).to(dev)
         table_dev = paged_table(w).to(dev)
         details["mean_length"] = round(float(lens_dev.float().mean()), 1)
@@ -630,7 +630,8 @@ def run_gpu(w: dict, steps: int, warmup: int):
         vn = torch.randn(w["B"], w["Hkv"], 1, w["D"], generator=g, device=dev, dtype=q.dtype)
         lens = step_lengths(w).to(dev)
         cos, sin = rope_tables(w, dev)
-        details["num_splits"] = plan(q.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"])[0]
+        details["num_splits"] = plan(q.dtype, w["B"], w["Hq"], w["Hkv"], w["Sk"], w["D"],
+                                     per_row=True)[0]
         details["mean_length"] = round(float(lens.float().mean()) + 1, 1)
 
         def eager(i):

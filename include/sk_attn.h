@@ -145,7 +145,8 @@ SK_API int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k
 
 /*
  * Split-KV plan for single-token decode: the number of key splits the gfx950
- * table picks and the scratch bytes sk_decode then needs.  Replaces the split
+ * table picks and the scratch bytes sk_decode (uniform cache length) then
+ * needs; what sk_decode runs with num_splits = 0.  Replaces the split
  * heuristic chain decode_heuristic -> seed_configs
  * (reference: src/stackkernels/_opt/heuristics/flash_decode.py:9-12,
  * src/stackkernels/_opt/classes/decode.py:9-63) as used at
@@ -153,6 +154,16 @@ SK_API int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k
  */
 SK_API int sk_decode_plan(int dtype, int B, int Hq, int Hkv, int Sk, int D,
                    int* num_splits, size_t* workspace_bytes);
+
+/*
+ * The same for per-row cache lengths and paged pools (sk_decode_varlen,
+ * sk_decode_paged and their _rope forms with num_splits = 0): for groups of
+ * up to 16 query heads about twice the uniform plan's splits, since rows
+ * shorter than the longest leave a one-round grid uneven.  No counterpart in
+ * the reference (its decode has one cache length).
+ */
+SK_API int sk_decode_plan_varlen(int dtype, int B, int Hq, int Hkv, int Sk, int D,
+                          int* num_splits, size_t* workspace_bytes);
 
 /*
  * Single-token decode (Sq == 1), non-causal over all Sk keys.  Replaces the
@@ -203,8 +214,9 @@ SK_API int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D,
  * sk_decode with a cache length per batch row: row b attends to keys
  * [0, clamp(cache_seqlens[b], 0, Sk)) of its cache; a row with no key gives
  * O = 0.  cache_seqlens is a device array of B int32.  Sk is the cache
- * capacity and sets the split plan (sk_decode_plan / sk_decode_workspace
- * with the same Sk).  The reference has no counterpart yet: it realises the
+ * capacity and sets the split plan (sk_decode_plan_varlen /
+ * sk_decode_workspace with the same Sk; num_splits = 0 runs the
+ * sk_decode_plan_varlen count).  The reference has no counterpart yet: it realises the
  * per-sequence cache lengths its decode roadmap names (stubs
  * src/stackkernels/_core/attention/varlen.py, paged.py; reference decode
  * src/stackkernels/_core/attention/decode.py:192-312 takes one S_k for all rows).
@@ -224,7 +236,7 @@ SK_API int sk_decode_varlen(int dtype, const void* q, const void* k, const void*
  * (clamped to max_pages * page_size).  page_size is a positive multiple of 32;
  * a page index outside [0, num_pages) masks its keys.  block_table (B x
  * max_pages int32) and cache_seqlens (B int32) live on the device.  Plan the
- * splits with Sk = max_pages * page_size.  The reference has no counterpart
+ * splits with sk_decode_plan_varlen at Sk = max_pages * page_size.  The reference has no counterpart
  * yet: it realises the paged KV decode of its roadmap (stub
  * src/stackkernels/_core/attention/paged.py).
  */
@@ -389,7 +401,8 @@ SK_API int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v
  *            SK_OP_DECODE_COMBINE (grid 0 when one split writes O directly);
  *   Sq       ignored for decode; num_splits: decode only (0 = the table's pick);
  *   variant  SK_VARIANT_* bits: the decode over a paged pool, the RoPE
- *            prologue (forward and decode);
+ *            prologue (forward and decode), per-row cache lengths (decode:
+ *            the sk_decode_plan_varlen split count; paged implies it);
  *   query_device  0: no HIP call is made (works without a GPU) and the
  *            device-reported slots hold -1; 1: also ask the HIP runtime for
  *            the kernel's LDS bytes, registers per lane and resident
@@ -405,6 +418,7 @@ SK_API int sk_kv_cache_update_paged_rope(int dtype, const void* k, const void* v
 
 #define SK_VARIANT_PAGED 1
 #define SK_VARIANT_ROPE 2
+#define SK_VARIANT_VARLEN 4  /* decode with per-row cache lengths (the paged pool implies it) */
 
 #define SK_CFG_GRID 0           /* workgroups per launch                        */
 #define SK_CFG_THREADS 1        /* threads per workgroup (64 per wavefront)     */

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
                              ctypes.c_size_t, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_int, _c_float, _vp]),
     "sk_decode_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _intp, _sizep]),
+    "sk_decode_plan_varlen": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _intp,
+                                       _sizep]),
     "sk_decode_workspace": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                      _sizep]),
     "sk_decode": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _c_int,

@@ -32,13 +32,16 @@ from stackkernels_amd._core.attention.layout import validate_attention_layout
 from stackkernels_amd._core.attention.workspace import decode_workspace
 
 
-def plan(dtype: torch.dtype, b: int, hq: int, hkv: int, sk: int, d: int) -> tuple[int, int]:
-    """(num_splits, workspace bytes) the library picks for this decode shape."""
+def plan(dtype: torch.dtype, b: int, hq: int, hkv: int, sk: int, d: int,
+         per_row: bool = False) -> tuple[int, int]:
+    """(num_splits, workspace bytes) the library picks for this decode shape
+    (``per_row``: with per-row cache lengths or a paged pool)."""
     lib = _lib.load()
     ns = ctypes.c_int(0)
     nb = ctypes.c_size_t(0)
-    _lib.check(lib.sk_decode_plan(_lib.dtype_code(dtype), b, hq, hkv, sk, kernel_head_dim(d),
-                                  ctypes.byref(ns), ctypes.byref(nb)), "flash_decode plan")
+    fn = lib.sk_decode_plan_varlen if per_row else lib.sk_decode_plan
+    _lib.check(fn(_lib.dtype_code(dtype), b, hq, hkv, sk, kernel_head_dim(d), ctypes.byref(ns),
+                  ctypes.byref(nb)), "flash_decode plan")
     return ns.value, nb.value
 
 
@@ -72,7 +75,8 @@ def flash_decode(q, k, v, sm_scale: float | None = None, num_splits: int | None 
     qk, kk, vk = (kernel_operand(pad_head(t, dk)) for t in (q, k, v))
     lib = _lib.load()
     code = _lib.dtype_code(q.dtype)
-    ws, ns = decode_workspace(q.dtype, b, hq, hkv, sk, dk, dev, num_splits)
+    ws, ns = decode_workspace(q.dtype, b, hq, hkv, sk, dk, dev, num_splits,
+                              per_row=lens is not None)
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
     with torch.cuda.device(dev):
         if rope is not None:
@@ -151,7 +155,7 @@ def flash_decode_paged(q, k_pool, v_pool, block_table, cache_seqlens,
     lib = _lib.load()
     code = _lib.dtype_code(q.dtype)
     sk = max_pages * page_size
-    ws, ns = decode_workspace(q.dtype, b, hq, hkv, sk, dk, dev, num_splits)
+    ws, ns = decode_workspace(q.dtype, b, hq, hkv, sk, dk, dev, num_splits, per_row=True)
     out = torch.empty((b, hq, 1, dk), dtype=q.dtype, device=dev)
     paged_args = (code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(),
                   ws.data_ptr(), ws.numel(), ns, b, hq, hkv, num_pages, page_size, max_pages, dk,

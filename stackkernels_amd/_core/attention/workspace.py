@@ -43,16 +43,18 @@ def bwd_workspace(dtype: torch.dtype, B: int, Hq: int, Hkv: int, Sq: int, Sk: in
 
 
 def decode_workspace(dtype: torch.dtype, B: int, Hq: int, Hkv: int, Sk: int, D: int, device,
-                     num_splits: int | None = None) -> tuple[torch.Tensor, int]:
+                     num_splits: int | None = None,
+                     per_row: bool = False) -> tuple[torch.Tensor, int]:
     """(uint8 scratch, split count) for ``sk_decode*`` (D: the kernel head dim):
-    the gfx950 table's split count when ``num_splits`` is None, else the
-    given one."""
+    the gfx950 table's split count when ``num_splits`` is None (``per_row``:
+    the plan for per-row cache lengths and paged pools), else the given one."""
     lib = _lib.load()
     code = _lib.dtype_code(dtype)
     nb = ctypes.c_size_t(0)
     if num_splits is None:
         ns = ctypes.c_int(0)
-        _lib.check(lib.sk_decode_plan(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
+        fn = lib.sk_decode_plan_varlen if per_row else lib.sk_decode_plan
+        _lib.check(fn(code, B, Hq, Hkv, Sk, D, ctypes.byref(ns), ctypes.byref(nb)),
                    "flash_decode plan")
         num_splits = ns.value
     else:

@@ -38,7 +38,7 @@ _DTYPE_CODES = {"float32": 0, "fp32": 0, "float": 0, "float16": 1, "fp16": 1, "h
 
 # sk_kernel_config ops and cfg slots (include/sk_attn.h).
 _OP_FWD, _OP_BWD_DKV, _OP_BWD_DQ, _OP_DECODE, _OP_DECODE_COMBINE = 0, 1, 2, 3, 4
-_VARIANT_PAGED, _VARIANT_ROPE = 1, 2
+_VARIANT_PAGED, _VARIANT_ROPE, _VARIANT_VARLEN = 1, 2, 4
 _SLOTS = ("grid", "threads", "block_m", "block_n", "stages", "head_dim", "splits", "paired",
           "workspace_bytes", "keys_per_split", "lds_bytes", "vgprs", "wg_per_cu", "chunks")
 
@@ -134,7 +134,8 @@ def pick(
     ``cache`` is accepted for call compatibility: the kernels' tiles are
     compiled in, so there is no tuned-configuration cache to consult.
     ``kwargs``: ``kv_len``, ``num_kv_heads``, ``is_causal``, ``paged``,
-    ``rope`` (decode / forward variants).
+    ``rope`` (decode / forward variants), ``varlen`` (decode with per-row
+    cache lengths: its split plan).
     """
     op_name = str(op).strip().lower()
     if op_name not in _FWD_OPS + _BWD_OPS + _DECODE_OPS:
@@ -145,7 +146,8 @@ def pick(
     fingerprint = arch or prof.fingerprint()
     code = _dtype_code(dtype)
     prob = _problem(op_name, shape, kwargs)
-    variant = (_VARIANT_PAGED if kwargs.get("paged") else 0) | (_VARIANT_ROPE if kwargs.get("rope") else 0)
+    variant = ((_VARIANT_PAGED if kwargs.get("paged") else 0) | (_VARIANT_ROPE if kwargs.get("rope") else 0)
+               | (_VARIANT_VARLEN if kwargs.get("varlen") else 0))
     query = _device_query(prof)
     splits_req = int((override or {}).get("SPLIT_KV", kwargs.get("num_splits", 0)) or 0)
 

@@ -68,22 +68,25 @@ int check_ptr(const char* name, const void* p) {
 // the table sizes the split count to the workgroups the chip holds at once,
 // counted as eight waves per CU (16 query heads per wave: 1, 2 or 4 waves per
 // workgroup):
-// * groups of up to 16 heads (one-wave workgroups): about two rounds.  One
-//   round (C4: 4 splits) is 1.6% faster on uniform cache lengths but 6.5%
-//   slower with per-row lengths and paged pools, which take the same plan;
+// * groups of up to 16 heads (one-wave workgroups): one round with a
+//   uniform cache length (every split the same size; C4: 4 splits, 1.7%
+//   faster than two rounds), about two rounds with per-row lengths and over
+//   paged pools (per_row), whose rows spread their keys over their splits so
+//   a row shorter than the longest leaves a one-round grid uneven (8
+//   splits: 6.9% and 7.7% faster than 4 at the C4 shape with lengths U[1, Sk]);
 // * 32- and 64-head groups: exactly one round, so no split waits for a second
 //   round; a 64-head group writes 32 KB of partials per split, so fewer,
 //   longer splits also keep that traffic small (C5: 64 splits; 32 and 128
 //   splits measured 15% and 10% slower).
 // Every split keeps at least 256 keys (8 tiles) and the count is capped at
 // 1024 (the combine kernel's LDS weight array).
-int plan_splits(int B, int Hq, int Hkv, int Sk, int D) {
+int plan_splits(int B, int Hq, int Hkv, int Sk, int D, bool per_row) {
   (void)D;
   if (Sk <= 0 || B <= 0 || Hkv <= 0) return 1;
   const int group = Hq / Hkv;
   const int waves = group <= 16 ? 1 : group <= 32 ? 2 : 4;
   int64_t slots = 256LL * 8 / waves;
-  const int rounds = group <= 16 ? 2 : 1;
+  const int rounds = group <= 16 && per_row ? 2 : 1;
 #if SK_DEC_RING_STAGES
   // study build: the LDS-ring candidate holds 160 KB / ring bytes workgroups per CU
   const int dpad = sk::padded_head_dim(D);
@@ -201,10 +204,10 @@ static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, i
 
 // Split count and keys per split of a decode call (num_splits 0: the gfx950
 // table's pick).  fp32 decode runs unsplit.
-static int decode_splits(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,
+static int decode_splits(int dtype, int B, int Hq, int Hkv, int Sk, int D, bool per_row, int num_splits,
                          int* splits, int* kps) {
   if (dtype == SK_F32) num_splits = 1;
-  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk, D);
+  if (num_splits == 0) num_splits = plan_splits(B, Hq, Hkv, Sk, D, per_row);
   if (num_splits < 1 || num_splits > 1024)
     return fail(SK_EINVAL, "num_splits=%d outside [1, 1024]", num_splits);
   *kps = keys_per_split_for(Sk, num_splits);
@@ -365,17 +368,28 @@ int sk_attn_bwd(int dtype, const void* dout, const void* q, const void* k, const
   return SK_OK;
 }
 
-int sk_decode_plan(int dtype, int B, int Hq, int Hkv, int Sk, int D, int* num_splits,
-                   size_t* workspace_bytes) {
-  g_err[0] = 0;
+static int decode_plan_impl(int dtype, int B, int Hq, int Hkv, int Sk, int D, bool per_row,
+                            int* num_splits, size_t* workspace_bytes) {
   int rc = check_dims(dtype, B, Hq, Hkv, 1, Sk, D);
   if (rc) return rc;
   if (!num_splits || !workspace_bytes) return fail(SK_EINVAL, "output pointer is NULL");
-  int splits = dtype == SK_F32 ? 1 : plan_splits(B, Hq, Hkv, Sk, D);
+  int splits = dtype == SK_F32 ? 1 : plan_splits(B, Hq, Hkv, Sk, D, per_row);
   if (splits > 1) splits = (Sk + keys_per_split_for(Sk, splits) - 1) / keys_per_split_for(Sk, splits);
   *num_splits = splits;
   *workspace_bytes = decode_ws_bytes(dtype, B, Hq, D, splits);
   return SK_OK;
+}
+
+int sk_decode_plan(int dtype, int B, int Hq, int Hkv, int Sk, int D, int* num_splits,
+                   size_t* workspace_bytes) {
+  g_err[0] = 0;
+  return decode_plan_impl(dtype, B, Hq, Hkv, Sk, D, false, num_splits, workspace_bytes);
+}
+
+int sk_decode_plan_varlen(int dtype, int B, int Hq, int Hkv, int Sk, int D, int* num_splits,
+                          size_t* workspace_bytes) {
+  g_err[0] = 0;
+  return decode_plan_impl(dtype, B, Hq, Hkv, Sk, D, true, num_splits, workspace_bytes);
 }
 
 int sk_decode_workspace(int dtype, int B, int Hq, int Hkv, int Sk, int D, int num_splits,
@@ -436,7 +450,9 @@ static int decode_impl(int dtype, const void* q, const void* k, const void* v, v
     return fail(SK_EUNSUPPORTED, "decode supports up to 64 query heads per KV head, got %d", Hq / Hkv);
 
   int kps = 0;
-  if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &num_splits, &kps))) return rc;
+  if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, seqlens != nullptr, num_splits, &num_splits,
+                          &kps)))
+    return rc;
   const size_t need = decode_ws_bytes(dtype, B, Hq, D, num_splits);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(SK_EWORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, need);
@@ -569,10 +585,10 @@ int sk_decode_noalloc(int dtype, const void* q, const void* k, const void* v, vo
     // the table's split count, lowered until the partials fit the scratch
     const size_t per_split = (size_t)B * Hq * (sk::padded_head_dim(D) + 1) * sizeof(float);
     const int64_t fit = std::max<int64_t>(1, (int64_t)(kBytes / per_split));
-    num_splits = (int)std::min<int64_t>(plan_splits(B, Hq, Hkv, Sk, D), fit);
+    num_splits = (int)std::min<int64_t>(plan_splits(B, Hq, Hkv, Sk, D, false), fit);
   }
   int splits = 0, kps = 0;
-  if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &splits, &kps))) return rc;
+  if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, false, num_splits, &splits, &kps))) return rc;
   const size_t need = decode_ws_bytes(dtype, B, Hq, D, splits);
   if (need > kBytes)
     return fail(SK_EWORKSPACE,
@@ -875,7 +891,8 @@ int sk_kernel_config(int op, int dtype, int B, int Hq, int Hkv, int Sq, int Sk, 
     ws = bwd_ws_bytes(dtype, B, Hq, Hkv, Sq, Sk, D, is_causal != 0);
   } else if (decode) {
     int ns = 0, per = 0;
-    if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, num_splits, &ns, &per))) return rc;
+    const bool per_row = (variant & (SK_VARIANT_PAGED | SK_VARIANT_VARLEN)) != 0;
+    if ((rc = decode_splits(dtype, B, Hq, Hkv, Sk, D, per_row, num_splits, &ns, &per))) return rc;
     sk::DecParams p{};
     p.B = B, p.Hq = Hq, p.Hkv = Hkv, p.Sk = Sk, p.D = D, p.group = Hq / Hkv;
     p.num_splits = ns, p.keys_per_split = per, p.dpad = sk::padded_head_dim(D);

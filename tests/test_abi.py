@@ -30,7 +30,8 @@ def header_functions():
 def test_header_declares_expected_api():
     names = set(header_functions())
     assert {"sk_abi_version", "sk_last_error", "sk_attn_fwd", "sk_attn_bwd",
-            "sk_attn_bwd_workspace", "sk_attn_bwd_workspace_min", "sk_decode_plan", "sk_decode",
+            "sk_attn_bwd_workspace", "sk_attn_bwd_workspace_min", "sk_decode_plan",
+            "sk_decode_plan_varlen", "sk_rope_rotate", "sk_decode",
             "sk_decode_workspace",
             "sk_decode_varlen", "sk_kv_cache_update", "sk_decode_paged",
             "sk_kv_cache_update_paged", "sk_attn_fwd_rope", "sk_decode_rope",
@@ -91,12 +92,23 @@ def test_decode_plan_table(lib):
     assert lib.sk_decode_plan(2, 64, 32, 8, 32768, 128, ctypes.byref(ns), ctypes.byref(nb)) == 0
     assert 1 < ns.value <= 1024
     assert nb.value == 64 * 32 * ns.value * (128 + 1) * 4
+    # uniform length: one round of one-wave workgroups (256 CUs x 8 / 512 (b, h_kv) units = 4);
+    # per-row lengths / paged pools: about two rounds (8)
+    assert ns.value == 4
+    assert lib.sk_decode_plan_varlen(2, 64, 32, 8, 32768, 128, ctypes.byref(ns),
+                                     ctypes.byref(nb)) == 0
+    assert ns.value == 8 and nb.value == 64 * 32 * 8 * (128 + 1) * 4
     # small cache: one split, no scratch
     assert lib.sk_decode_plan(2, 2, 8, 2, 32, 64, ctypes.byref(ns), ctypes.byref(nb)) == 0
     assert ns.value == 1 and nb.value == 0
     # C5: fp16 MQA B=8 Hq=64 Hkv=1 Sk=131072
     assert lib.sk_decode_plan(1, 8, 64, 1, 131072, 128, ctypes.byref(ns), ctypes.byref(nb)) == 0
     assert ns.value >= 64
+    # groups above 16 heads: one round in both plans
+    c5 = ns.value
+    assert lib.sk_decode_plan_varlen(1, 8, 64, 1, 131072, 128, ctypes.byref(ns),
+                                     ctypes.byref(nb)) == 0
+    assert ns.value == c5
 
 
 def test_decode_argument_errors(lib):

@@ -92,6 +92,14 @@ def test_pick_decode_matches_the_launch_plan():
     assert cfg["kernel_variant"] == "decode_split_kernel" and cfg["num_warps"] == 1
     assert cfg["grid"] == ns * 64 * 8
     assert cfg["combine"]["grid"] == 64 * 32
+    # per-row lengths (and paged pools): the varlen plan
+    vl = pick("flash_decode", (64, 32, 1, 128), dtype="bfloat16", kv_len=32768, num_kv_heads=8,
+              varlen=True)
+    assert vl["SPLIT_KV"] == plan(__import__("torch").bfloat16, 64, 32, 8, 32768, 128,
+                                  per_row=True)[0] == 2 * cfg["SPLIT_KV"]
+    pg = pick("flash_decode", (64, 32, 1, 128), dtype="bfloat16", kv_len=32768, num_kv_heads=8,
+              paged=True)
+    assert pg["SPLIT_KV"] == vl["SPLIT_KV"]
     # MQA C5: four waves per workgroup share each tile; one round of 64 splits
     c5 = pick("flash_decode", (8, 64, 1, 128), dtype="float16", kv_len=131072, num_kv_heads=1)
     assert c5["kernel_variant"] == "decode_split_kernel" and c5["num_warps"] == 4
@@ -244,6 +252,8 @@ def test_layout_and_workspace():
     assert [layout.padded_head_dim(d) for d in (16, 64, 80, 96, 128, 200, 256, 300)] == \
         [64, 64, 96, 96, 128, 256, 256, 0]
     ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu")
+    assert ns == 4 and ws.numel() == 64 * 32 * 4 * (128 + 1) * 4
+    ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu", per_row=True)
     assert ns == 8 and ws.numel() == 64 * 32 * 8 * (128 + 1) * 4
     ws, ns = workspace.decode_workspace(torch.bfloat16, 64, 32, 8, 32768, 128, "cpu", num_splits=4)
     assert ns == 4 and ws.numel() == 64 * 32 * 4 * (128 + 1) * 4
