@@ -8,8 +8,8 @@
 // * One workgroup per (batch, KV head, key split) serves every query head of
 //   that KV head's group, so each K/V byte is read from HBM once per call
 //   (the reference reads it once per query head).  The group's heads are the
-//   16-wide column dimension of v_mfma_f32_16x16x32: S^T = K Q^T for 32 keys
-//   at a time, then O^T += V^T P^T with V^T read transposed from LDS by
+//   16-wide column dimension of v_mfma_f32_16x16x32: S^T = K Q^T for a tile
+//   of 32 or 64 keys, then O^T += V^T P^T with V^T read transposed from LDS by
 //   ds_read_b64_tr_b16.  Up to 16 heads per wave; a group of 32 or 64 heads
 //   (MQA) runs 2 or 4 waves that share each K/V tile.
 // * K/V tiles arrive through fully coalesced 16-byte loads (a 64-lane load
@@ -25,16 +25,16 @@
 
 namespace sk {
 
-template <int DP>
+template <int DP, int BN = 32>
 struct DecTile {
-  static constexpr int kBN = 32;                      // keys per tile
+  static constexpr int kBN = BN;                      // keys per tile
   static constexpr int kStride = DP + 16;             // 16-bit words per LDS row
   static constexpr int kWords = kBN * kStride;
   static constexpr int kChunksPerRow = DP / 8;
   static constexpr int kChunks = kBN * kChunksPerRow;
 };
 
-// Rows of the 32-key tile that starts at key n0 of batch row b (a tile never
+// Rows of the tile that starts at key n0 of batch row b (a tile never
 // straddles a page): contiguous caches, or the tile's page of a paged cache.
 // ok is false when the page index lies outside the pool; such a tile reads as
 // zeros and its keys are masked.
@@ -132,10 +132,29 @@ __device__ __forceinline__ void load_q(const DecParams& p, int b, int hq, bool h
   }
 }
 
+// Keys per tile of decode_split_kernel.  The four-wave kernel (groups of 33
+// to 64 query heads, MQA) takes 64 keys per barrier pair: each tile's serial
+// chain (LDS store, barrier, score MFMAs, row maximum, exp2, output MFMAs,
+// barrier) has a fixed latency that 64 keys amortise over twice the bytes,
+// which made the C5 decode 3-10% faster and a 48-head group 3.5% faster.
+// 32 keys elsewhere: with two waves the 64-key staging takes the kernel from
+// 148 to 208 VGPRs and measured 3% slower (groups of 32), one-wave
+// workgroups gained nothing (C4), a page of a paged pool may hold only 32
+// keys, and the D = 256 tile is already twice the bytes.
+// (SK_DEC_BN_W4=32 builds the 32-key candidate of the tile study.)
+#ifndef SK_DEC_BN_W4
+#define SK_DEC_BN_W4 64
+#endif
+template <int DP, int NWH, bool PAGED>
+constexpr int dec_split_bn() {
+  return NWH == 4 && !PAGED && DP <= 128 ? SK_DEC_BN_W4 : 32;
+}
+
 template <class T, int DP, int NWH, bool PAGED>
 __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
-  using Tile = DecTile<DP>;
-  constexpr int BN = Tile::kBN;
+  constexpr int BN = dec_split_bn<DP, NWH, PAGED>();
+  using Tile = DecTile<DP, BN>;
+  constexpr int NKB = BN / 16;  // 16-key blocks of S^T per tile
   constexpr int NT = NWH * 64;
   constexpr int LOADS = (Tile::kChunks + NT - 1) / NT;
   constexpr bool kRagged = Tile::kChunks % NT != 0;  // last round covers part of the tile
@@ -241,9 +260,9 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
     if (t + 1 < n_tiles) load_tile(t + 1, pg_nxt);
     const int n0 = k_lo + t * BN;
 
-    f32x4 sacc[2];
+    f32x4 sacc[NKB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb) {
       sacc[kb] = f32x4{};
 #pragma unroll
       for (int s = 0; s < KD; ++s) {
@@ -260,13 +279,16 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
     }
     if (!tile_ok || n0 + BN > k_hi) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (!tile_ok || n0 + 16 * kb + 4 * g + r >= k_hi) sacc[kb][r] = kNegInf;
     }
     float mt = fmaxf(fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3])),
                      fmaxf(fmaxf(sacc[1][0], sacc[1][1]), fmaxf(sacc[1][2], sacc[1][3])));
+#pragma unroll
+    for (int kb = 2; kb < NKB; ++kb)
+      mt = fmaxf(mt, fmaxf(fmaxf(sacc[kb][0], sacc[kb][1]), fmaxf(sacc[kb][2], sacc[kb][3])));
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = xhalf_max(mt);
     const float m_new = fmaxf(m_run, mt);
@@ -274,22 +296,29 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
     const float alpha = fast_exp2((m_run - m_sub) * p.scale_log2);
     const float neg_m = -m_sub * p.scale_log2;
     m_run = m_new;
-    float e[8];
+    float e[4 * NKB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      e[j] = fast_exp2(fmaf(sacc[0][j], p.scale_log2, neg_m));
-      e[4 + j] = fast_exp2(fmaf(sacc[1][j], p.scale_log2, neg_m));
-    }
-    l_run = l_run * alpha + ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-    const u32x4 pk = {pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
-                      pack2<T>(e[6], e[7])};
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-    for (int c = 0; c < DB; ++c) {
-      const uint16_t* vp = vs + v_off + 16 * c;
-      const u32x2 lo = lds_read_tr(vp);
-      const u32x2 hi = lds_read_tr(vp + 16 * Tile::kStride);
-      const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-      oacc[c] = mfma16<T>(a, pk, oacc[c] * alpha);
+      for (int j = 0; j < 4; ++j) e[4 * kb + j] = fast_exp2(fmaf(sacc[kb][j], p.scale_log2, neg_m));
+    l_run *= alpha;
+#pragma unroll
+    for (int j = 0; j < 4 * NKB; j += 4) l_run += (e[j] + e[j + 1]) + (e[j + 2] + e[j + 3]);
+    // O^T += V^T P^T, one 32-key k-step per 32 keys of the tile; the
+    // rescale by alpha rides on the first.
+#pragma unroll
+    for (int s2 = 0; s2 < BN / 32; ++s2) {
+      const float* es = e + 8 * s2;
+      const u32x4 pk = {pack2<T>(es[0], es[1]), pack2<T>(es[2], es[3]), pack2<T>(es[4], es[5]),
+                        pack2<T>(es[6], es[7])};
+#pragma unroll
+      for (int c = 0; c < DB; ++c) {
+        const uint16_t* vp = vs + v_off + 16 * c + 32 * s2 * Tile::kStride;
+        const u32x2 lo = lds_read_tr(vp);
+        const u32x2 hi = lds_read_tr(vp + 16 * Tile::kStride);
+        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+        oacc[c] = mfma16<T>(a, pk, s2 == 0 ? oacc[c] * alpha : oacc[c]);
+      }
     }
     __syncthreads();
   }
@@ -620,7 +649,6 @@ static KernelPlan plan_decode_dp(const DecParams& p) {
   k.grid = dim3((unsigned)p.num_splits, (unsigned)(p.B * p.Hkv));
   k.elem = T::code;
   k.head_dim = DP;
-  k.block_n = 32;
   k.paged = PAGED;
   k.rope = p.rope.cos != nullptr;
   int nwh = 0;
@@ -648,6 +676,8 @@ static KernelPlan plan_decode_dp(const DecParams& p) {
 #endif
   k.block = dim3(64 * nwh);
   k.block_m = 16 * nwh;
+  k.block_n = nwh == 1 ? dec_split_bn<DP, 1, PAGED>()
+                       : nwh == 2 ? dec_split_bn<DP, 2, PAGED>() : dec_split_bn<DP, 4, PAGED>();
   return k;
 }
 

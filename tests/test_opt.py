@@ -104,6 +104,11 @@ def test_pick_decode_matches_the_launch_plan():
     c5 = pick("flash_decode", (8, 64, 1, 128), dtype="float16", kv_len=131072, num_kv_heads=1)
     assert c5["kernel_variant"] == "decode_split_kernel" and c5["num_warps"] == 4
     assert c5["SPLIT_KV"] == 64 and c5["grid"] == 64 * 8
+    # 64-key tiles for the multi-wave kernel, 32 for one-wave workgroups and paged pools
+    assert c5["BLOCK_N"] == 64 and cfg["BLOCK_N"] == 32
+    c5p = pick("flash_decode", (8, 64, 1, 128), dtype="float16", kv_len=131072, num_kv_heads=1,
+               paged=True)
+    assert c5p["BLOCK_N"] == 32 and c5p["num_warps"] == 4
     # short cache: one split, no combine pass
     one = pick("flash_decode", (2, 8, 1, 64), kv_len=100, num_kv_heads=2)
     assert one["SPLIT_KV"] == 1 and "combine" not in one and one["workspace_bytes"] == 0

@@ -31,8 +31,9 @@ def test_device_profile_is_mi355x():
     ("flash_attn", (1, 32, 16384, 64), dict(dtype="float16", is_causal=True), 65536, 1),
     ("flash_decode", (64, 32, 1, 128), dict(dtype="bfloat16", kv_len=32768, num_kv_heads=8),
      None, 8),
+    # C5: 64-key K and V tiles (2 x 18 KiB); the 512 workgroups run two per CU
     ("flash_decode", (8, 64, 1, 128), dict(dtype="float16", kv_len=131072, num_kv_heads=1),
-     18432, 3),
+     36864, 2),
 ])
 def test_reported_occupancy_matches_the_table(op, shape, kw, lds, per_cu):
     cfg, text = pick(op, shape, explain=True, **kw)
