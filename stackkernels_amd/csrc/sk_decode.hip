@@ -587,6 +587,21 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecParams p) {
   const int hq = bh % p.Hq;
   const int ns = p.num_splits;
   const float* lse = p.part_lse + (int64_t)bh * ns;
+  const float* po = p.part_o + (int64_t)bh * ns * p.dpad;
+  const int sg = tid >> 5;        // split group 0..7: splits sg, sg + 8, ...
+  const int d4 = (tid & 31) * 4;  // head-dim quad
+
+  // The first 64 splits' partials of head-dim block 0 are loaded before the
+  // LSE pass, so their latency overlaps it (the weights are not needed to
+  // issue them).  Summation order is the same as without the prefetch.
+  constexpr int kPre = 8;
+  f32x4 pre[kPre];
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+    const int s = sg + 8 * k;
+    pre[k] = s < ns && d4 < p.D ? *reinterpret_cast<const f32x4*>(po + (int64_t)s * p.dpad + d4)
+                                : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   float mx = kNegInf;
   for (int s = tid; s < ns; s += 256) mx = fmaxf(mx, lse[s]);
@@ -608,16 +623,20 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecParams p) {
   den = (red[0][1] + red[1][1]) + (red[2][1] + red[3][1]);
   const float inv = den > 0.f ? 1.f / den : 0.f;
 
-  const float* po = p.part_o + (int64_t)bh * ns * p.dpad;
   uint16_t* op = (uint16_t*)p.o + b * p.o_sb + hq * p.o_sh;
-  const int sg = tid >> 5;         // split group 0..7
-  const int d4 = (tid & 31) * 4;   // head-dim quad
   for (int d0 = 0; d0 < p.D; d0 += 128) {
     const int d = d0 + d4;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (d < p.D)
-      for (int s = sg; s < ns; s += 8)
+    if (d < p.D) {
+      int s = sg;
+      if (d0 == 0) {
+#pragma unroll
+        for (int k = 0; k < kPre; ++k, s += 8)
+          if (s < ns) acc += w[s] * pre[k];
+      }
+      for (; s < ns; s += 8)
         acc += w[s] * *reinterpret_cast<const f32x4*>(po + (int64_t)s * p.dpad + d);
+    }
     *reinterpret_cast<f32x4*>(&part[sg][d4]) = acc;
     __syncthreads();
     if (tid < 64) {
