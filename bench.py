@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "fa9388dbc2bd0c71541fb099f987d6f91d4fa1b51f49264ced35e6b5cefc6ed1"
+TRAFFIC_SOURCES_SHA256 = "e9e05c6dcd03d32232510a82fcd308364ad8a2add668e31af18d9cc8fb8183a9"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 679_832_706,
-    "fwd_long": 847_654_650,
-    "fwdbwd": 4_552_900_127,
-    "decode": 8_612_473_677,
-    "decode_mqa": 573_007_102,
-    "decode_varlen": 4_305_218_702,
-    "kv_update": 67_240_134,
-    "decode_paged": 4_305_360_111,
-    "decode_rope": 8_612_484_943,
-    "kv_update_rope": 75_523_400,
-    "decode_step": 4_306_745_642,
+    "fwd": 682_278_263,
+    "fwd_long": 842_371_768,
+    "fwdbwd": 4_535_306_146,
+    "decode": 8_601_597_301,
+    "decode_mqa": 573_053_304,
+    "decode_varlen": 4_305_224_770,
+    "kv_update": 67_240_132,
+    "decode_paged": 4_305_376_485,
+    "decode_rope": 8_601_618_819,
+    "kv_update_rope": 75_523_347,
+    "decode_step": 4_306_761_910,
 }
 
 
