@@ -962,8 +962,10 @@ def gemm_calibration(steps: int, warmup: int, n: int = 8192) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # defaults: 10 untimed and 50 timed steps per loop, so every launch median
+    # is taken over 50 launches
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", choices=sorted(ALL_WORKLOADS) + ["copy", "gemm"], default="fwd",
                     help="headline workload (default fwd = C2); 'copy' times a plain 1 GiB "
                          "device copy, the calibration kernel for the HBM-traffic counters; "
