@@ -56,8 +56,7 @@ def _hipcc() -> str:
 # Kernels that stream tiles with buffer_load ... lds and count their own loads
 # with s_waitcnt vmcnt.  A register spill would add scratch loads to that
 # count, so the waits would no longer cover the tiles: such a build is refused.
-RING_KERNELS = ("fwd_mfma_kernel", "bwd_dkv_kernel", "bwd_dq_kernel", "bwd_dq_ds_kernel",
-                "decode_ring_kernel")
+RING_KERNELS = ("fwd_mfma_kernel", "bwd_dkv_kernel", "bwd_dq_kernel", "bwd_dq_ds_kernel")
 
 
 def _check_no_scratch(src: str, remarks: str) -> None:

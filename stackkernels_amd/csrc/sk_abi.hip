@@ -85,16 +85,8 @@ int plan_splits(int B, int Hq, int Hkv, int Sk, int D, bool per_row) {
   if (Sk <= 0 || B <= 0 || Hkv <= 0) return 1;
   const int group = Hq / Hkv;
   const int waves = group <= 16 ? 1 : group <= 32 ? 2 : 4;
-  int64_t slots = 256LL * 8 / waves;
+  const int64_t slots = 256LL * 8 / waves;
   const int rounds = group <= 16 && per_row ? 2 : 1;
-#if SK_DEC_RING_STAGES
-  // study build: the LDS-ring candidate holds 160 KB / ring bytes workgroups per CU
-  const int dpad = sk::padded_head_dim(D);
-  if (group > 16 && (dpad == 64 || dpad == 128 || dpad == 256)) {
-    const int ring = (dpad == 256 ? 2 : SK_DEC_RING_STAGES) * 2 * 32 * dpad * 2;
-    slots = 256LL * std::min(160 * 1024 / ring, 16 / waves);
-  }
-#endif
   const int64_t units = (int64_t)B * Hkv;
   int64_t splits = (rounds * slots + units - 1) / units;
   splits = std::min<int64_t>(splits, std::max(1, Sk / 256));

@@ -350,226 +350,6 @@ __global__ void __launch_bounds__(NWH * 64) decode_split_kernel(DecParams p) {
   }
 }
 
-// Candidate of the decode tile study, not part of the gfx950 table: the
-// large-group split kernel with its K/V tiles brought by buffer_load ... lds
-// into a SK_DEC_RING_STAGES-deep LDS ring instead of register staging.
-// Compiled only for a study build (-DSK_DEC_RING_STAGES=3, 5 or 8); it
-// measured 5-10% slower than decode_split_kernel at C5.
-#ifndef SK_DEC_RING_STAGES
-#define SK_DEC_RING_STAGES 0
-#endif
-#if SK_DEC_RING_STAGES
-// Split kernel for large groups (32 or 64 query heads per KV head, MQA):
-// the same math as decode_split_kernel, with the K/V stream driven by
-// direct-to-LDS buffer loads into a STAGES-deep ring (no register staging,
-// so each workgroup keeps STAGES-1 tiles of 16 KiB in flight; HBM streaming
-// needs ~100 KB in flight per CU).  Unpadded tiles with 16-byte-chunk XOR
-// swizzles for the 64-bank LDS: K rows c ^ (r % 16) (16-lane 16-byte reads
-// of 16 rows), V rows c ^ 2 (r % 8) (32-lane transposed reads of 8 rows x
-// 2 chunks).
-template <int DP>
-__device__ __forceinline__ int dec_swz_k(int r) {
-  return DP == 64 ? (r >> 1) & 7 : r & 15;
-}
-template <int DP>
-__device__ __forceinline__ int dec_swz_v(int r) {
-  return DP == 64 ? 2 * ((r >> 1) & 3) : 2 * (r & 7);
-}
-
-template <class T, int DP, int NWH, int STAGES, bool PAGED>
-__global__ void __launch_bounds__(NWH * 64) decode_ring_kernel(DecParams p) {
-  constexpr int BN = 32;                  // keys per tile
-  constexpr int CPR = DP / 8;             // 16-byte chunks per row
-  constexpr int ROWB = DP * 2;
-  constexpr int TILEB = BN * ROWB;        // one K or V tile
-  constexpr int STAGEB = 2 * TILEB;
-  constexpr int SEGROWS = 1024 / ROWB;    // rows per 1 KiB load segment
-  constexpr int SEGS = TILEB / 1024;      // segments per K (or V) tile
-  constexpr int LW = (SEGS + NWH - 1) / NWH;  // segment slots per wave
-  constexpr int KD = DP / 32;             // k-steps over the head dim (S^T)
-  constexpr int DB = DP / 16;             // 16-wide head-dim blocks of O^T
-  static_assert(STAGES >= 2 && STAGES <= 8, "2 to 8 stages");
-
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGEB];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c16 = lane & 15;
-  const int g = lane >> 4;
-
-  const int split = blockIdx.x;
-  const int bk = blockIdx.y;
-  const int b = p.longest_first ? row_of_rank(p, bk / p.Hkv) : bk / p.Hkv;
-  const int hkv = bk % p.Hkv;
-  // Keys this row sees: all S_k, or its cache length.  With per-row lengths
-  // the row's keys are spread over all its splits (32-key multiples), so a
-  // short row does not leave most of its workgroups empty.
-  const int sk_b =
-      p.seqlens ? min(max(__builtin_amdgcn_readfirstlane(p.seqlens[b]), 0), p.Sk) : p.Sk;
-  const int kps = p.seqlens ? max(32, ((sk_b + p.num_splits - 1) / p.num_splits + 31) / 32 * 32)
-                            : p.keys_per_split;
-  const int k_lo = split * kps;
-  const int k_hi = min(sk_b, k_lo + kps);
-  const int n_tiles = k_hi > k_lo ? (k_hi - k_lo + BN - 1) / BN : 0;
-
-  const int hd = 16 * wave + c16;  // head within the group for this lane's column
-  const bool head_ok = hd < p.group;
-  const int hq = hkv * p.group + (head_ok ? hd : 0);
-
-  const uint16_t* kbase = (const uint16_t*)p.k + b * p.k_sb + hkv * p.k_sh;
-  const uint16_t* vbase = (const uint16_t*)p.v + b * p.v_sb + hkv * p.v_sh;
-
-  u32x4 qreg[KD];
-  load_q<T>(p, b, hq, head_ok, g, qreg);
-
-  // Per-lane byte offsets of this wave's load segments (tile-relative).
-  uint32_t koff[LW], voff[LW];
-#pragma unroll
-  for (int j = 0; j < LW; ++j) {
-    const int seg = wave + j * NWH;
-    const int r = seg * SEGROWS + lane / CPR;
-    const int pc = lane % CPR;
-    const int kc = pc ^ dec_swz_k<DP>(r);
-    const int vc = pc ^ dec_swz_v<DP>(r);
-    koff[j] = kc * 8 < p.D ? (uint32_t)((r * p.k_ss + kc * 8) * 2) : kBufferOob;
-    voff[j] = vc * 8 < p.D ? (uint32_t)((r * p.v_ss + vc * 8) * 2) : kBufferOob;
-  }
-  // Paged: bit t % 32 of page_ok records whether tile t's page lies in the
-  // pool, set when the tile is issued (STAGES - 1 tiles ahead), so the tile
-  // loop does not read the block table again.
-  uint32_t page_ok = 0;
-  auto issue_tile = [&](int t) {
-    const int n0 = k_lo + t * BN;
-    const TileRows tr = tile_rows<PAGED>(p, kbase, vbase, b, hkv, n0);
-    if (PAGED) page_ok = (page_ok & ~(1u << (t & 31))) | ((uint32_t)tr.ok << (t & 31));
-    const int rows = tr.ok ? min(BN, k_hi - n0) : 0;
-    // (The paged row pointers come from a table load; readfirstlane states
-    // what is true -- they are wave-uniform -- so the DMA resources stay
-    // scalar.)
-    const i32x4 kr = uniform_words(make_rsrc_words(tr.k, tile_bytes(rows, p.k_ss, p.D)));
-    const i32x4 vr = uniform_words(make_rsrc_words(tr.v, tile_bytes(rows, p.v_ss, p.D)));
-    const uint32_t st = lds_addr(smem) + (t % STAGES) * STAGEB;
-#pragma unroll
-    for (int j = 0; j < LW; ++j) {
-      const int seg = wave + j * NWH;
-      buffer_load_lds_b128(kr, st + seg * 1024, koff[j]);
-      buffer_load_lds_b128(vr, st + TILEB + seg * 1024, voff[j]);
-    }
-  };
-  static_assert(SEGS % NWH == 0, "every wave issues the same number of loads");
-  constexpr int kLoads = 2 * SEGS / NWH;  // DMA instructions per wave per tile
-
-#pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t)
-    if (t < n_tiles) issue_tile(t);
-
-  // Lane-constant LDS offsets: K operand of k-step s (16x16x32 A operand):
-  // row c16 (+16 kb), chunk 4s + g.  V^T operand of head-dim block c: rows
-  // 4g + c16/4 (+16 for the upper half, same swizzle), chunk 2c + (c16%4)/2,
-  // 8-byte half c16%2.
-  int k_lds[KD];
-#pragma unroll
-  for (int s = 0; s < KD; ++s) k_lds[s] = c16 * ROWB + (((4 * s + g) ^ dec_swz_k<DP>(c16)) * 16);
-  const int vrow = 4 * g + c16 / 4;
-  const int v_base = TILEB + vrow * ROWB + 8 * (c16 & 1);
-  const int v_sw = dec_swz_v<DP>(vrow);
-  const int v_g = (c16 & 3) / 2;
-
-  f32x4 oacc[DB];
-#pragma unroll
-  for (int c = 0; c < DB; ++c) oacc[c] = f32x4{};
-  float m_run = kNegInf;
-  float l_run = 0.f;
-
-  for (int t = 0; t < n_tiles; ++t) {
-    // Tile t landed (this wave's segments, then everyone's); the barrier also
-    // retires all reads of the stage refilled next (it held tile t-1).
-    wait_tiles<kLoads, STAGES - 2>(min(STAGES - 2, n_tiles - 1 - t));
-    __syncthreads();
-    if (t + STAGES - 1 < n_tiles) issue_tile(t + STAGES - 1);
-    const uint8_t* st = smem + (t % STAGES) * STAGEB;
-    const int n0 = k_lo + t * BN;
-
-    // S^T = K Q^T: sacc[kb][r] = S^T[key n0 + 16 kb + 4 g + r][head column c16].
-    f32x4 sacc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f32x4{};
-#pragma unroll
-      for (int s = 0; s < KD; ++s) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(st + k_lds[s] + kb * 16 * ROWB);
-        sacc[kb] = mfma16<T>(a, qreg[s], sacc[kb]);
-      }
-    }
-    const bool tile_ok = !PAGED || ((page_ok >> (t & 31)) & 1u);
-    if (!tile_ok || n0 + BN > k_hi) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (!tile_ok || n0 + 16 * kb + 4 * g + r >= k_hi) sacc[kb][r] = kNegInf;
-    }
-    float mt = fmaxf(fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3])),
-                     fmaxf(fmaxf(sacc[1][0], sacc[1][1]), fmaxf(sacc[1][2], sacc[1][3])));
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = xhalf_max(mt);
-    // Lazy rescaling (offset moves only when a score exceeds it by 2^8).
-    const bool grow = (mt - m_run) * p.scale_log2 > kRescaleLog2;
-    if (__any(grow)) {
-      const float alpha = grow ? fast_exp2((m_run - mt) * p.scale_log2) : 1.f;
-      m_run = grow ? mt : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int c = 0; c < DB; ++c) oacc[c] *= alpha;
-    }
-    const float neg_m = (m_run == kNegInf) ? 0.f : -m_run * p.scale_log2;
-    float e[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      e[j] = fast_exp2(fmaf(sacc[0][j], p.scale_log2, neg_m));
-      e[4 + j] = fast_exp2(fmaf(sacc[1][j], p.scale_log2, neg_m));
-    }
-    l_run += ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-    const u32x4 pk = {pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
-                      pack2<T>(e[6], e[7])};
-#pragma unroll
-    for (int c = 0; c < DB; ++c) {
-      const uint8_t* vp = st + v_base + (((2 * c + v_g) ^ v_sw) * 16);
-      const u32x2 lo = lds_read_tr((const uint16_t*)vp);
-      const u32x2 hi = lds_read_tr((const uint16_t*)(vp + 16 * ROWB));
-      oacc[c] = mfma16<T>(__builtin_shufflevector(lo, hi, 0, 1, 2, 3), pk, oacc[c]);
-    }
-  }
-
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot = xhalf_sum(l_tot);
-  if (!head_ok) return;
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (p.num_splits == 1) {
-    uint16_t* op = (uint16_t*)p.o + b * p.o_sb + hq * p.o_sh;
-#pragma unroll
-    for (int c = 0; c < DB; ++c) {
-      const int d = 16 * c + 4 * g;
-      if (d < p.D) {
-        const u32x2 w = {pack2<T>(oacc[c][0] * inv, oacc[c][1] * inv),
-                         pack2<T>(oacc[c][2] * inv, oacc[c][3] * inv)};
-        *reinterpret_cast<u32x2*>(op + d) = w;
-      }
-    }
-  } else {
-    const int64_t row = ((int64_t)b * p.Hq + hq) * p.num_splits + split;
-    float* po = p.part_o + row * p.dpad;
-#pragma unroll
-    for (int c = 0; c < DB; ++c) {
-      const int d = 16 * c + 4 * g;
-      *reinterpret_cast<f32x4*>(po + d) = oacc[c] * inv;
-    }
-    if (g == 0) p.part_lse[row] = l_tot > 0.f ? m_run * p.scale + __logf(l_tot) : kNegInf;
-  }
-}
-
-#endif  // SK_DEC_RING_STAGES
-
 // Merge split partials: one 256-thread workgroup per (batch, query head).
 // Split weights exp(LSE_s - max) go to LDS; then 8 groups of 32 lanes each
 // sum a strided subset of the splits with 16-byte loads (4 head-dim values
@@ -660,8 +440,7 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecParams p) {
 // every group size, with 1, 2 or 4 waves per workgroup (16 query heads per
 // wave) sharing each K/V tile through LDS.  An LDS-ring variant (tiles by
 // buffer_load ... lds, 3 to 8 stages of 16 KB) measured 5-10% slower at C5
-// (MQA, 64 heads) with the same bytes in flight per CU; it is kept only as
-// a study candidate (SK_DEC_RING_STAGES above).
+// (MQA, 64 heads) with the same bytes in flight per CU.
 template <class T, int DP, bool PAGED>
 static KernelPlan plan_decode_dp(const DecParams& p) {
   KernelPlan k;
@@ -685,14 +464,6 @@ static KernelPlan plan_decode_dp(const DecParams& p) {
   }
   k.kernel = "decode_split_kernel";
   k.stages = 0;
-#if SK_DEC_RING_STAGES
-  if constexpr (DP == 64 || DP == 128 || DP == 256) {
-    constexpr int kStages = DP == 256 ? 2 : SK_DEC_RING_STAGES;
-    if (nwh == 2) k.fn = (const void*)decode_ring_kernel<T, DP, 2, kStages, PAGED>;
-    if (nwh == 4) k.fn = (const void*)decode_ring_kernel<T, DP, 4, kStages, PAGED>;
-    if (nwh > 1) k.kernel = "decode_ring_kernel", k.stages = kStages;
-  }
-#endif
   k.block = dim3(64 * nwh);
   k.block_m = 16 * nwh;
   k.block_n = nwh == 1 ? dec_split_bn<DP, 1, PAGED>()
