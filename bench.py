@@ -85,7 +85,7 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "e9e05c6dcd03d32232510a82fcd308364ad8a2add668e31af18d9cc8fb8183a9"
+TRAFFIC_SOURCES_SHA256 = "c718559f5103f328f13a8841467e0a7941071f229c40d33aad8752b250223eec"
 HBM_TRAFFIC_BYTES = {
     "fwd": 682_278_263,
     "fwd_long": 842_371_768,

@@ -62,20 +62,10 @@
 #ifndef SK_DQ_XL
 #define SK_DQ_XL 4
 #endif
-// dK/dV pipelined schedule: statistics broadcast by DPP (1) or read per lane (0).
-#ifndef SK_BWD_STAT_DPP
-#define SK_BWD_STAT_DPP 0
-#endif
-// dK/dV pipelined schedule: first row operands of a step read before its
-// barrier (1) or after it (0).
-#ifndef SK_BWD_DKV_PRELOAD
-#define SK_BWD_DKV_PRELOAD 1
-#endif
 // dK/dV ring depth at D = 128: 6 (pipelined schedule) or 4.
 #ifndef SK_BWD_DKV_STAGES
 #define SK_BWD_DKV_STAGES 6
 #endif
-// Key blocks of 32 per dK/dV wave in the 6-deep schedule: 2 or 1.
 // The D = 64 dK/dV ring: 6 (the pipelined schedule, the table), or 4 for the
 // one-tile-per-step schedule in a tile-study build.  Against 4, bit-identical:
 // C3 shape at D = 64 9.9% faster, causal MHA S = 8192 7.1%, causal S = 2048
@@ -89,6 +79,8 @@
 #ifndef SK_BWD_DKV_DO_D256
 #define SK_BWD_DKV_DO_D256 128
 #endif
+// Key blocks of 32 per dK/dV wave in the 6-deep schedule: 1, or 2 in a
+// tile-study build.
 #ifndef SK_BWD_DKV_KB
 #define SK_BWD_DKV_KB 1
 #endif
@@ -331,12 +323,6 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // key group's P blocks (block kb at +kb*kPBlock; 16-byte chunk k of every
   // lane at +1024*k).
   const int stat_lds = kSReg + wave * 256 + 16 * hl;
-  // The same statistics one float per lane: lane L holds query row
-  // 8*((L%16)/4) + L%4 + 4*hl, so within each 16-lane row of the wave lane r
-  // holds the row of result register r, and a DPP row broadcast of lane r
-  // hands every lane its register-r statistic.
-  const int stat_lds1 = kSReg + wave * 256 + 4 * (8 * ((lane & 15) >> 2) + (lane & 3) + 4 * hl);
-  auto ldf1 = [&](int addr) { return *reinterpret_cast<const float*>(smem + addr); };
   const int p_lds = kPReg + KB * kg * kPBlock + lane * 16;
   const float c_log2 = p.abs_scale_log2;
 
@@ -560,15 +546,13 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   constexpr int XL = 4;                // transposed-operand read lead
   constexpr int SL = 2;                // statistics / P read lead
   constexpr int F0 = NS >= 8 ? 1 : 0;  // first softmax / dS slot
-  // Statistics by one 4-byte read per lane and DPP row broadcasts (else four
-  // 16-byte reads per lane).
-  constexpr bool kStatDpp = SK_BWD_STAT_DPP;
   // Preloaded step start: barrier j waits for tile j+2, so at the end of
   // step j a wave already reads the first KLP row operands of step j+1 (role
   // 0: Q(j+2), role 1: dO(j+1)) and its MFMAs start right after the next
   // barrier; the DMA of tile j+4 is issued at slot kIssSlot, after the
-  // step's first MFMAs, instead of right after the barrier.
-  constexpr bool kPre = SK_BWD_DKV_PRELOAD;
+  // step's first MFMAs, instead of right after the barrier.  (Reading them
+  // after the barrier, and the statistics by one 4-byte read per lane with
+  // DPP row broadcasts, were slower candidates of the tile study.)
   constexpr int KLP = (KL + KB - 1) / KB;  // row operands read before slot 0
   constexpr int kIssSlot = 2;
   constexpr int kPreSlot = NS + 1;
@@ -594,14 +578,8 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       "every pair is packed before its accumulate slot");
   auto pair_t = [](int kb, int g) { return 4 * ((g >> 2) * KB + kb) + (g & 3); };
   auto begin_v2 = [&](int j) {
-    if constexpr (kPre) {
-      wait_tiles<kLoads, 1>(min(1, max(0, n_it - j - 3)));  // tile j+2 landed
-      __syncthreads();
-    } else {
-      wait_tiles<kLoads, 2>(min(2, max(0, n_it - j - 2)));  // tile j+1 landed
-      __syncthreads();
-      if (j + 4 < n_it) issue((j + 4) % STAGES);
-    }
+    wait_tiles<kLoads, 1>(min(1, max(0, n_it - j - 3)));  // tile j+2 landed
+    __syncthreads();
   };
   // Role 0, tile j in stage st, tile j+1 in stage st1, P buffer pbi; sc holds
   // S(j), nx receives S(j+1).
@@ -621,21 +599,11 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     // (key block 0) that uses them
     f32x4 lv[4];
     auto lv_slot = [&](int q) { return pf(pair_t(0, 2 * q)) - SL; };
-    float lx = 0.f;
-    if constexpr (kStatDpp) {
-      lx = ldf1(stat_lds1 + st * kStatStage);
-    } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (lv_slot(q) < 0) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
-    }
+    for (int q = 0; q < 4; ++q)
+      if (lv_slot(q) < 0) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
     // statistic of result register r
-    auto lse_r = [&](int r) {
-      if constexpr (kStatDpp)
-        return row_bcast(lx, r);
-      else
-        return lv[r / 4][r % 4];
-    };
+    auto lse_r = [&](int r) { return lv[r / 4][r % 4]; };
     u32x4 aq[KD];
     u32x4 xt[NX];
     float pe[KB][16];
@@ -649,7 +617,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     auto xt_slot = [&](int x) { return NS + (x / DB) * DB * KB + x % DB - XL; };
 #pragma unroll
     for (int s = 0; s < KD; ++s)
-      if (s * KB - KL < 0) aq[s] = kPre ? pre[s] : ld128(row_lds[s] + st1 * QT);
+      if (s * KB - KL < 0) aq[s] = pre[s];
 #pragma unroll
     for (int x = 0; x < NX; ++x)
       if (xt_slot(x) < 0) read_xt(x);
@@ -660,8 +628,8 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 #pragma unroll
       for (int s = 0; s < KD; ++s)
         if (s * KB - KL == i && i >= 0) aq[s] = ld128(row_lds[s] + st1 * QT);
-      if (kPre && i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
-      if (kPre && i == kPreSlot) {
+      if (i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
+      if (i == kPreSlot) {
 #pragma unroll
         for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + ((st1 + 1) % STAGES) * QT);
       }
@@ -670,7 +638,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
         if (xt_slot(x) == i) read_xt(x);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (!kStatDpp && lv_slot(q) == i) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
+        if (lv_slot(q) == i) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
       if (i < NS) {
         const int s = i / KB, kb = i % KB;
         nx[kb] = mfma32<T>(aq[s], kv[kb][s], nx[kb]);
@@ -720,20 +688,10 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     const uint8_t* pb = smem + p_lds + pbp * 4 * kPBlock;
     f32x4 pr[KB][4], dv[4];
     auto pr_slot = [&](int kb, int q) { return pf(pair_t(kb, 2 * q)) + 1 - SL; };
-    float dx = 0.f;
-    if constexpr (kStatDpp) {
-      dx = ldf1(stat_lds1 + stp * kStatStage);
-    } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (pr_slot(0, q) < 0) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
-    }
-    auto delta_r = [&](int r) {
-      if constexpr (kStatDpp)
-        return row_bcast(dx, r);
-      else
-        return dv[r / 4][r % 4];
-    };
+    for (int q = 0; q < 4; ++q)
+      if (pr_slot(0, q) < 0) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+    auto delta_r = [&](int r) { return dv[r / 4][r % 4]; };
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -751,7 +709,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     auto xq_slot = [&](int x) { return NS + (x / DB) * DB * KB + x % DB - XL; };
 #pragma unroll
     for (int s = 0; s < KD; ++s)
-      if (s * KB - KL < 0) ad[s] = kPre ? pre[s] : ld128(row_lds[s] + st * QT);
+      if (s * KB - KL < 0) ad[s] = pre[s];
 #pragma unroll
     for (int x = 0; x < NX; ++x)
       if (xq_slot(x) < 0) read_xq(x);
@@ -762,8 +720,8 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 #pragma unroll
       for (int s = 0; s < KD; ++s)
         if (s * KB - KL == i && i >= 0) ad[s] = ld128(row_lds[s] + st * QT);
-      if (kPre && i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
-      if (kPre && i == kPreSlot) {
+      if (i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
+      if (i == kPreSlot) {
 #pragma unroll
         for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + ((st + 1) % STAGES) * QT);
       }
@@ -772,7 +730,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
         if (xq_slot(x) == i) read_xq(x);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (!kStatDpp && pr_slot(0, q) == i) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+        if (pr_slot(0, q) == i) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -817,15 +775,13 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       if (t < n_it) issue(t);
     begin_v2(0);
     score_all(0, sv[0]);
-    if constexpr (kPre) {
-      // first row operands of the next body: role 0's S(1) reads Q(1), role
-      // 1's dP(1) reads dO(1), both in stage 1
+    // first row operands of the next body: role 0's S(1) reads Q(1), role
+    // 1's dP(1) reads dO(1), both in stage 1
 #pragma unroll
-      for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + QT);
-    }
+    for (int s = 0; s < KLP; ++s) pre[s] = ld128(row_lds[s] + QT);
     if (role == 0)
       body0(0, 0, 1, 0, sv[0], sv[1]);
-    else if (kPre && 4 < n_it)
+    else if (4 < n_it)
       issue(4);
     for (int j0 = 1; j0 < n_it; j0 += STAGES) {
 #pragma unroll
@@ -946,6 +902,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 template <class T, int DP, int BN, int NW, int STAGES, int OCC, int MODE, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
+  static_assert(MODE == 0 || MODE == 2, "dQ schedule: 0 (tiles in order) or 2");
   using L = BwdTile<DP, BN>;  // K and V tiles
   constexpr int BM = 32 * NW;
   constexpr int KD = DP / 16;  // k-steps over the head dim (S^T, dP^T)
@@ -1108,44 +1065,6 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
     for (int x = 0; x < KN * 8; ++x) elem(x, sd, pd);
   };
 
-  // Stage A: S^T / dP^T MFMAs of tile tn interleaved with the dS elements of
-  // the current tile, fenced per MFMA (see the dK/dV kernel).  MFMA order
-  // cycles over the 2*KB accumulators so consecutive links of one chain are
-  // 2*KB MFMAs apart.
-  auto stage_a = [&](int tn, f32x16 (&sn)[KB], f32x16 (&pn)[KB], const f32x16 (&sd)[KB],
-                     const f32x16 (&pd)[KB]) {
-    constexpr int NM = 2 * KD * KB;
-    constexpr int KLEAD = 3;
-    constexpr int NE = KN * 8;
-    constexpr int EPM = (NE + NM - 1) / NM;
-    const uint8_t* st = stage(tn);
-    auto addr = [&](int i) {
-      const int j = i % (2 * KB);
-      return st + (j / KB) * L::kTileBytes + k_lds[i / (2 * KB)] + (j % KB) * 32 * RB;
-    };
-    u32x4 a[NM];
-#pragma unroll
-    for (int i = 0; i < KLEAD; ++i) a[i] = lds_b128(addr(i));
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      sn[kb] = f32x16{};
-      pn[kb] = f32x16{};
-    }
-#pragma unroll
-    for (int i = 0; i < NM; ++i) {
-      if (i + KLEAD < NM) a[i + KLEAD] = lds_b128(addr(i + KLEAD));
-      const int j = i % (2 * KB), s = i / (2 * KB);
-      if (j / KB == 0)
-        sn[j % KB] = mfma32<T>(a[i], qreg[s], sn[j % KB]);
-      else
-        pn[j % KB] = mfma32<T>(a[i], greg[s], pn[j % KB]);
-#pragma unroll
-      for (int k = 0; k < EPM; ++k)
-        if (i * EPM + k < NE) elem(i * EPM + k, sd, pd);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
   // Stage B: dQ^T += K^T dS^T for tile t: lane holds
   // [d 32*c + 8*(r/4) + 4*hl + r%4][query row].
   auto gemm_dq = [&](int t) {
@@ -1277,28 +1196,6 @@ __global__ void __launch_bounds__(NW * 64, OCC) bwd_dq_kernel(BwdParams p) {
         last(s1, s0);
       else
         last(s0, s1);
-    }
-  } else if constexpr (MODE == 1) {
-    // Fixed register roles: even tiles in s0/p0, odd tiles in s1/p1.
-    if (n_tiles > 0) {
-      sync_tile(0, PD);
-      gemm_sdp(0, s0, p0);
-    }
-    auto iteration = [&](int t, f32x16 (&cs)[KB], f32x16 (&cp)[KB], f32x16 (&ns)[KB],
-                         f32x16 (&np)[KB]) {
-      premask(t, cs);
-      if (t + 1 < n_tiles) {
-        sync_tile(t + 1, PD - 1);
-        if (t + 1 + PD < n_tiles) issue_tile(t + 1 + PD);
-        stage_a(t + 1, ns, np, cs, cp);
-      } else {
-        tile_valu(cs, cp);
-      }
-      gemm_dq(t);
-    };
-    for (int t = 0; t < n_tiles; t += 2) {
-      iteration(t, s0, p0, s1, p1);
-      if (t + 1 < n_tiles) iteration(t + 1, s1, p1, s0, p0);
     }
   } else {
     // Tiles in order without the interleave: the other resident wave of the
@@ -1537,8 +1434,9 @@ __global__ void __launch_bounds__(256, OCC) bwd_dq_ds_kernel(BwdParams p) {
 // schedule of a wave's MFMA and VALU work.
 // SK_BWD_DQ_TILE (key tile, workgroups per CU, schedule) overrides the
 // D <= 128 row for candidate builds.  Schedules: 0 tiles in order (the other
-// wave of the SIMD overlaps the VALU work), 1 S^T and dP^T one tile ahead,
-// 2 S^T one tile ahead and dP^T in step.
+// wave of the SIMD overlaps the VALU work), 2 S^T one tile ahead and dP^T in
+// step.  (Schedule 1, S^T and dP^T both one tile ahead, was a slower
+// candidate of the tile study and is no longer in the sources.)
 #ifndef SK_BWD_DQ_TILE
 #define SK_BWD_DQ_TILE 32, 2, 2
 #endif

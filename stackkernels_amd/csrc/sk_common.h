@@ -104,35 +104,6 @@ __device__ __forceinline__ float to_f32<F16>(uint16_t x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Lane r of every 16-lane row of the wave, broadcast to that row (DPP
-// row_newbcast).  r must fold to a constant: the switch selects the
-// instruction's immediate.
-template <int R>
-__device__ __forceinline__ float row_bcast_c(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + R, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row_bcast(float x, int r) {
-  switch (r) {
-    case 0: return row_bcast_c<0>(x);
-    case 1: return row_bcast_c<1>(x);
-    case 2: return row_bcast_c<2>(x);
-    case 3: return row_bcast_c<3>(x);
-    case 4: return row_bcast_c<4>(x);
-    case 5: return row_bcast_c<5>(x);
-    case 6: return row_bcast_c<6>(x);
-    case 7: return row_bcast_c<7>(x);
-    case 8: return row_bcast_c<8>(x);
-    case 9: return row_bcast_c<9>(x);
-    case 10: return row_bcast_c<10>(x);
-    case 11: return row_bcast_c<11>(x);
-    case 12: return row_bcast_c<12>(x);
-    case 13: return row_bcast_c<13>(x);
-    case 14: return row_bcast_c<14>(x);
-    default: return row_bcast_c<15>(x);
-  }
-}
-
 // Online-softmax rescale threshold in log2 units: the running exponent offset
 // is raised only when a score exceeds it by more than this, so unnormalised
 // probabilities stay <= 2^8 (exact in bf16/fp16 range, no fp32 overflow).
