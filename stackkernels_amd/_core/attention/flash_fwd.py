@@ -6,7 +6,9 @@ Same contract as the reference's ``flash_attn_fwd``
 (B, H_q, S_q) fp32; GQA/MQA by ``H_q % H_kv == 0``; bottom-right causal mask.
 ``rope_cos`` / ``rope_sin`` / ``start_pos`` rotate q in the kernel's prologue
 (query row i at position ``start_pos + i``): the prefill step with the
-reference's ``apply_rope`` on q fused in.  Forward only.
+reference's ``apply_rope`` on q fused in.  This launcher is forward only; the
+torch-level ``flash_attention`` pairs it with a backward that rotates q again
+(``sk_rope_rotate``) and carries dQ back through the rotation's adjoint.
 """
 
 from __future__ import annotations
