@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "c718559f5103f328f13a8841467e0a7941071f229c40d33aad8752b250223eec"
+TRAFFIC_SOURCES_SHA256 = "455d254e6970e7fcc5537d65b1d55a4940c4157b46a22dcbdad50e402bf96606"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 682_278_263,
-    "fwd_long": 842_371_768,
-    "fwdbwd": 4_535_306_146,
-    "decode": 8_601_597_301,
-    "decode_mqa": 573_053_304,
-    "decode_varlen": 4_305_224_770,
-    "kv_update": 67_240_132,
-    "decode_paged": 4_305_376_485,
-    "decode_rope": 8_601_618_819,
-    "kv_update_rope": 75_523_347,
-    "decode_step": 4_306_761_910,
+    "fwd": 678_607_198,
+    "fwd_long": 812_783_306,
+    "fwdbwd": 4_534_102_498,
+    "decode": 8_601_597_265,
+    "decode_mqa": 573_053_179,
+    "decode_varlen": 4_305_224_753,
+    "kv_update": 67_240_133,
+    "decode_paged": 4_305_376_498,
+    "decode_rope": 8_601_618_818,
+    "kv_update_rope": 75_523_556,
+    "decode_step": 4_306_761_706,
 }
 
 
