@@ -331,8 +331,9 @@ SK_API int sk_attn_fwd_rope(int dtype, const void* q, const void* k, const void*
  * Rotate a (B, H, S, D) tensor by its RoPE angles (inverse = 0) or by their
  * negatives (inverse = 1, the adjoint: the gradient of the rotation), token t
  * of batch row b at the position given above (positions as in the other
- * *_rope calls, tokens = S).  Element strides {b, h, s} for x and out; out
- * may be x (in place), otherwise it must not overlap it.  The rotation is
+ * *_rope calls, tokens = S).  Element strides {b, h, s} for x and out; out's
+ * rows must not overlap one another; out may be x (in place, with the same
+ * strides), otherwise it must not overlap it (SK_EINVAL).  The rotation is
  * the one the fused kernels apply, bit for bit, so it rebuilds the rotated q
  * that sk_attn_fwd_rope used and carries dq back through the rotation for
  * sk_attn_bwd.  Replaces rope_fwd / _rope_fwd_kernel and rope_bwd /

@@ -796,6 +796,24 @@ int sk_rope_rotate(int dtype, const void* x, void* out, int B, int H, int S, int
     return rc;
   if (rows == 0) return SK_OK;
   if ((rc = check_ptr("x", x)) || (rc = check_ptr("out", out))) return rc;
+  {
+    // out's rows must not overlap one another (else the writes race): sorted
+    // by stride, each dimension of extent > 1 must step past the rows of the
+    // dimensions below it.
+    int64_t ext[3] = {B, H, S}, st[3] = {out_strides[0], out_strides[1], out_strides[2]};
+    for (int i = 0; i < 3; ++i)
+      for (int j = i + 1; j < 3; ++j)
+        if (st[j] < st[i]) std::swap(st[i], st[j]), std::swap(ext[i], ext[j]);
+    int64_t span = D;  // elements the dimensions below cover
+    for (int i = 0; i < 3; ++i) {
+      if (ext[i] <= 1) continue;
+      if (st[i] < span) return fail(SK_EINVAL, "out strides make rows overlap");
+      span = st[i] * ext[i];
+    }
+  }
+  if (x == out && (x_strides[0] != out_strides[0] || x_strides[1] != out_strides[1] ||
+                   x_strides[2] != out_strides[2]))
+    return fail(SK_EINVAL, "in place (out == x) needs out's strides to equal x's");
   if (x != out) {
     // In place or disjoint: a partial overlap would let one row's write
     // reach another row's unread input.

@@ -279,6 +279,24 @@ def test_rope_argument_errors(lib):
     assert pdec() == _lib.SK_EINVAL and "multiple of 32" in _lib.last_error()
 
 
+def test_rope_rotate_argument_errors(lib):
+    """sk_rope_rotate checks its layout before launching: out's rows must not
+    overlap, in place needs equal strides, a partial overlap of x and out is
+    rejected.  (Every case here fails before the launch: the pointers are
+    not device memory.)"""
+    from stackkernels_amd._core.attention import _lib
+
+    def rot(x=4096, out=1 << 20, xs=(4096, 1024, 64), os_=(4096, 1024, 64), B=2, H=4, S=16, D=64):
+        return lib.sk_rope_rotate(2, x, out, B, H, S, D, _st(*xs), _st(*os_), 16, 16, 0, 64, 64,
+                                  None, 0, 0, None)
+
+    assert rot(os_=(4096, 1024, 0)) == _lib.SK_EINVAL and "overlap" in _lib.last_error()
+    assert rot(os_=(4096, 32, 64)) == _lib.SK_EINVAL and "overlap" in _lib.last_error()
+    assert rot(os_=(64, 1024, 64)) == _lib.SK_EINVAL and "overlap" in _lib.last_error()
+    assert rot(out=4096, os_=(8192, 1024, 64)) == _lib.SK_EINVAL and "in place" in _lib.last_error()
+    assert rot(out=4096 + 256) == _lib.SK_EINVAL and "overlaps x" in _lib.last_error()
+
+
 def test_decode_noalloc_rejects_oversized_splits(lib):
     """An explicit split count whose partials exceed the static scratch is
     rejected before anything runs (no device call on this path)."""
