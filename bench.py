@@ -85,19 +85,19 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "455d254e6970e7fcc5537d65b1d55a4940c4157b46a22dcbdad50e402bf96606"
+TRAFFIC_SOURCES_SHA256 = "08beffe97915bff2b011d7732ad0f6bff334b28054800709de6e296783abfc1a"
 HBM_TRAFFIC_BYTES = {
-    "fwd": 678_607_198,
-    "fwd_long": 812_783_306,
-    "fwdbwd": 4_534_102_498,
-    "decode": 8_601_597_265,
-    "decode_mqa": 573_053_179,
-    "decode_varlen": 4_305_224_753,
-    "kv_update": 67_240_133,
-    "decode_paged": 4_305_376_498,
-    "decode_rope": 8_601_618_818,
-    "kv_update_rope": 75_523_556,
-    "decode_step": 4_306_761_706,
+    "fwd": 681_165_750,
+    "fwd_long": 838_971_108,
+    "fwdbwd": 4_535_370_302,
+    "decode": 8_601_597_260,
+    "decode_mqa": 573_053_237,
+    "decode_varlen": 4_305_224_903,
+    "kv_update": 67_240_127,
+    "decode_paged": 4_305_376_554,
+    "decode_rope": 8_601_618_835,
+    "kv_update_rope": 75_523_377,
+    "decode_step": 4_306_761_979,
 }
 
 
