@@ -186,3 +186,38 @@ def test_many_chunks_full_size(device):
         for x, e, what in zip(five, exact, ("dQ", "dK", "dV")):
             assert_close_maxabs(x[b:b + 1, h:h + 1], e, TOL[dt], f"{what} (b={b}, h={h})")
         assert np.isfinite(exact[0]).all()
+
+
+def _random_shapes(n, seed):
+    g = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(g.integers(1, 5))
+        out.append((int(g.integers(1, 4)), hkv * int(g.choice([1, 2, 4])), hkv,
+                    int(g.integers(1, 700)), int(g.integers(1, 900)), int(g.choice([80, 96, 128])),
+                    i % 2 == 0,
+                    torch.bfloat16 if g.integers(0, 2) else torch.float16))
+    return out
+
+
+@pytest.mark.parametrize("shape", _random_shapes(12, 2024),
+                         ids=lambda s: "x".join(map(str, s[:6])) + ("c" if s[6] else "n"))
+def test_random_shapes_every_chunking_bit_identical(device, shape):
+    """Seeded random shapes (ragged S_q and S_k in either order, GQA, head dims 80 (run
+    zero-padded to 96), 96 and 128, every other one causal, fp16 or bf16): the one-chunk five-GEMM backward, chunks of
+    one pair and the seven-GEMM backward give the same bits, and the oracle's gradients
+    within the rounding bound."""
+    b, hq, hkv, sq, sk, d, causal, dtype = shape
+    print(f"random chunking case {shape}", flush=True)
+    q, k, v = make_qkv(b, hq, hkv, sq, sk, d, dtype, seed=sq * 7 + sk)
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(sk)).to(dtype).to(q.device)
+    o, lse = flash_attn_fwd(q, k, v, is_causal=causal)
+    pref, mn, pair = _sizes(dtype, b, hq, hkv, sq, sk, d, causal)
+    full = _bwd(do, q, k, v, o, lse, causal, pref)
+    ones = _bwd(do, q, k, v, o, lse, causal, mn + pair)
+    seven = _bwd(do, q, k, v, o, lse, causal, mn)
+    torch.cuda.synchronize()
+    for x, y, z, what in zip(full, ones, seven, ("dQ", "dK", "dV")):
+        assert torch.equal(x, y), f"{what}: chunks of one pair differ"
+        assert torch.equal(x, z), f"{what}: seven-GEMM backward differs"
+    _check_bound(q, k, v, do, causal, full)
