@@ -183,7 +183,8 @@ const char* sk_last_error(void) { return g_err; }
 static int fwd_shape(int dtype, int B, int Hq, int Hkv, int Sq, int Sk, int D, int is_causal,
                      sk::FwdParams* p) {
   p->B = B, p->Hq = Hq, p->Hkv = Hkv, p->Sq = Sq, p->Sk = Sk, p->D = D, p->group = Hq / Hkv;
-  const int rows = dtype == SK_F32 ? 64 : sk::fwd_rows_per_block(dtype, D, (int64_t)B * Hq, Sq, Sk, is_causal != 0);
+  const int rows = dtype == SK_F32 ? sk::fwd_f32_rows_per_block(D, Sq)
+                                   : sk::fwd_rows_per_block(dtype, D, (int64_t)B * Hq, Sq, Sk, is_causal != 0);
   p->n_mblocks = (Sq + rows - 1) / rows;
   if ((int64_t)p->n_mblocks * B * Hq > 0x7fffffffLL)
     return fail(SK_EINVAL, "grid too large: %lld workgroups", (long long)p->n_mblocks * B * Hq);

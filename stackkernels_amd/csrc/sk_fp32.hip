@@ -1,12 +1,14 @@
-// fp32 attention kernels (forward, backward) on the gfx950 vector ALUs, and
-// the backward row-statistics pass shared by every dtype.
+// fp32 attention kernels (forward, backward) and the backward row-statistics
+// pass shared by every dtype.
 //
 // fp32 inputs are computed in true fp32 (no reduced-precision MFMA inputs),
 // which is what the reference path does (_reference/torch/attention.py:56-61).
-// Four lanes share one row: each holds a quarter of the head dimension, and
-// q.k partial sums are combined with two cross-lane adds.  K/V (or Q/dO)
-// tiles of 16 rows are staged in LDS; the online softmax is updated once per
-// tile.
+// The forward of padded head dims up to 128 runs on the matrix cores
+// (fwd_f32_mfma_kernel, v_mfma_f32_32x32x2_f32: fp32 products, fp32
+// accumulation).  The other kernels here run on the vector ALUs: four lanes
+// share one row, each holding a quarter of the head dimension, and q.k
+// partial sums are combined with two cross-lane adds; K/V (or Q/dO) tiles of
+// 16 rows are staged in LDS and the online softmax is updated once per tile.
 #include "sk_common.h"
 #include "sk_kernels.h"
 #include "sk_rope.h"
@@ -131,6 +133,230 @@ __global__ void __launch_bounds__(256) fwd_f32_kernel(FwdParams p) {
     if (d < p.D) op[d] = acc[i] * inv;
   }
   if (part == 0) p.lse[(int64_t)bh * p.Sq + row] = l_run > 0.f ? m_run + logf(l_run) : kNegInf;
+}
+
+// Forward on the matrix cores (padded head dim 64 or 128, at least 32 query
+// rows).  v_mfma_f32_32x32x2_f32 multiplies and accumulates in fp32: lane l
+// supplies A[l%32][l/32] and B[l/32][l%32], and holds D[8*(r/4) + 4*(l/32) +
+// r%4][l%32] in register r, as for the 16-bit 32x32 products.  A workgroup
+// of 8 waves (two per SIMD) owns 256 query rows of one (batch, head), 32 per
+// wave with q in registers; 64-key K/V tiles go through a 2-deep LDS ring
+// written by buffer_load ... lds, one barrier per tile (a tile is about 16k
+// MFMA cycles per wave, so one tile of load look-ahead is ample).
+// * S^T = K Q^T: k-step s contracts head-dim column s in lanes 0-31 and
+//   DP/2 + s in lanes 32-63 (the same permutation on both operands), so one
+//   16-byte LDS read gives a lane four k-steps of K.  K rows are stored with
+//   16-byte chunk c at c ^ (row % 16), which puts the 16 rows a read touches
+//   in distinct bank quads.  Two 32-key score blocks per tile are two
+//   independent MFMA chains.
+// * O^T += V^T P^T: P^T is the score registers themselves (k-step r
+//   contracts the keys the two lane halves hold in register r), and output
+//   block c holds head-dim columns DB*m + c (m its row), so one 16-byte read
+//   of a V row serves all DB blocks and the epilogue writes whole 16-byte
+//   pieces of each output row.
+// * Online softmax in base 2 with |sm_scale| * log2(e) folded into one FMA;
+//   the running maximum moves every tile (the VALU work is small beside the
+//   MFMAs).  Masking and the rows without a visible key follow the reference
+//   path as in fwd_f32_kernel.
+constexpr int kF32MmaRows = 256;
+
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(512, 1) fwd_f32_mfma_kernel(FwdParams p) {
+  constexpr int NW = 8;
+  constexpr int BN = 64;
+  constexpr int KS = DP / 2;              // k-steps of S^T (per lane half: DP/2 columns)
+  constexpr int DB = DP / 32;             // output blocks of 32 head-dim columns
+  constexpr int RB = DP * 4;              // row bytes
+  constexpr int KT = BN * RB;             // tile bytes
+  constexpr int CPR = RB / 16;            // 16-byte chunks per row
+  constexpr int SEGR = 1024 / RB;         // rows per 1 KiB DMA segment
+  constexpr int LK = KT / 1024 / NW;      // segments per wave per tile (K, and V)
+  static_assert(DP == 64 || DP == 128, "padded head dim 64 or 128");
+  static_assert((KT / 1024) % NW == 0, "tile segments must divide over the waves");
+  typedef float vrow_t __attribute__((ext_vector_type(DB)));
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * KT];  // K stages, then V stages
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hl = lane >> 5;
+
+  // Heaviest query block first under the causal mask; XCD-aware order.
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int bh = w / p.n_mblocks;
+  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
+  const int b = bh / p.Hq, hq = bh % p.Hq, hkv = hq / p.group;
+  const int m0 = mblk * kF32MmaRows;
+  const int mw = m0 + 32 * wave;
+  const int row = mw + l32;
+  const bool row_ok = row < p.Sq;
+  const int diag = p.Sk - p.Sq;
+
+  // Q^T operand: lane holds q[row][hl * KS + s] at k-step s (rotated when
+  // the call carries RoPE tables; zero past S_q and D; negated for a
+  // negative scale).
+  float qv[KS];
+  {
+    const float* qp = (const float*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)row * p.q_ss;
+    const int rrow = row_ok ? rope_row(p.rope, b, row) : -1;
+    if (rrow >= 0) {
+      const int half = p.D >> 1;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int d = hl * KS + s;
+        qv[s] = d < p.D ? rope1(qp, d, half, p.rope, rrow) : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KS / 4; ++j) {
+        const int d = hl * KS + 4 * j;
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        if (row_ok && d < p.D) x = *reinterpret_cast<const f32x4*>(qp + d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qv[4 * j + e] = x[e];
+      }
+    }
+    if (p.q_sign) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qv[s] = -qv[s];
+    }
+  }
+
+  // DMA: segment j of this wave is segment wave + 8 j of the tile; the
+  // lane's global byte offset of the chunk that lands at its LDS slot.
+  const float* kbase = (const float*)p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = (const float*)p.v + b * p.v_sb + hkv * p.v_sh;
+  uint32_t koff[LK], voff[LK];
+#pragma unroll
+  for (int j = 0; j < LK; ++j) {
+    const int r = (wave + j * NW) * SEGR + lane / CPR;
+    const int pc = lane % CPR;
+    const int kc = pc ^ (r & 15);
+    koff[j] = kc * 4 < p.D ? (uint32_t)((r * p.k_ss + kc * 4) * 4) : kBufferOob;
+    voff[j] = pc * 4 < p.D ? (uint32_t)((r * p.v_ss + pc * 4) * 4) : kBufferOob;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto range = [&](int rows, int64_t stride) {
+    return rows > 0 ? (int)(((int64_t)(rows - 1) * stride + p.D) * 4) : 0;
+  };
+  auto issue = [&](int t) {
+    const int n0 = t * BN;
+    const int rows = min(BN, p.Sk - n0);
+    const int st = t & 1;
+    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.k_ss, range(rows, p.k_ss));
+    const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.v_ss, range(rows, p.v_ss));
+#pragma unroll
+    for (int j = 0; j < LK; ++j)
+      buffer_load_lds_b128(kr, lds0 + st * KT + (wave + j * NW) * 1024, koff[j]);
+#pragma unroll
+    for (int j = 0; j < LK; ++j)
+      buffer_load_lds_b128(vr, lds0 + (2 + st) * KT + (wave + j * NW) * 1024, voff[j]);
+  };
+
+  int n_end = p.Sk;
+  if (CAUSAL) n_end = min(p.Sk, m0 + kF32MmaRows + diag);
+  const int n_tiles = n_end > 0 ? (n_end + BN - 1) / BN : 0;
+  // Tiles [0, vis) hold keys this wave's rows can see.
+  int vis = mw < p.Sq ? n_tiles : 0;
+  if (CAUSAL) {
+    const int last_key = mw + 31 + diag;
+    vis = last_key < 0 ? 0 : min(vis, last_key / BN + 1);
+  }
+
+  // Lane-constant LDS byte offsets: K chunk j of this lane's half (row l32
+  // of key block kb adds kb * 32 rows, which keeps the swizzle), and this
+  // lane's V piece (columns DB*m .. DB*m + DB-1, m = l32) in row 4*hl.
+  int k_lds[KS / 4];
+#pragma unroll
+  for (int j = 0; j < KS / 4; ++j) k_lds[j] = l32 * RB + (((hl * (KS / 4) + j) ^ (l32 & 15)) * 16);
+  const int v_lds = 2 * KT + 4 * hl * RB + l32 * DB * 4;
+
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int c = 0; c < DB; ++c) oacc[c] = f32x16{};
+  float m_run = kNegInf, l_run = 0.f;
+
+  if (n_tiles > 0) issue(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    wait_vmcnt<0>();  // tile t (the only one in flight) landed for this wave ...
+    __syncthreads();  // ... and for all; every read of tile t-1 retired
+    if (t + 1 < n_tiles) issue(t + 1);  // into tile t-1's stage
+    if (t >= vis) continue;
+    const int st = t & 1;
+    const uint8_t* kt = smem + st * KT;
+    f32x16 sc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int j = 0; j < KS / 4; ++j) {
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(kt + k_lds[j]);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(kt + 32 * RB + k_lds[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], qv[4 * j + e], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], qv[4 * j + e], sc[1], 0, 0, 0);
+      }
+    }
+    // Register r of block kb: key n0 + 32 kb + 8 (r/4) + 4 hl + r%4.
+    const int n0 = t * BN;
+    if (n0 + BN > p.Sk || (CAUSAL && n0 + BN - 1 > mw + diag)) {
+      int lim = p.Sk - 1;
+      if (CAUSAL) lim = min(lim, row + diag);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (n0 + 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3) > lim) sc[kb][r] = kNegInf;
+    }
+    float mt = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[kb][r]);
+    mt = xhalf_max(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = m_new == kNegInf ? 1.f : fast_exp2((m_run - m_new) * p.scale_log2);
+    const float neg_m = m_new == kNegInf ? 0.f : -m_new * p.scale_log2;
+    m_run = m_new;
+    float ps = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sc[kb][r] = fast_exp2(fmaf(sc[kb][r], p.scale_log2, neg_m));
+        ps += sc[kb][r];
+      }
+    l_run = l_run * alpha + ps;
+#pragma unroll
+    for (int c = 0; c < DB; ++c) oacc[c] *= alpha;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int krow = 32 * kb + 8 * (r >> 2) + (r & 3);
+        const vrow_t x = *reinterpret_cast<const vrow_t*>(smem + st * KT + v_lds + krow * RB);
+#pragma unroll
+        for (int c = 0; c < DB; ++c)
+          oacc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(x[c], sc[kb][r], oacc[c], 0, 0, 0);
+      }
+  }
+
+  const float l_tot = xhalf_sum(l_run);
+  if (!row_ok) return;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  float* op = (float*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)row * p.o_ss;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int d = DB * (8 * (r >> 2) + 4 * hl + (r & 3));
+    if (d < p.D) {
+      vrow_t x;
+#pragma unroll
+      for (int c = 0; c < DB; ++c) x[c] = oacc[c][r] * inv;
+      *reinterpret_cast<vrow_t*>(op + d) = x;
+    }
+  }
+  if (hl == 0)
+    p.lse[(int64_t)bh * p.Sq + row] = l_tot > 0.f ? m_run * p.scale + logf(l_tot) : kNegInf;
 }
 
 // Row statistics for the backward, any dtype:
@@ -352,7 +578,37 @@ static KernelPlan plan_fwd_f32_dp(const FwdParams& p, bool causal) {
   return k;
 }
 
+// The matrix-core kernel for padded head dims up to 128 and at least 32
+// query rows (no paged or per-row-length decode: those have one query row);
+// the vector kernel otherwise.
+static bool fwd_f32_on_mfma(int d, int sq) {
+  const int dp = padded_head_dim(d);
+  return dp > 0 && dp <= 128 && sq >= 32;
+}
+
+int fwd_f32_rows_per_block(int d, int sq) { return fwd_f32_on_mfma(d, sq) ? kF32MmaRows : kF32Rows; }
+
+template <int DP>
+static KernelPlan plan_fwd_f32_mfma(const FwdParams& p, bool causal) {
+  KernelPlan k;
+  k.fn = causal ? (const void*)fwd_f32_mfma_kernel<DP, true> : (const void*)fwd_f32_mfma_kernel<DP, false>;
+  k.grid = dim3((unsigned)(p.n_mblocks * p.B * p.Hq));
+  k.block = dim3(512);
+  k.kernel = "fwd_f32_mfma_kernel";
+  k.elem = 0;
+  k.head_dim = DP;
+  k.block_m = kF32MmaRows;
+  k.block_n = 64;
+  k.stages = 2;
+  k.causal = causal;
+  k.rope = p.rope.cos != nullptr;
+  return k;
+}
+
 KernelPlan plan_fwd_f32(const FwdParams& p, bool causal) {
+  if (fwd_f32_on_mfma(p.D, p.Sq) && !p.block_table && !p.seqlens)
+    return padded_head_dim(p.D) <= 64 ? plan_fwd_f32_mfma<64>(p, causal)
+                                      : plan_fwd_f32_mfma<128>(p, causal);
   switch (padded_head_dim(p.D)) {
     case 64: return plan_fwd_f32_dp<64>(p, causal);
     case 96: return plan_fwd_f32_dp<96>(p, causal);

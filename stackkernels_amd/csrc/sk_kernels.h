@@ -239,6 +239,8 @@ hipError_t run_plan(const KernelPlan& k, const void* params, hipStream_t s);
 
 KernelPlan plan_fwd_mfma(int dtype, const FwdParams& p, bool causal);
 KernelPlan plan_fwd_f32(const FwdParams& p, bool causal);
+// Query rows per workgroup of the fp32 forward for head dim d and sq queries.
+int fwd_f32_rows_per_block(int d, int sq);
 KernelPlan plan_decode_mfma(int dtype, const DecParams& p);
 KernelPlan plan_decode_combine(int dtype, const DecParams& p);
 // The backward plans fill the block counts of p they derive.

@@ -1,4 +1,5 @@
-"""GPU parity of both entries of the forward tile table at D = 128 and D = 64.
+"""GPU parity of both entries of the forward tile table at D = 128 and D = 64, and of
+the fp32 forward's matrix-core kernel at its block and tile edges.
 
 The table picks by shape: short work (S_q <= 2048, causal S_q <= 4096, or
 fewer than 2048 blocks of 256 rows in the grid) runs 4 waves with two
@@ -60,3 +61,32 @@ def test_forward_table_entry_matches_oracle(b, h, s, sk, d, causal, dt, rows):
         what = f"(b={bi}, h={hi}, S_q={s}, S_k={sk}, D={d}, causal={causal}, {name})"
         assert_close_maxabs(sl(out), o_ref, TOL[dt], "O " + what)
         assert_lse_close(sl(lse), lse_ref, "LSE " + what)
+
+
+@pytest.mark.parametrize("b,h,hkv,s,sk,d,causal,scale,kernel", [
+    (2, 4, 2, 256, 256, 128, True, None, "fwd_f32_mfma_kernel"),   # one whole block
+    (2, 4, 2, 257, 300, 128, True, None, "fwd_f32_mfma_kernel"),   # one row into a second block
+    (1, 8, 1, 513, 130, 96, True, None, "fwd_f32_mfma_kernel"),    # S_q > S_k: rows see no key
+    (1, 4, 4, 700, 1000, 80, False, -0.2, "fwd_f32_mfma_kernel"),  # D = 80 on the 128 kernel
+    (2, 6, 3, 300, 65, 64, False, 0.5, "fwd_f32_mfma_kernel"),     # keys end 1 past a tile
+    (2, 4, 2, 32, 2000, 40, True, None, "fwd_f32_mfma_kernel"),    # the shortest query run
+    (2, 4, 2, 31, 500, 128, True, None, "fwd_f32_kernel"),         # one row short of it
+])
+def test_fp32_forward_matches_oracle(b, h, hkv, s, sk, d, causal, scale, kernel):
+    """The fp32 forward on the matrix cores (256-row blocks, 64-key tiles, padded head
+    dims 64 and 128) at block and tile edges, and the vector kernel just below its
+    query-length threshold: O within 1e-4, LSE within 1e-3 of the float64 oracle."""
+    from oracle import attention_oracle as orc
+
+    from _gpu_util import make_qkv
+
+    cfg = pick("flash_attn", (b, h, s, d), dtype="float32", kv_len=sk, is_causal=causal)
+    assert cfg["kernel_variant"] == kernel
+    q, k, v = make_qkv(b, h, hkv, s, sk, d, torch.float32, seed=s + sk + d)
+    out, lse = flash_attn_fwd(q, k, v, is_causal=causal, sm_scale=scale)
+    torch.cuda.synchronize()
+    assert native_loaded()
+    o_ref, lse_ref = orc.attention_forward(np64(q), np64(k), np64(v), causal, scale)
+    what = f"(S_q={s}, S_k={sk}, D={d}, causal={causal}, scale={scale})"
+    assert_close_maxabs(out, o_ref, TOL[torch.float32], f"O {what}")
+    assert_lse_close(lse, lse_ref, f"LSE {what}")

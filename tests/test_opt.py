@@ -169,8 +169,15 @@ def test_pick_forward_and_backward():
     assert not u256["paired_causal_blocks"] and u256["grid"] == 256
     s128 = pick("flash_fwd", (1, 16, 4096, 128), dtype="bfloat16", is_causal=True)
     assert s128["BLOCK_M"] == 128 and not s128["paired_causal_blocks"] and s128["grid"] == 512
+    # fp32: the matrix-core forward (8 waves x 32 rows) for head dims up to 128 and at
+    # least 32 query rows, the vector-ALU kernel (64 rows) for D = 256 and short queries
     f32 = pick("flash_attn", (1, 8, 512, 64), dtype="float32")
-    assert f32["kernel_variant"] == "fwd_f32_kernel"
+    assert f32["kernel_variant"] == "fwd_f32_mfma_kernel"
+    assert (f32["BLOCK_M"], f32["BLOCK_N"], f32["grid"]) == (256, 64, 2 * 8)
+    assert pick("flash_attn", (1, 8, 512, 96), dtype="float32")["head_dim_padded"] == 128
+    for shape in ((1, 8, 16, 64), (1, 8, 512, 256)):
+        v = pick("flash_attn", shape, dtype="float32")
+        assert v["kernel_variant"] == "fwd_f32_kernel" and v["BLOCK_M"] == 64
     b = pick("flash_bwd", (2, 32, 2048, 128), dtype="bfloat16", kv_len=8192, num_kv_heads=8,
              is_causal=True)
     # D = 128: the five-GEMM backward (dQ from the dS tiles dK/dV stores)
