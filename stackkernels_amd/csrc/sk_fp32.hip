@@ -638,6 +638,347 @@ hipError_t launch_bwd_prep(int dtype, const BwdParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Backward on the matrix cores (padded head dim 64 or 128), the same fp32
+// products as the forward's matrix-core kernel and its operand layouts: the
+// k-steps of a product over the head dim contract column s in lanes 0-31 and
+// DP/2 + s in lanes 32-63; a product over keys or queries contracts the two
+// rows the lane halves hold in score register r (8 (r/4) + 4 hl + r%4); an
+// output block c holds head-dim columns DB*m + c.  Streamed tiles (32 rows)
+// keep 16-byte chunk c of row r at c ^ (r % 16), so the row-wise operand
+// reads (16 rows, one chunk each) and the column-piece reads (one row, 32
+// chunks) both hit distinct bank quads.  A workgroup is 4 waves, one per SIMD
+// (the resident operands and two accumulator sets exceed 256 registers), and
+// its tiles go through a 2-deep ring written by buffer_load ... lds, one
+// barrier per step; a step is 192 (dQ) or 256 (dK/dV) MFMAs of 64 cycles per
+// wave, so one step of load look-ahead is ample.  P = exp2(S * scale * log2 e
+// - lse * log2 e) is set to 0 where the key is masked, past S_k, or the query
+// past S_q; dS = P (dP - delta).
+constexpr int kF32MmaTile = 32;
+
+// Byte offset, in a swizzled tile of DP fp32 columns, of the DB-column piece
+// m (columns DB*m .. DB*m + DB - 1) of row r.
+template <int DP>
+__device__ __forceinline__ int f32_piece(int r, int m) {
+  constexpr int DB = DP / 32;
+  const int chunk = (DB * m) >> 2, sub = (DB * m) & 3;
+  return r * DP * 4 + ((chunk ^ (r & 15)) << 4) + 4 * sub;
+}
+
+// dQ: a wave owns 32 queries of one (batch, query head), q and dO resident;
+// 32-key K and V tiles stream.  S^T = K Q^T and dP^T = V dO^T (two chains),
+// then dQ^T += K^T dS^T.
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(256, 1) bwd_dq_f32_mfma_kernel(BwdParams p) {
+  constexpr int NW = 4, BN = kF32MmaTile, BM = 32 * NW;
+  constexpr int KS = DP / 2, DB = DP / 32, RB = DP * 4, KT = BN * RB;
+  constexpr int CPR = RB / 16, SEGR = 1024 / RB, LK = KT / 1024 / NW;
+  static_assert(DP == 64 || DP == 128, "padded head dim 64 or 128");
+  static_assert(LK >= 1 && (KT / 1024) % NW == 0, "tile segments must divide over the waves");
+  typedef float vrow_t __attribute__((ext_vector_type(DB)));
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * KT];  // K stages, then V stages
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hl = lane >> 5;
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int bh = w / p.n_mblocks;
+  const int mblk = p.n_mblocks - 1 - (w - bh * p.n_mblocks);
+  const int b = bh / p.Hq, hq = bh % p.Hq, hkv = hq / p.group;
+  const int m0 = mblk * BM;
+  const int mw = m0 + 32 * wave;
+  const int row = mw + l32;
+  const bool row_ok = row < p.Sq;
+  const int diag = p.Sk - p.Sq;
+
+  const int64_t qrow = ((int64_t)bh * p.Sq + row) * p.D;
+  float qv[KS], gv[KS];
+#pragma unroll
+  for (int j = 0; j < KS / 4; ++j) {
+    const int d = hl * KS + 4 * j;
+    f32x4 x = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+    if (row_ok && d < p.D) {
+      x = *reinterpret_cast<const f32x4*>((const float*)p.q + qrow + d);
+      y = *reinterpret_cast<const f32x4*>((const float*)p.dout + qrow + d);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[4 * j + e] = x[e], gv[4 * j + e] = y[e];
+  }
+  const float lse2 = row_ok ? p.lse_log2[(int64_t)bh * p.Sq + row] : __builtin_inff();
+  const float dl = row_ok ? p.delta[(int64_t)bh * p.Sq + row] : 0.f;
+
+  const float* kbase = (const float*)p.k + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+  const float* vbase = (const float*)p.v + ((int64_t)b * p.Hkv + hkv) * p.Sk * p.D;
+  uint32_t goff[LK];
+#pragma unroll
+  for (int j = 0; j < LK; ++j) {
+    const int r = (wave + j * NW) * SEGR + lane / CPR;
+    const int c = (lane % CPR) ^ (r & 15);
+    goff[j] = c * 4 < p.D ? (uint32_t)((r * p.D + c * 4) * 4) : kBufferOob;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int t) {
+    const int n0 = t * BN;
+    const int bytes = min(BN, p.Sk - n0) * p.D * 4;
+    const i32x4 kr = make_rsrc_words(kbase + (int64_t)n0 * p.D, bytes);
+    const i32x4 vr = make_rsrc_words(vbase + (int64_t)n0 * p.D, bytes);
+    const int st = t & 1;
+#pragma unroll
+    for (int j = 0; j < LK; ++j) buffer_load_lds_b128(kr, lds0 + st * KT + (wave + j * NW) * 1024, goff[j]);
+#pragma unroll
+    for (int j = 0; j < LK; ++j)
+      buffer_load_lds_b128(vr, lds0 + (2 + st) * KT + (wave + j * NW) * 1024, goff[j]);
+  };
+
+  int n_end = p.Sk;
+  if (CAUSAL) n_end = min(p.Sk, m0 + BM + diag);
+  const int n_tiles = n_end > 0 ? (n_end + BN - 1) / BN : 0;
+  int vis = mw < p.Sq ? n_tiles : 0;
+  if (CAUSAL) {
+    const int last_key = mw + 31 + diag;
+    vis = last_key < 0 ? 0 : min(vis, last_key / BN + 1);
+  }
+  // Row-wise operand chunk j of key row l32; column piece of key row
+  // 8 (r/4) + 4 hl + r%4 for the K^T operand of k-step r.
+  int k_lds[KS / 4], kt_lds[16];
+#pragma unroll
+  for (int j = 0; j < KS / 4; ++j) k_lds[j] = l32 * RB + (((hl * (KS / 4) + j) ^ (l32 & 15)) << 4);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) kt_lds[r] = f32_piece<DP>(8 * (r >> 2) + 4 * hl + (r & 3), l32);
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int c = 0; c < DB; ++c) acc[c] = f32x16{};
+  if (n_tiles > 0) issue(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    wait_vmcnt<0>();  // tile t landed for this wave ...
+    __syncthreads();  // ... and for all; every read of tile t-1 retired
+    if (t + 1 < n_tiles) issue(t + 1);
+    if (t >= vis) continue;
+    const uint8_t* kt = smem + (t & 1) * KT;
+    const uint8_t* vt = smem + (2 + (t & 1)) * KT;
+    f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int j = 0; j < KS / 4; ++j) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(kt + k_lds[j]);
+      const f32x4 g = *reinterpret_cast<const f32x4*>(vt + k_lds[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qv[4 * j + e], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(g[e], gv[4 * j + e], dp, 0, 0, 0);
+      }
+    }
+    // Register r: key t*BN + 8 (r/4) + 4 hl + r%4 of query row `row`.
+    int lim = p.Sk - 1;
+    if (CAUSAL) lim = min(lim, row + diag);
+    const int n0 = t * BN + 4 * hl;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr =
+          n0 + 8 * (r >> 2) + (r & 3) <= lim ? fast_exp2(fmaf(s[r], p.scale_log2, -lse2)) : 0.f;
+      s[r] = pr * (dp[r] - dl);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const vrow_t x = *reinterpret_cast<const vrow_t*>(kt + kt_lds[r]);
+#pragma unroll
+      for (int c = 0; c < DB; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(x[c], s[r], acc[c], 0, 0, 0);
+    }
+  }
+  if (!row_ok) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int d = DB * (8 * (r >> 2) + 4 * hl + (r & 3));
+    if (d < p.D) {
+      vrow_t x;
+#pragma unroll
+      for (int c = 0; c < DB; ++c) x[c] = acc[c][r] * p.scale;
+      *reinterpret_cast<vrow_t*>((float*)p.dq + qrow + d) = x;
+    }
+  }
+}
+
+// dK, dV: a wave owns 32 keys of one (batch, KV head), K and V resident; the
+// group's query heads and their 32-query tiles stream (Q, dO and the row
+// statistics), so the GQA sum happens in registers.  S = Q K^T and dP = dO
+// V^T (two chains), then dV^T += dO^T P and dK^T += Q^T dS.
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(256, 1) bwd_dkv_f32_mfma_kernel(BwdParams p) {
+  constexpr int NW = 4, BMQ = kF32MmaTile, BNK = 32 * NW;
+  constexpr int KS = DP / 2, DB = DP / 32, RB = DP * 4, QT = BMQ * RB;
+  constexpr int CPR = RB / 16, SEGR = 1024 / RB, LQ = QT / 1024 / NW;
+  constexpr int kStat = 4 * QT;         // per stage: 64 lse*log2e, then 64 delta
+  static_assert(DP == 64 || DP == 128, "padded head dim 64 or 128");
+  static_assert(LQ >= 1 && (QT / 1024) % NW == 0, "tile segments must divide over the waves");
+  typedef float vrow_t __attribute__((ext_vector_type(DB)));
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * QT + 2 * 512];  // Q, dO stages; stats
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hl = lane >> 5;
+  // Lowest key block first: under the causal mask it sees the most queries.
+  const int w = xcd_work_index(blockIdx.x, gridDim.x);
+  const int bk = w / p.n_nblocks;
+  const int nblk = w - bk * p.n_nblocks;
+  const int b = bk / p.Hkv, hkv = bk % p.Hkv;
+  const int n0 = nblk * BNK;
+  const int nw = n0 + 32 * wave;
+  const int key = nw + l32;
+  const bool key_ok = key < p.Sk;
+  const int diag = p.Sk - p.Sq;
+
+  const int64_t krow = ((int64_t)bk * p.Sk + key) * p.D;
+  float kv[KS], vv[KS];
+#pragma unroll
+  for (int j = 0; j < KS / 4; ++j) {
+    const int d = hl * KS + 4 * j;
+    f32x4 x = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+    if (key_ok && d < p.D) {
+      x = *reinterpret_cast<const f32x4*>((const float*)p.k + krow + d);
+      y = *reinterpret_cast<const f32x4*>((const float*)p.v + krow + d);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kv[4 * j + e] = x[e], vv[4 * j + e] = y[e];
+  }
+
+  // Query tiles that can see a key of this block: rows i >= n0 - diag.
+  int m_begin = 0;
+  if (CAUSAL) m_begin = max(0, n0 - diag) / BMQ * BMQ;
+  const int n_mt = m_begin < p.Sq ? (p.Sq - m_begin + BMQ - 1) / BMQ : 0;
+  const int n_it = n0 < p.Sk ? p.group * n_mt : 0;
+
+  uint32_t goff[LQ];
+#pragma unroll
+  for (int j = 0; j < LQ; ++j) {
+    const int r = (wave + j * NW) * SEGR + lane / CPR;
+    const int c = (lane % CPR) ^ (r & 15);
+    goff[j] = c * 4 < p.D ? (uint32_t)((r * p.D + c * 4) * 4) : kBufferOob;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  const int64_t bh0 = (int64_t)b * p.Hq + hkv * p.group;
+  auto issue = [&](int it) {
+    const int gi = it / n_mt;
+    const int m = m_begin + (it - gi * n_mt) * BMQ;
+    const int rows = min(BMQ, p.Sq - m);
+    const int64_t r0 = (bh0 + gi) * p.Sq + m;
+    const i32x4 qr = make_rsrc_words((const float*)p.q + r0 * p.D, rows * p.D * 4);
+    const i32x4 gr = make_rsrc_words((const float*)p.dout + r0 * p.D, rows * p.D * 4);
+    const int st = it & 1;
+#pragma unroll
+    for (int j = 0; j < LQ; ++j) buffer_load_lds_b128(qr, lds0 + st * QT + (wave + j * NW) * 1024, goff[j]);
+#pragma unroll
+    for (int j = 0; j < LQ; ++j)
+      buffer_load_lds_b128(gr, lds0 + (2 + st) * QT + (wave + j * NW) * 1024, goff[j]);
+    if (wave < 2) {  // wave 0: lse * log2 e, wave 1: delta (64 slots; the first 32 used)
+      const i32x4 sr = make_rsrc_words((wave == 0 ? p.lse_log2 : p.delta) + r0, rows * 4);
+      buffer_load_lds_b32(sr, lds0 + kStat + st * 512 + wave * 256, lane * 4);
+    }
+  };
+
+  // Row-wise operand chunk j of query row l32; column piece of query row
+  // 8 (r/4) + 4 hl + r%4 for the dO^T / Q^T operands of k-step r.
+  int q_lds[KS / 4], qt_lds[16];
+#pragma unroll
+  for (int j = 0; j < KS / 4; ++j) q_lds[j] = l32 * RB + (((hl * (KS / 4) + j) ^ (l32 & 15)) << 4);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) qt_lds[r] = f32_piece<DP>(8 * (r >> 2) + 4 * hl + (r & 3), l32);
+
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int c = 0; c < DB; ++c) dk[c] = f32x16{}, dv[c] = f32x16{};
+  if (n_it > 0) issue(0);
+  for (int it = 0; it < n_it; ++it) {
+    wait_vmcnt<0>();  // step it's tiles landed for this wave ...
+    __syncthreads();  // ... and for all; every read of step it-1 retired
+    if (it + 1 < n_it) issue(it + 1);
+    const int m = m_begin + (it % n_mt) * BMQ;
+    // Skip a tile none of this wave's keys can see (or keys past S_k).
+    if (nw >= p.Sk || (CAUSAL && m + BMQ - 1 + diag < nw)) continue;
+    const uint8_t* qt = smem + (it & 1) * QT;
+    const uint8_t* gt = smem + (2 + (it & 1)) * QT;
+    const float* stl = reinterpret_cast<const float*>(smem + kStat + (it & 1) * 512);
+    f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int j = 0; j < KS / 4; ++j) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(qt + q_lds[j]);
+      const f32x4 g = *reinterpret_cast<const f32x4*>(gt + q_lds[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], kv[4 * j + e], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(g[e], vv[4 * j + e], dp, 0, 0, 0);
+      }
+    }
+    // Register r: query m + 8 (r/4) + 4 hl + r%4 against key `key`.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(stl + 8 * i + 4 * hl);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(stl + 64 + 8 * i + 4 * hl);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * i + e;
+        const int q = m + 8 * i + 4 * hl + e;
+        const bool ok = key_ok && q < p.Sq && (!CAUSAL || key <= q + diag);
+        const float pr = ok ? fast_exp2(fmaf(s[r], p.scale_log2, -l4[e])) : 0.f;
+        s[r] = pr;
+        dp[r] = pr * (dp[r] - d4[e]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const vrow_t g = *reinterpret_cast<const vrow_t*>(gt + qt_lds[r]);
+      const vrow_t x = *reinterpret_cast<const vrow_t*>(qt + qt_lds[r]);
+#pragma unroll
+      for (int c = 0; c < DB; ++c) {
+        dv[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(g[c], s[r], dv[c], 0, 0, 0);
+        dk[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(x[c], dp[r], dk[c], 0, 0, 0);
+      }
+    }
+  }
+  if (!key_ok) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int d = DB * (8 * (r >> 2) + 4 * hl + (r & 3));
+    if (d < p.D) {
+      vrow_t x, y;
+#pragma unroll
+      for (int c = 0; c < DB; ++c) x[c] = dk[c][r] * p.scale, y[c] = dv[c][r];
+      *reinterpret_cast<vrow_t*>((float*)p.dk + krow + d) = x;
+      *reinterpret_cast<vrow_t*>((float*)p.dv + krow + d) = y;
+    }
+  }
+}
+
+template <int DP>
+static KernelPlan plan_bwd_f32_mfma(BwdParams& p, bool causal, bool dq) {
+  KernelPlan k;
+  if (dq) {
+    p.n_mblocks = (p.Sq + 127) / 128;
+    k.fn = causal ? (const void*)bwd_dq_f32_mfma_kernel<DP, true>
+                  : (const void*)bwd_dq_f32_mfma_kernel<DP, false>;
+    k.grid = dim3((unsigned)((int64_t)p.n_mblocks * p.B * p.Hq));
+    k.kernel = "bwd_dq_f32_mfma_kernel";
+    k.block_m = 128;
+    k.block_n = kF32MmaTile;
+  } else {
+    p.n_nblocks = (p.Sk + 127) / 128;
+    k.fn = causal ? (const void*)bwd_dkv_f32_mfma_kernel<DP, true>
+                  : (const void*)bwd_dkv_f32_mfma_kernel<DP, false>;
+    k.grid = dim3((unsigned)((int64_t)p.n_nblocks * p.B * p.Hkv));
+    k.kernel = "bwd_dkv_f32_mfma_kernel";
+    k.block_m = kF32MmaTile;
+    k.block_n = 128;
+  }
+  k.block = dim3(256);
+  k.elem = 0;
+  k.head_dim = DP;
+  k.stages = 2;
+  k.causal = causal;
+  return k;
+}
+
 template <int DP>
 static KernelPlan plan_bwd_f32_dp(BwdParams& p, bool causal, bool dq) {
   p.n_mblocks = (p.Sq + kF32Rows - 1) / kF32Rows;
@@ -664,7 +1005,10 @@ static KernelPlan plan_bwd_f32_dp(BwdParams& p, bool causal, bool dq) {
 }
 
 static KernelPlan plan_bwd_f32(BwdParams& p, bool causal, bool dq) {
-  switch (padded_head_dim(p.D)) {
+  const int dp = padded_head_dim(p.D);
+  if (dp > 0 && dp <= 64) return plan_bwd_f32_mfma<64>(p, causal, dq);
+  if (dp > 64 && dp <= 128) return plan_bwd_f32_mfma<128>(p, causal, dq);
+  switch (dp) {
     case 64: return plan_bwd_f32_dp<64>(p, causal, dq);
     case 96: return plan_bwd_f32_dp<96>(p, causal, dq);
     case 128: return plan_bwd_f32_dp<128>(p, causal, dq);

@@ -1,4 +1,5 @@
-"""GPU parity of the HIP backward (bf16 / fp16 MFMA kernels) against the oracle.
+"""GPU parity of the HIP backward (bf16 / fp16 and fp32 MFMA kernels, the fp32
+vector kernels at D = 256) against the oracle.
 
 The grid follows the reference's tests/ops/test_flash_attn.py::test_flash_attn_backward
 (heads {(4,4),(4,2),(4,1)} x causal, random upstream gradient) widened to every
@@ -6,7 +7,8 @@ head dim the reference supports and to ragged / fully-masked shapes; the
 full-size BASELINE config 3 (bf16 causal GQA, bottom-right mask) is checked
 against the repo's PyTorch reference path run in fp32 on the device, whose
 gradients come from autograd exactly as the reference's backward does.
-Tolerance: max-abs <= 2e-2 on dQ / dK / dV (bf16 / fp16), stated by the target.
+Tolerance: max-abs <= 2e-2 on dQ / dK / dV (bf16 / fp16) and 1e-4 (fp32), stated by
+the target.
 """
 
 import pytest
@@ -25,6 +27,7 @@ from _gpu_util import (TOL, assert_close_maxabs, assert_lse_close, make_qkv, nat
 pytestmark = pytest.mark.gpu
 
 HALF = [torch.float16, torch.bfloat16]
+ALL = [torch.float32, *HALF]
 
 
 @pytest.fixture(autouse=True)
@@ -60,7 +63,7 @@ def _check(q, k, v, g, causal, dtype, scale=None):
     assert_close_maxabs(v.grad, dv, TOL[dtype], "dV")
 
 
-@pytest.mark.parametrize("dtype", HALF, ids=str)
+@pytest.mark.parametrize("dtype", ALL, ids=str)
 @pytest.mark.parametrize("heads", [(4, 4), (4, 2), (4, 1)])
 @pytest.mark.parametrize("is_causal", [False, True])
 def test_backward_reference_grid(device, dtype, heads, is_causal):
@@ -69,7 +72,7 @@ def test_backward_reference_grid(device, dtype, heads, is_causal):
     _check(q, k, v, g, is_causal, dtype)
 
 
-@pytest.mark.parametrize("dtype", HALF, ids=str)
+@pytest.mark.parametrize("dtype", ALL, ids=str)
 @pytest.mark.parametrize("head_dim", [64, 80, 96, 128, 256])
 @pytest.mark.parametrize("is_causal", [False, True])
 @pytest.mark.parametrize("heads", [(8, 8), (8, 2), (8, 1)])
@@ -78,7 +81,7 @@ def test_backward_head_dims(device, dtype, head_dim, is_causal, heads):
     _check(q, k, v, g, is_causal, dtype)
 
 
-@pytest.mark.parametrize("dtype", HALF, ids=str)
+@pytest.mark.parametrize("dtype", ALL, ids=str)
 @pytest.mark.parametrize("sq,sk", [(1, 1), (1, 300), (3, 5), (65, 65), (127, 129), (200, 77),
                                    (129, 1000), (300, 300), (513, 257)])
 @pytest.mark.parametrize("is_causal", [False, True])
@@ -87,7 +90,7 @@ def test_backward_ragged_shapes(device, dtype, sq, sk, is_causal):
     _check(q, k, v, g, is_causal, dtype)
 
 
-@pytest.mark.parametrize("dtype", HALF, ids=str)
+@pytest.mark.parametrize("dtype", ALL, ids=str)
 def test_backward_fully_masked_rows(device, dtype):
     # causal, S_q > S_k: rows i < S_q - S_k see no key; their dQ is 0 and they add nothing to dK/dV
     q, k, v, g = _run(2, 4, 2, 200, 70, 64, dtype, True)
@@ -117,7 +120,33 @@ def test_backward_custom_and_negative_scale(device, dtype, scale):
         check_backward(np64(ours), np64(path), exact[i], mass[i], dt, name)
 
 
-@pytest.mark.parametrize("dtype", HALF, ids=str)
+@pytest.mark.parametrize("scale", [0.05, 1.0, -0.09])
+def test_backward_fp32_custom_and_negative_scale(device, scale):
+    """fp32 at non-default scales: every gradient within 1e-4 of the oracle (at scale 1.0
+    |dQ| and |dK| reach ~28, where fp32 still resolves 2e-6)."""
+    q, k, v, g = _run(1, 4, 4, 70, 90, 64, torch.float32, True, scale=scale)
+    _check(q, k, v, g, True, torch.float32, scale)
+
+
+@pytest.mark.parametrize("head_dim,kernels", [
+    (64, "bwd_dkv_f32_mfma_kernel+bwd_dq_f32_mfma_kernel"),
+    (96, "bwd_dkv_f32_mfma_kernel+bwd_dq_f32_mfma_kernel"),
+    (256, "bwd_dkv_f32_kernel+bwd_dq_f32_kernel"),
+])
+def test_backward_fp32_kernels_and_long_sequence(device, head_dim, kernels):
+    """The fp32 backward runs on the matrix cores up to a padded head dim of 128 (the
+    vector kernels at 256); a causal GQA shape over several 128-key and 128-query blocks
+    with ragged ends, against the oracle at 1e-4."""
+    from stackkernels_amd._opt.pick import pick
+
+    cfg = pick("flash_bwd", (1, 8, 700, head_dim), dtype="float32", kv_len=900, num_kv_heads=2,
+               is_causal=True)
+    assert cfg["kernel_variant"] == kernels
+    q, k, v, g = _run(1, 8, 2, 700, 900, head_dim, torch.float32, True, seed=head_dim)
+    _check(q, k, v, g, True, torch.float32)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
 def test_backward_empty_sequences(device, dtype):
     # no keys: O = 0, every gradient 0; no queries: dK = dV = 0
     for sq, sk in ((10, 0), (0, 10)):
@@ -129,7 +158,7 @@ def test_backward_empty_sequences(device, dtype):
         assert torch.all(dq == 0) and torch.all(dk == 0) and torch.all(dv == 0)
 
 
-@pytest.mark.parametrize("dtype", HALF, ids=str)
+@pytest.mark.parametrize("dtype", ALL, ids=str)
 def test_backward_deterministic(device, dtype):
     q, k, v = make_qkv(2, 8, 2, 300, 333, 128, dtype)
     o, lse = flash_attn_fwd(q, k, v, is_causal=True)
