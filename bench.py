@@ -69,6 +69,7 @@ if ROOT not in sys.path:
 
 METRIC = "attn fwd/bwd TFLOP/s (% bf16 MFMA peak); flash_decode KV GB/s (% HBM peak)"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA (the fp32 study workloads)
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 PEAK_NOTE = {
     "mfma": "MI355X published dense bf16/fp16 MFMA peak, 2500 TFLOP/s (256 CUs x 2.4 GHz x "
@@ -76,6 +77,7 @@ PEAK_NOTE = {
             "below it: the vendor's bf16 GEMM sustains about 1307 TFLOP/s at 70% MFMA busy and "
             "1.69 GHz (bench.py --workload gemm)",
     "hbm": "MI355X published HBM3E peak, 8000 GB/s",
+    "mfma_f32": "MI355X published dense fp32 matrix peak, 157.3 TFLOP/s",
 }
 
 # HBM bytes per step of each workload's kernels, from two rocprofv3 --pmc runs
@@ -196,6 +198,15 @@ STUDY_WORKLOADS = {
                         B=2, Hq=32, Hkv=8, Sq=2048, Sk=8192, D=256, causal=True, dtype="bf16",
                         kind="fwdbwd"),
 }
+# fp32 inputs (true fp32 products and accumulation on the fp32 MFMA), priced
+# against the fp32 matrix peak; selectable with --workload.
+STUDY_WORKLOADS.update({
+    "fwd_f32": dict(name="fp32 study: flash_attention fwd fp32 causal MHA, C2 shape", B=4, Hq=32,
+                    Hkv=32, Sq=4096, Sk=4096, D=128, causal=True, dtype="fp32", kind="fwd"),
+    "fwdbwd_f32": dict(name="fp32 study: C3 shape fwd+bwd fp32 causal GQA bottom-right", B=2,
+                       Hq=32, Hkv=8, Sq=2048, Sk=8192, D=128, causal=True, dtype="fp32",
+                       kind="fwdbwd"),
+})
 ALL_WORKLOADS = {**WORKLOADS, **STUDY_WORKLOADS}
 
 
@@ -291,7 +302,7 @@ def _rate(units: float, unit: str, seconds: float) -> float:
 
 
 def _make_inputs(w: dict, torch, dev, sets: int = 1):
-    dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float16
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[w["dtype"]]
     g = torch.Generator(device=dev).manual_seed(0)
     out = []
     if w["kind"] == "decode_paged":  # (q, k_pool, v_pool)
@@ -840,9 +851,13 @@ def run_cpu_baseline(w: dict, budget_s: float):
         # (16,384^2 fp32 scores are 1 GiB per head)
         hkv_chunk = max(1, 4 // grp) if w["Sq"] * w["Sk"] <= (1 << 26) else 1
     hq_chunk = hkv_chunk * grp
-    q = torch.randn(1, hq_chunk, w["Sq"], w["D"], generator=g).bfloat16().float()
-    k = torch.randn(1, hkv_chunk, w["Sk"], w["D"], generator=g).bfloat16().float()
-    v = torch.randn(1, hkv_chunk, w["Sk"], w["D"], generator=g).bfloat16().float()
+    def rnd(*shape):  # 16-bit workloads: values representable in the input type
+        x = torch.randn(*shape, generator=g)
+        return x if w["dtype"] == "fp32" else x.bfloat16().float()
+
+    q = rnd(1, hq_chunk, w["Sq"], w["D"])
+    k = rnd(1, hkv_chunk, w["Sk"], w["D"])
+    v = rnd(1, hkv_chunk, w["Sk"], w["D"])
     do = torch.randn_like(q) if w["kind"] == "fwdbwd" else None
     done = 0
     t0 = time.perf_counter()
@@ -881,8 +896,9 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
     value = _rate(units, unit, ms_step / 1e3)
     achieved = _rate(units, unit, ms_kernel / 1e3)
     bound = "hbm" if unit == "GB/s" else "mfma"
-    peak = PEAK_HBM_GBPS if bound == "hbm" else PEAK_BF16_TFLOPS
-    kernel = {"fwd": "fwd_mfma_kernel", "fwdbwd": "fwd + bwd kernels",
+    f32 = w["dtype"] == "fp32"
+    peak = PEAK_HBM_GBPS if bound == "hbm" else PEAK_FP32_TFLOPS if f32 else PEAK_BF16_TFLOPS
+    kernel = {"fwd": "fwd_f32_mfma_kernel" if f32 else "fwd_mfma_kernel", "fwdbwd": "fwd + bwd kernels",
               "decode": "decode_split_kernel + decode_combine_kernel",
               "decode_varlen": "decode_split_kernel + decode_combine_kernel",
               "decode_paged": "decode_split_kernel (paged) + decode_combine_kernel",
@@ -905,7 +921,7 @@ def measure(key: str, steps: int, warmup: int, cpu_s: float) -> dict:
             "peak": peak,
             "unit": unit,
             "frac": round(achieved / peak, 4),
-            "peak_basis": PEAK_NOTE[bound],
+            "peak_basis": PEAK_NOTE["mfma_f32" if f32 and bound == "mfma" else bound],
             "traffic": traffic,
             "traffic_unit": "HBM bytes per step",
             "traffic_note": traffic_note,
@@ -971,7 +987,7 @@ def main() -> int:
                          "device copy, the calibration kernel for the HBM-traffic counters; "
                          "'gemm' times a bf16 8192^3 torch.matmul, the sustained-MFMA reference; "
                          "fwd_d64, fwd_d64_long, fwd_d256, fwdbwd_d64, fwdbwd_d256 are tile-study "
-                         "shapes outside the default run")
+                         "shapes and fwd_f32, fwdbwd_f32 fp32 shapes, outside the default run")
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload (0 disables)")
