@@ -87,7 +87,7 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "08beffe97915bff2b011d7732ad0f6bff334b28054800709de6e296783abfc1a"
+TRAFFIC_SOURCES_SHA256 = "ccaaef2a5414897f661ccb1e71790df88bc953186da9804e25d4771eb8178d47"
 HBM_TRAFFIC_BYTES = {
     "fwd": 681_165_750,
     "fwd_long": 838_971_108,

@@ -580,10 +580,14 @@ static KernelPlan plan_fwd_f32_dp(const FwdParams& p, bool causal) {
 
 // The matrix-core kernel for padded head dims up to 128 and at least 32
 // query rows (no paged or per-row-length decode: those have one query row);
-// the vector kernel otherwise.
+// the vector kernel otherwise.  A tile-study build with -DSK_F32_MFMA=0
+// sends every fp32 forward and backward to the vector kernels.
+#ifndef SK_F32_MFMA
+#define SK_F32_MFMA 1
+#endif
 static bool fwd_f32_on_mfma(int d, int sq) {
   const int dp = padded_head_dim(d);
-  return dp > 0 && dp <= 128 && sq >= 32;
+  return SK_F32_MFMA && dp > 0 && dp <= 128 && sq >= 32;
 }
 
 int fwd_f32_rows_per_block(int d, int sq) { return fwd_f32_on_mfma(d, sq) ? kF32MmaRows : kF32Rows; }
@@ -1006,8 +1010,8 @@ static KernelPlan plan_bwd_f32_dp(BwdParams& p, bool causal, bool dq) {
 
 static KernelPlan plan_bwd_f32(BwdParams& p, bool causal, bool dq) {
   const int dp = padded_head_dim(p.D);
-  if (dp > 0 && dp <= 64) return plan_bwd_f32_mfma<64>(p, causal, dq);
-  if (dp > 64 && dp <= 128) return plan_bwd_f32_mfma<128>(p, causal, dq);
+  if (SK_F32_MFMA && dp > 0 && dp <= 64) return plan_bwd_f32_mfma<64>(p, causal, dq);
+  if (SK_F32_MFMA && dp > 64 && dp <= 128) return plan_bwd_f32_mfma<128>(p, causal, dq);
   switch (dp) {
     case 64: return plan_bwd_f32_dp<64>(p, causal, dq);
     case 96: return plan_bwd_f32_dp<96>(p, causal, dq);
