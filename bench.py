@@ -87,7 +87,7 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "ccaaef2a5414897f661ccb1e71790df88bc953186da9804e25d4771eb8178d47"
+TRAFFIC_SOURCES_SHA256 = "69e6a79db93d112bb53944d70ab8e9dc307b3e05172ba6a38ce8f4fbd5326f72"
 HBM_TRAFFIC_BYTES = {
     "fwd": 681_165_750,
     "fwd_long": 838_971_108,

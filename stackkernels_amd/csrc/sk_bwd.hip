@@ -79,8 +79,9 @@
 #ifndef SK_BWD_DKV_DO_D256
 #define SK_BWD_DKV_DO_D256 128
 #endif
-// Key blocks of 32 per dK/dV wave in the 6-deep schedule: 1, or 2 in a
-// tile-study build.
+// Key blocks of 32 per dK/dV wave in the D = 128 6-deep schedule: 1, or 2 in
+// a tile-study build (at D = 64 the step has too few MFMA slots to place two
+// key blocks' element pairs, so that schedule keeps one).
 #ifndef SK_BWD_DKV_KB
 #define SK_BWD_DKV_KB 1
 #endif
@@ -1476,9 +1477,9 @@ static KernelPlan plan_dkv_t(BwdParams& p, bool causal) {
   // and SK_BWD_DKV_STAGES_D64=4 build the 4-deep one-tile-per-step schedule
   // instead.  D = 256 keeps the 4-deep one (the 6-deep ring does not fit).
   constexpr int STAGES = DP == 128 ? SK_BWD_DKV_STAGES : DP == 64 ? SK_BWD_DKV_STAGES_D64 : 4;
-  // Keys per wave: 64 (two 32-key blocks; four waves, one per SIMD) in the
-  // 6-deep schedule, else 32 (eight waves).
-  constexpr int KB = STAGES == 6 ? SK_BWD_DKV_KB : 1;
+  // Keys per wave: 64 (two 32-key blocks; four waves, one per SIMD) in a
+  // tile-study build of the D = 128 6-deep schedule, else 32 (eight waves).
+  constexpr int KB = STAGES == 6 && DP == 128 ? SK_BWD_DKV_KB : 1;
   p.n_nblocks = (p.Sk + 127) / 128;
   KernelPlan k;
   k.fn = causal ? (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, KB, true>
