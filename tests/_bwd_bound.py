@@ -8,6 +8,9 @@ FlashAttention-2 does:
   P V), so delta = rowsum(dO * O) is off by at most 2u * sum_d (P|V|)_d |dO_d|;
 * P is rounded before dV = P^T dO;
 * dS = P (dP - delta) is rounded before dQ = scale dS K and dK = scale dS^T Q;
+* above 128 head-dim columns (padded head dim 256) the dK/dV kernel hands P
+  from one of its wave roles to the other in the input type (its LDS
+  budget), so dS is formed from a rounded P as well;
 * each gradient is rounded to the input type at the end.
 
 Running the error of each rounding through the products gives, per element,
@@ -21,7 +24,9 @@ delta of the oracle):
 Each rounding can also be off by half the type's subnormal spacing (eta =
 2^-25 in fp16, where P and dS values below 2^-14 lose relative precision;
 negligible in bf16), so every visible (i, j) adds eta / u to the weights of
-P and dS above.  The bound is
+P and dS above.  Where dS is formed from a rounded P (head dim above 128),
+that rounding adds |dS| and (eta / u) |dP - delta| to the weight of dS.  The
+bound is
 
     |ours - exact| <= |path - exact| + K u (|exact| + A),   K = 2,
 
@@ -61,6 +66,8 @@ def rounding_mass(q, k, v, do, causal, scale, dtype):
     e = ((p @ np.abs(vv)) * np.abs(do)).sum(-1, keepdims=True)
     floor = (SUBNORMAL_HALF_STEP[dtype] / UNIT_ROUNDOFF[dtype]) * (p > 0)
     w = np.abs(ds) + 2.0 * p * e + floor
+    if d > 128:  # dS formed from P rounded to the input type
+        w = w + np.abs(ds) + floor * np.abs(dp - delta)
     a_dq = abs(sc) * (w @ np.abs(kk))
     a_dk = abs(sc) * (np.swapaxes(w, -1, -2) @ np.abs(q))
     a_dv = np.swapaxes(p + floor, -1, -2) @ np.abs(do)

@@ -15,7 +15,9 @@ from _bwd_bound import check_backward, rounding_mass
 def _model_backward(q, k, v, do, causal, scale, dt, mistake=None):
     """fp32 FlashAttention-2 backward with the kernels' rounding: O stored in
     dt by a forward that rounds P before P V; delta from the stored O; P and
-    dS rounded to dt before their products; gradients rounded to dt."""
+    dS rounded to dt before their products (above 128 head-dim columns dS is
+    formed from the rounded P, which the dK/dV kernel hands between its wave
+    roles in dt); gradients rounded to dt."""
     r = lambda x: orc.round_to(np.asarray(x, dtype=np.float32), dt)  # noqa: E731
     b, hq, sq, d = q.shape
     hkv, sk = k.shape[1], k.shape[2]
@@ -37,7 +39,7 @@ def _model_backward(q, k, v, do, causal, scale, dt, mistake=None):
     if mistake == "delta_from_next_row":
         delta = np.roll(delta, 1, axis=2)
     dp = do_eff @ np.swapaxes(vv, -1, -2)
-    ds = p * (dp - delta)
+    ds = (r(p) if d > 128 else p) * (dp - delta)
     if mistake == "ds_without_p":
         ds = dp - delta
     dv = np.swapaxes(r(p), -1, -2) @ do_eff
@@ -71,6 +73,10 @@ CASES = [
     (1, 8, 1, 40, 50, 240, True, 0.3),
     (1, 4, 4, 30, 40, 64, True, 1.0),
     (2, 4, 2, 33, 17, 96, True, -0.5),
+    # head dim above 128 with fp16 P values down in the subnormal range
+    # (two random-shape seeds that the bound without that rounding missed)
+    (3, 6, 3, 121, 160, 144, True, 0.3),
+    (3, 6, 3, 160, 160, 216, True, 0.3),
 ]
 
 
