@@ -87,7 +87,7 @@ PEAK_NOTE = {
 # so these are recorded figures.  TRAFFIC_SOURCES_SHA256 is the digest of the
 # kernel sources (kernel_sources_digest) the counters were measured on; when
 # the sources differ, the line reports traffic null rather than a stale figure.
-TRAFFIC_SOURCES_SHA256 = "69e6a79db93d112bb53944d70ab8e9dc307b3e05172ba6a38ce8f4fbd5326f72"
+TRAFFIC_SOURCES_SHA256 = "caabc7557ffd45bbbc639c87567a7368ad6532d52283fbb03d5e3d5445c1d131"
 HBM_TRAFFIC_BYTES = {
     "fwd": 681_165_750,
     "fwd_long": 838_971_108,

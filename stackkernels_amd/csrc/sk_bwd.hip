@@ -79,12 +79,6 @@
 #ifndef SK_BWD_DKV_DO_D256
 #define SK_BWD_DKV_DO_D256 128
 #endif
-// Key blocks of 32 per dK/dV wave in the D = 128 6-deep schedule: 1, or 2 in
-// a tile-study build (at D = 64 the step has too few MFMA slots to place two
-// key blocks' element pairs, so that schedule keeps one).
-#ifndef SK_BWD_DKV_KB
-#define SK_BWD_DKV_KB 1
-#endif
 // Five-GEMM backward at D = 128 (1, the table) or seven GEMMs everywhere (0):
 // the dK/dV kernel stores dS and bwd_dq_ds_kernel computes dQ from it.
 #ifndef SK_BWD_FIVE_GEMM
@@ -174,10 +168,10 @@ __device__ __forceinline__ u32x4 lds_tr_pair(const uint8_t* lo, const uint8_t* h
 // ahead so that every step interleaves MFMAs with the VALU work of the
 // previous tile in the same wave (a wave overlaps MFMA and VALU issue only
 // with its own instructions).
-template <class T, int DP, int DO, int STAGES, int KB, bool CAUSAL>
-__global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
-  constexpr int NW = 8 / KB;   // waves: two roles per key group
-  constexpr int NKG = 4 / KB;  // key groups of 32 * KB keys
+template <class T, int DP, int DO, int STAGES, bool CAUSAL>
+__global__ void __launch_bounds__(512, 1) bwd_dkv_kernel(BwdParams p) {
+  constexpr int NW = 8;   // waves: two roles per key group
+  constexpr int NKG = 4;  // key groups of 32 keys
   constexpr int BMQ = 32;  // queries per tile (one 32x32 score block per wave)
   using L = BwdTile<DP, BMQ>;  // Q and dO tiles
   constexpr int BNK = 128;
@@ -201,7 +195,6 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // the pipelined schedule below, S one step ahead of P.
   constexpr bool kV2 = STAGES == 6;
   static_assert(STAGES == 4 || (kV2 && DP <= 128), "a 4-deep ring, or 6-deep at D <= 128");
-  static_assert(KB == 1 || (KB == 2 && kV2), "two key blocks per wave in the 6-deep schedule only");
   static_assert((2 * L::kSegs) % NW == 0, "tile segments must divide over the waves");
   static_assert((STAGES - 1) * QT + 16 * RB < 65536, "stage offsets must fit the ds immediate");
 
@@ -227,19 +220,17 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   const int b = bk / p.Hkv;
   const int hkv = bk - b * p.Hkv;
   const int n0 = nblk * BNK;
-  const int nw = n0 + 32 * KB * kg;  // first key of this wave (block kb: + 32 kb)
+  const int nw = n0 + 32 * kg;  // first key of this wave
   const int key = nw + l32;
   const int diag = p.Sk - p.Sq;
   const int d_out0 = dsp * DO;
 
   // Resident B operand, rows of this lane's key: K (sign-flipped for a
   // negative scale) for role 0, V for role 1: x[key][16*s + 8*hl .. +7].
-  u32x4 kv[KB][KD];
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    const int kr0 = nw + 32 * kb;
-    const int krows = max(0, min(32, p.Sk - kr0));
-    const int64_t k0 = ((int64_t)bk * p.Sk + min(kr0, p.Sk)) * p.D;
+  u32x4 kv[KD];
+  {
+    const int krows = max(0, min(32, p.Sk - nw));
+    const int64_t k0 = ((int64_t)bk * p.Sk + min(nw, p.Sk)) * p.D;
     const int bytes = __builtin_amdgcn_readfirstlane(tile_bytes(krows, p.D, p.D));
     const uint16_t* src = (const uint16_t*)(role == 0 ? p.k : p.v) + k0;
     const uint32_t sgn = role == 0 ? p.op_sign : 0u;
@@ -248,7 +239,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     for (int s = 0; s < KD; ++s) {
       const int d0 = 16 * s + 8 * hl;
       const uint32_t off = d0 < p.D ? (uint32_t)((l32 * p.D + d0) * 2) : kBufferOob;
-      kv[kb][s] = buffer_load_b128(r, off) ^ sgn;
+      kv[s] = buffer_load_b128(r, off) ^ sgn;
     }
   }
 
@@ -298,11 +289,9 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     }
   };
 
-  f32x16 acc[KB][DB];  // role 0: dV^T, role 1: dK^T, per key block
+  f32x16 acc[DB];  // role 0: dV^T, role 1: dK^T
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-    for (int c = 0; c < DB; ++c) acc[kb][c] = f32x16{};
+  for (int c = 0; c < DB; ++c) acc[c] = f32x16{};
 
   // Lane-constant LDS byte addresses.  Row-wise A operand (query row l32,
   // chunk 2s + hl) of S (role 0: Q region) or dP (role 1: dO region);
@@ -321,10 +310,9 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     tr_hi[c] += tr_reg;
   }
   // This wave's statistics copy (queries 8*i + 4*hl .. +3 at +32*i) and its
-  // key group's P blocks (block kb at +kb*kPBlock; 16-byte chunk k of every
-  // lane at +1024*k).
+  // key group's P block (16-byte chunk k of every lane at +1024*k).
   const int stat_lds = kSReg + wave * 256 + 16 * hl;
-  const int p_lds = kPReg + KB * kg * kPBlock + lane * 16;
+  const int p_lds = kPReg + kg * kPBlock + lane * 16;
   const float c_log2 = p.abs_scale_log2;
 
   auto ld128 = [&](int addr) { return *reinterpret_cast<const u32x4*>(smem + addr); };
@@ -337,20 +325,8 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     for (int s = 0; s < KD; ++s) a[s] = ld128(row_lds[s] + stg * QT);
     f32x16 sc = f32x16{};
 #pragma unroll
-    for (int s = 0; s < KD; ++s) sc = mfma32<T>(a[s], kv[0][s], sc);
+    for (int s = 0; s < KD; ++s) sc = mfma32<T>(a[s], kv[s], sc);
     return sc;
-  };
-  // The same for every key block of the wave (one read of each A operand).
-  auto score_all = [&](int stg, f32x16 (&out)[KB]) SK_INLINE {
-    u32x4 a[KD];
-#pragma unroll
-    for (int s = 0; s < KD; ++s) a[s] = ld128(row_lds[s] + stg * QT);
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) out[kb] = f32x16{};
-#pragma unroll
-    for (int s = 0; s < KD; ++s)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) out[kb] = mfma32<T>(a[s], kv[kb][s], out[kb]);
   };
   // acc^T += X^T G, X^T read transposed from stage stg, G the packed B
   // operand (P or dS) of the two 16-query k-steps.
@@ -366,7 +342,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int c = 0; c < DB; ++c) acc[0][c] = mfma32<T>(x[s2][c], g[s2], acc[0][c]);
+      for (int c = 0; c < DB; ++c) acc[c] = mfma32<T>(x[s2][c], g[s2], acc[c]);
   };
   auto pack16 = [&](const float (&v)[16], u32x4 (&g)[2]) {
 #pragma unroll
@@ -396,7 +372,7 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       (int64_t)bkl * p.group * p.ds_head_tiles + 4 * ds_off(nblk, p.ds_nqt, p.ds_c, CAUSAL) +
       (int64_t)kg * ds_cnt(nblk, p.ds_nqt, p.ds_c, CAUSAL) - ds_qb(nblk, p.ds_c, CAUSAL);
   auto store_ds = [&](const u32x4 (&gin)[2]) SK_INLINE {
-    if constexpr (KB == 1 && SK_BWD_FIVE_GEMM) {
+    if constexpr (SK_BWD_FIVE_GEMM) {
       if (p.ds != nullptr) {
         if (nw < p.Sk) {
           const int64_t tile = ds_t0 + (int64_t)ds_gi * p.ds_head_tiles + (ds_m0 >> 5);
@@ -538,11 +514,11 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // blocks).  Operand reads run KL / XL slots ahead of their first use; the
   // VALU work on element pairs is spread over the slots in the order the
   // accumulate slots consume the packed operands.
-  constexpr int NS = KD * KB;          // score MFMAs per step
-  constexpr int NA = 2 * DB * KB;      // accumulate MFMAs per step
+  constexpr int NS = KD;               // score MFMAs per step
+  constexpr int NA = 2 * DB;           // accumulate MFMAs per step
   constexpr int NX = 2 * DB;           // transposed reads per step
   constexpr int NM = NS + NA;
-  constexpr int NP = 8 * KB;           // element pairs per step
+  constexpr int NP = 8;                // element pairs per step
   constexpr int KL = 3;                // row-operand read lead (MFMA slots)
   constexpr int XL = 4;                // transposed-operand read lead
   constexpr int SL = 2;                // statistics / P read lead
@@ -554,52 +530,43 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // step's first MFMAs, instead of right after the barrier.  (Reading them
   // after the barrier, and the statistics by one 4-byte read per lane with
   // DPP row broadcasts, were slower candidates of the tile study.)
-  constexpr int KLP = (KL + KB - 1) / KB;  // row operands read before slot 0
+  constexpr int KLP = KL;  // row operands read before slot 0
   constexpr int kIssSlot = 2;
   constexpr int kPreSlot = NS + 1;
   u32x4 pre[KLP];
-  // Pair t in consumption order: (s2, kb, g) with t = 4 (s2 KB + kb) + g % 4
-  // and g the pair of elements 2g, 2g+1 of key block kb (g / 4 = s2).  Group
-  // u = t / 4 feeds accumulate slot NS + u DB; pair t starts (FMA) at slot
-  // pf(t), exponentiates at pf(t) + 1 and packs at pf(t) + 2.
-  auto pf = [](int t) {
-    if constexpr (KB == 1)
-      return t < 4 ? F0 + t * (NS - 3 - F0) / 3 : NS - 2 + (t - 4) * (DB - 1) / 3;
-    else
-      return F0 + (3 * t) / 2;
+  // Element pair g (elements 2g, 2g+1; k-step g / 4 of the accumulate
+  // operand) starts (FMA) at slot pf(g), exponentiates at pf(g) + 1 and
+  // packs at pf(g) + 2; pairs 4u .. 4u+3 feed accumulate slot NS + u DB.
+  auto pf = [](int g) {
+    return g < 4 ? F0 + g * (NS - 3 - F0) / 3 : NS - 2 + (g - 4) * (DB - 1) / 3;
   };
   static_assert(
       [] {
-        for (int t = 0; t < NP; ++t)
-          if ((KB == 1 ? (t < 4 ? F0 + t * (NS - 3 - F0) / 3 : NS - 2 + (t - 4) * (DB - 1) / 3)
-                       : F0 + (3 * t) / 2) + 3 > NS + (t / 4) * DB)
+        for (int g = 0; g < NP; ++g)
+          if ((g < 4 ? F0 + g * (NS - 3 - F0) / 3 : NS - 2 + (g - 4) * (DB - 1) / 3) + 3 >
+              NS + (g / 4) * DB)
             return false;
         return true;
       }(),
       "every pair is packed before its accumulate slot");
-  auto pair_t = [](int kb, int g) { return 4 * ((g >> 2) * KB + kb) + (g & 3); };
   auto begin_v2 = [&](int j) {
     wait_tiles<kLoads, 1>(min(1, max(0, n_it - j - 3)));  // tile j+2 landed
     __syncthreads();
   };
   // Role 0, tile j in stage st, tile j+1 in stage st1, P buffer pbi; sc holds
   // S(j), nx receives S(j+1).
-  auto body0 = [&](int j, int st, int st1, int pbi, f32x16 (&sc)[KB], f32x16 (&nx)[KB]) SK_INLINE {
-    if (CAUSAL) {
+  auto body0 = [&](int j, int st, int st1, int pbi, f32x16& sc, f32x16& nx) SK_INLINE {
+    if (CAUSAL && nw + 31 > cur_m0 + diag) {
+      // masked iff 8*(r/4) + r%4 < lim
+      const int lim = key - diag - cur_m0 - 4 * hl;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        if (nw + 32 * kb + 31 > cur_m0 + diag) {
-          // masked iff 8*(r/4) + r%4 < lim
-          const int lim = key + 32 * kb - diag - cur_m0 - 4 * hl;
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (8 * (r >> 2) + (r & 3) < lim) sc[kb][r] = kNegInf;
-        }
+      for (int r = 0; r < 16; ++r)
+        if (8 * (r >> 2) + (r & 3) < lim) sc[r] = kNegInf;
     }
     // statistics of elements 4q..4q+3, read SL slots before the first pair
-    // (key block 0) that uses them
+    // that uses them
     f32x4 lv[4];
-    auto lv_slot = [&](int q) { return pf(pair_t(0, 2 * q)) - SL; };
+    auto lv_slot = [&](int q) { return pf(2 * q) - SL; };
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (lv_slot(q) < 0) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
@@ -607,28 +574,27 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     auto lse_r = [&](int r) { return lv[r / 4][r % 4]; };
     u32x4 aq[KD];
     u32x4 xt[NX];
-    float pe[KB][16];
-    u32x4 pk[KB][2];
+    float pe[16];
+    u32x4 pk[2];
     uint8_t* pb = smem + p_lds + pbi * 4 * kPBlock;
     auto read_xt = [&](int x) {
       const int s2 = x / DB, c = x % DB;
       const int o = st * QT + 16 * s2 * RB;
       xt[x] = lds_tr_pair(smem + tr_lo[c] + o, smem + tr_hi[c] + o);
     };
-    auto xt_slot = [&](int x) { return NS + (x / DB) * DB * KB + x % DB - XL; };
+    auto xt_slot = [&](int x) { return NS + x - XL; };
 #pragma unroll
     for (int s = 0; s < KD; ++s)
-      if (s * KB - KL < 0) aq[s] = pre[s];
+      if (s - KL < 0) aq[s] = pre[s];
 #pragma unroll
     for (int x = 0; x < NX; ++x)
       if (xt_slot(x) < 0) read_xt(x);
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) nx[kb] = f32x16{};
+    nx = f32x16{};
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
 #pragma unroll
       for (int s = 0; s < KD; ++s)
-        if (s * KB - KL == i && i >= 0) aq[s] = ld128(row_lds[s] + st1 * QT);
+        if (s - KL == i && i >= 0) aq[s] = ld128(row_lds[s] + st1 * QT);
       if (i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
       if (i == kPreSlot) {
 #pragma unroll
@@ -641,34 +607,30 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
       for (int q = 0; q < 4; ++q)
         if (lv_slot(q) == i) lv[q] = ldf4(stat_lds + st * kStatStage + 32 * q);
       if (i < NS) {
-        const int s = i / KB, kb = i % KB;
-        nx[kb] = mfma32<T>(aq[s], kv[kb][s], nx[kb]);
+        nx = mfma32<T>(aq[i], kv[i], nx);
       } else {
         const int a = i - NS;
-        const int s2 = a / (DB * KB), kb = (a / DB) % KB, c = a % DB;
-        acc[kb][c] = mfma32<T>(xt[s2 * DB + c], pk[kb][s2], acc[kb][c]);
+        acc[a % DB] = mfma32<T>(xt[a], pk[a / DB], acc[a % DB]);
       }
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          const int f = pf(pair_t(kb, g));
-          float* e = pe[kb];
-          if (f == i) {
-            e[2 * g] = fmaf(sc[kb][2 * g], c_log2, -lse_r(2 * g));
-            e[2 * g + 1] = fmaf(sc[kb][2 * g + 1], c_log2, -lse_r(2 * g + 1));
-          }
-          if (f + 1 == i) {
-            e[2 * g] = fast_exp2(e[2 * g]);
-            e[2 * g + 1] = fast_exp2(e[2 * g + 1]);
-          }
-          if (f + 2 == i) pk[kb][g >> 2][g & 3] = pack2<T>(e[2 * g], e[2 * g + 1]);
-          // P (fp32) of elements 4k..4k+3 goes to LDS for role 1 once both
-          // pairs are exponentiated.
-          if ((g & 1) && f + 2 == i)
-            *reinterpret_cast<f32x4*>(pb + kb * kPBlock + 1024 * (g >> 1)) =
-                f32x4{e[2 * g - 2], e[2 * g - 1], e[2 * g], e[2 * g + 1]};
+      for (int g = 0; g < 8; ++g) {
+        const int f = pf(g);
+        float* e = pe;
+        if (f == i) {
+          e[2 * g] = fmaf(sc[2 * g], c_log2, -lse_r(2 * g));
+          e[2 * g + 1] = fmaf(sc[2 * g + 1], c_log2, -lse_r(2 * g + 1));
         }
+        if (f + 1 == i) {
+          e[2 * g] = fast_exp2(e[2 * g]);
+          e[2 * g + 1] = fast_exp2(e[2 * g + 1]);
+        }
+        if (f + 2 == i) pk[g >> 2][g & 3] = pack2<T>(e[2 * g], e[2 * g + 1]);
+        // P (fp32) of elements 4k..4k+3 goes to LDS for role 1 once both
+        // pairs are exponentiated.
+        if ((g & 1) && f + 2 == i)
+          *reinterpret_cast<f32x4*>(pb + 1024 * (g >> 1)) =
+              f32x4{e[2 * g - 2], e[2 * g - 1], e[2 * g], e[2 * g + 1]};
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     cur_m0 += BMQ;
@@ -683,44 +645,41 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   // issue (so no store is issued after a tile load whose wait comes first:
   // one counter covers loads and stores, and they may complete out of
   // order); receives dS(j-1).
-  auto body1 = [&](int j, int st, int stp, int pbp, const f32x16 (&dpv)[KB], f32x16 (&dn)[KB],
+  auto body1 = [&](int j, int st, int stp, int pbp, const f32x16& dpv, f32x16& dn,
                    u32x4 (&dprev)[2]) SK_INLINE {
     if (SK_BWD_FIVE_GEMM && j >= 2) store_ds(dprev);
     const uint8_t* pb = smem + p_lds + pbp * 4 * kPBlock;
-    f32x4 pr[KB][4], dv[4];
-    auto pr_slot = [&](int kb, int q) { return pf(pair_t(kb, 2 * q)) + 1 - SL; };
+    f32x4 pr[4], dv[4];
+    auto pr_slot = [&](int q) { return pf(2 * q) + 1 - SL; };
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (pr_slot(0, q) < 0) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+      if (pr_slot(q) < 0) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
     auto delta_r = [&](int r) { return dv[r / 4][r % 4]; };
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (pr_slot(kb, q) < 0) pr[kb][q] = *reinterpret_cast<const f32x4*>(pb + kb * kPBlock + 1024 * q);
+    for (int q = 0; q < 4; ++q)
+      if (pr_slot(q) < 0) pr[q] = *reinterpret_cast<const f32x4*>(pb + 1024 * q);
     u32x4 ad[KD];
     u32x4 xq[NX];
-    float de[KB][16];
-    u32x4 dsk[KB][2];
+    float de[16];
+    u32x4 dsk[2];
     auto read_xq = [&](int x) {
       const int s2 = x / DB, c = x % DB;
       const int o = stp * QT + 16 * s2 * RB;
       xq[x] = lds_tr_pair(smem + tr_lo[c] + o, smem + tr_hi[c] + o);
     };
-    auto xq_slot = [&](int x) { return NS + (x / DB) * DB * KB + x % DB - XL; };
+    auto xq_slot = [&](int x) { return NS + x - XL; };
 #pragma unroll
     for (int s = 0; s < KD; ++s)
-      if (s * KB - KL < 0) ad[s] = pre[s];
+      if (s - KL < 0) ad[s] = pre[s];
 #pragma unroll
     for (int x = 0; x < NX; ++x)
       if (xq_slot(x) < 0) read_xq(x);
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) dn[kb] = f32x16{};
+    dn = f32x16{};
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
 #pragma unroll
       for (int s = 0; s < KD; ++s)
-        if (s * KB - KL == i && i >= 0) ad[s] = ld128(row_lds[s] + st * QT);
+        if (s - KL == i && i >= 0) ad[s] = ld128(row_lds[s] + st * QT);
       if (i == kIssSlot && j + 4 < n_it) issue((st + 4) % STAGES);
       if (i == kPreSlot) {
 #pragma unroll
@@ -731,51 +690,45 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
         if (xq_slot(x) == i) read_xq(x);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (pr_slot(0, q) == i) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
+        if (pr_slot(q) == i) dv[q] = ldf4(stat_lds + stp * kStatStage + 32 * q);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (pr_slot(kb, q) == i) pr[kb][q] = *reinterpret_cast<const f32x4*>(pb + kb * kPBlock + 1024 * q);
+      for (int q = 0; q < 4; ++q)
+        if (pr_slot(q) == i) pr[q] = *reinterpret_cast<const f32x4*>(pb + 1024 * q);
       if (i < NS) {
-        const int s = i / KB, kb = i % KB;
-        dn[kb] = mfma32<T>(ad[s], kv[kb][s], dn[kb]);
+        dn = mfma32<T>(ad[i], kv[i], dn);
       } else {
         const int a = i - NS;
-        const int s2 = a / (DB * KB), kb = (a / DB) % KB, c = a % DB;
-        acc[kb][c] = mfma32<T>(xq[s2 * DB + c], dsk[kb][s2], acc[kb][c]);
+        acc[a % DB] = mfma32<T>(xq[a], dsk[a / DB], acc[a % DB]);
       }
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int g = 0; g < 8; ++g) {
+        const int f = pf(g) + 1;
+        if (f == i) {
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          const int f = pf(pair_t(kb, g)) + 1;
-          if (f == i) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const int x = 2 * g + e;
-              de[kb][x] = pr[kb][x >> 2][x & 3] * (dpv[kb][x] - delta_r(x));
-            }
+          for (int e = 0; e < 2; ++e) {
+            const int x = 2 * g + e;
+            de[x] = pr[x >> 2][x & 3] * (dpv[x] - delta_r(x));
           }
-          if (f + 1 == i) dsk[kb][g >> 2][g & 3] = pack2<T>(de[kb][2 * g], de[kb][2 * g + 1]);
         }
+        if (f + 1 == i) dsk[g >> 2][g & 3] = pack2<T>(de[2 * g], de[2 * g + 1]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (SK_BWD_FIVE_GEMM) {
-      dprev[0] = dsk[0][0];
-      dprev[1] = dsk[0][1];
+      dprev[0] = dsk[0];
+      dprev[1] = dsk[1];
     }
   };
   // Each role runs its own copy of the step loop (the same barriers in the
   // same order).  role_body(st, par) runs step j >= 1 with tile j in stage
   // st and par = j & 1.
-  f32x16 sv[2][KB];  // role 0: S of even / odd tiles; role 1: dP of even / odd tiles
+  f32x16 sv[2];  // role 0: S of even / odd tiles; role 1: dP of even / odd tiles
   auto run_v2 = [&](auto role_body) SK_INLINE {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       if (t < n_it) issue(t);
     begin_v2(0);
-    score_all(0, sv[0]);
+    sv[0] = score(0);
     // first row operands of the next body: role 0's S(1) reads Q(1), role
     // 1's dP(1) reads dO(1), both in stage 1
 #pragma unroll
@@ -811,32 +764,29 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
     // register set by a branch, so both sets stay in registers)
     const int jl = n_it - 1;
     const int stp = jl % STAGES;
-    auto tail = [&](f32x16 (&dpv)[KB], int pbi) SK_INLINE {
+    auto tail = [&](f32x16& dpv, int pbi) SK_INLINE {
       const uint8_t* pb = smem + p_lds + pbi * 4 * kPBlock;
       f32x4 dv[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) dv[k] = ldf4(stat_lds + stp * kStatStage + 32 * k);
+      float de[16];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        float de[16];
+      for (int k = 0; k < 4; ++k) {
+        const f32x4 pr = *reinterpret_cast<const f32x4*>(pb + 1024 * k);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const f32x4 pr = *reinterpret_cast<const f32x4*>(pb + kb * kPBlock + 1024 * k);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) de[4 * k + e] = pr[e] * (dpv[kb][4 * k + e] - dv[k][e]);
-        }
-        u32x4 dsk[2];
-        pack16(de, dsk);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-          for (int c = 0; c < DB; ++c) {
-            const int o = stp * QT + 16 * s2 * RB;
-            const u32x4 x = lds_tr_pair(smem + tr_lo[c] + o, smem + tr_hi[c] + o);
-            acc[kb][c] = mfma32<T>(x, dsk[s2], acc[kb][c]);
-          }
-        if (SK_BWD_FIVE_GEMM && kb == 0) store_ds(dsk);
+        for (int e = 0; e < 4; ++e) de[4 * k + e] = pr[e] * (dpv[4 * k + e] - dv[k][e]);
       }
+      u32x4 dsk[2];
+      pack16(de, dsk);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int c = 0; c < DB; ++c) {
+          const int o = stp * QT + 16 * s2 * RB;
+          const u32x4 x = lds_tr_pair(smem + tr_lo[c] + o, smem + tr_hi[c] + o);
+          acc[c] = mfma32<T>(x, dsk[s2], acc[c]);
+        }
+      if (SK_BWD_FIVE_GEMM) store_ds(dsk);
     };
     if (jl & 1)
       tail(sv[1], 1);
@@ -878,24 +828,21 @@ __global__ void __launch_bounds__(512 / KB, 1) bwd_dkv_kernel(BwdParams p) {
   }
 
   const float osc = role == 0 ? 1.f : p.scale;
+  if (key >= p.Sk) return;
+  const int64_t krow = ((int64_t)bk * p.Sk + key) * p.D;
+  uint16_t* outp = (uint16_t*)(role == 0 ? p.dv : p.dk) + krow;
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    if (key + 32 * kb >= p.Sk) return;
-    const int64_t krow = ((int64_t)bk * p.Sk + key + 32 * kb) * p.D;
-    uint16_t* outp = (uint16_t*)(role == 0 ? p.dv : p.dk) + krow;
+  for (int c = 0; c < DB; ++c)
 #pragma unroll
-    for (int c = 0; c < DB; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = d_out0 + 32 * c + 8 * i + 4 * hl;
-        if (d < p.D) {
-          const f32x16& a = acc[kb][c];
-          *reinterpret_cast<u32x2*>(outp + d) =
-              u32x2{pack2<T>(a[4 * i] * osc, a[4 * i + 1] * osc),
-                    pack2<T>(a[4 * i + 2] * osc, a[4 * i + 3] * osc)};
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int d = d_out0 + 32 * c + 8 * i + 4 * hl;
+      if (d < p.D) {
+        const f32x16& a = acc[c];
+        *reinterpret_cast<u32x2*>(outp + d) =
+            u32x2{pack2<T>(a[4 * i] * osc, a[4 * i + 1] * osc),
+                  pack2<T>(a[4 * i + 2] * osc, a[4 * i + 3] * osc)};
       }
-  }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1477,15 +1424,12 @@ static KernelPlan plan_dkv_t(BwdParams& p, bool causal) {
   // and SK_BWD_DKV_STAGES_D64=4 build the 4-deep one-tile-per-step schedule
   // instead.  D = 256 keeps the 4-deep one (the 6-deep ring does not fit).
   constexpr int STAGES = DP == 128 ? SK_BWD_DKV_STAGES : DP == 64 ? SK_BWD_DKV_STAGES_D64 : 4;
-  // Keys per wave: 64 (two 32-key blocks; four waves, one per SIMD) in a
-  // tile-study build of the D = 128 6-deep schedule, else 32 (eight waves).
-  constexpr int KB = STAGES == 6 && DP == 128 ? SK_BWD_DKV_KB : 1;
   p.n_nblocks = (p.Sk + 127) / 128;
   KernelPlan k;
-  k.fn = causal ? (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, KB, true>
-                : (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, KB, false>;
+  k.fn = causal ? (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, true>
+                : (const void*)bwd_dkv_kernel<T, DP, DO, STAGES, false>;
   k.grid = dim3((unsigned)((int64_t)p.n_nblocks * launch_pairs(p) * (DP / DO)));
-  k.block = dim3(512 / KB);
+  k.block = dim3(512);
   k.kernel = "bwd_dkv_kernel";
   k.elem = T::code;
   k.head_dim = DP;
@@ -1555,7 +1499,7 @@ KernelPlan plan_bwd_dkv(int dtype, BwdParams& p, bool causal) {
 size_t bwd_ds_pair_bytes(int dtype, int Hq, int Hkv, int Sq, int Sk, int D, bool causal) {
   if (!SK_BWD_FIVE_GEMM) return 0;
   if (dtype != BF16::code && dtype != F16::code) return 0;
-  if (D <= 64 || D > 128 || SK_BWD_DKV_STAGES != 6 || SK_BWD_DKV_KB != 1) return 0;
+  if (D <= 64 || D > 128 || SK_BWD_DKV_STAGES != 6) return 0;
   if (Hkv <= 0 || Sq <= 0 || Sk <= 0) return 0;
   const int nqt = (Sq + 31) / 32;
   const int c = ds_causal_c(Sq, Sk);

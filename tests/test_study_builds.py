@@ -38,7 +38,6 @@ STUDY_BUILDS = [
     "SK_DEC_BN_W4=128",
     "SK_BWD_DKV_STAGES=4",
     "SK_BWD_DKV_STAGES_D64=4",
-    "SK_BWD_DKV_KB=2",
     "SK_BWD_DKV_DO_D256=256",
     "SK_BWD_DQ_TILE=32,2,0",
     "SK_BWD_DQ_TILE=64,2,0",
